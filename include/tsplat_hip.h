@@ -1,0 +1,185 @@
+/*
+ * tsplat_hip.h -- C ABI of libtsplat_hip.so, the gfx950 (MI355X) kernels for
+ * the NF24 packed-weight Linear and the exact SDPA of TripoSplat's flow model.
+ *
+ * Drop-in boundary.  The first group of each section keeps the exact symbol
+ * names, argument lists and status codes of the reference's AVX-512
+ * libraries, so an unmodified ctypes binding loads this library instead.
+ * Differences, all forced by the device:
+ *   - every array argument is a DEVICE pointer (hipMalloc / torch.cuda memory
+ *     on the current HIP device).  Host pointers and allocations smaller than
+ *     the arguments imply are rejected with status -6 before any launch;
+ *   - `threads` is accepted and ignored (there is no OpenMP pool);
+ *   - the reference-named calls run on the null stream and return after the
+ *     device has finished (blocking, like the CPU call).  The tsplat_*_async
+ *     variants only enqueue on the given stream (hipStream_t passed as void*)
+ *     and return immediately.
+ * Status codes: 0 ok; -1 null pointer; -2 bad sizes / stages / head dim;
+ * -3 range, stride or key-bias length mismatch; -4 range not 16-aligned (or a
+ * pointer not 16-byte aligned where float4 access is required); -5 device
+ * workspace allocation failed; -6 not device memory / allocation too small /
+ * other device; -7 HIP launch or runtime error (tsplat_last_hip_error()).
+ *
+ * Weight format NF24 (residual mode 4): w[k][n] = fp32((int32)code01[k][n] *
+ * 256 + q2[k][n]) * scale[n], code01 int16 [K][N], q2 int8 [K][N], scale fp32
+ * [N] (= max|W_row| / 127 / 1024).  codes2_t, scales1, scales2 and codebook
+ * are part of the reference signature; they must be non-null and are unused.
+ */
+#ifndef TSPLAT_HIP_H
+#define TSPLAT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------- NF24 GEMM: out = bias + x * W ------------------------ */
+
+/* scripts/gemm_nf24_i16_avx512.c:199-220 (triposplat_gemm_rnf8_avx512).
+ * Full GEMM over all N outputs; N must be a multiple of 16 (else -4), as in
+ * the reference, which routes other N to the _tail symbol. */
+int triposplat_gemm_rnf8_avx512(const float* x, const uint8_t* codes0_t, const uint8_t* codes1_t,
+                                const uint8_t* codes2_t, const float* scales0,
+                                const float* scales1, const float* scales2, const float* codebook,
+                                const float* bias, float* out, int M, int K, int N, int stride_x,
+                                int stride_out, int threads, int stages);
+
+/* scripts/gemm_nf24_i16_avx512.c:151-197: outputs [output_start,
+ * output_start + output_count) of each row into out[M][stride_out];
+ * start and count must be multiples of 16. */
+int triposplat_gemm_rnf8_avx512_range(const float* x, const uint8_t* codes0_t,
+                                      const uint8_t* codes1_t, const uint8_t* codes2_t,
+                                      const float* scales0, const float* scales1,
+                                      const float* scales2, const float* codebook,
+                                      const float* bias, float* out, int M, int K, int N,
+                                      int output_start, int output_count, int stride_x,
+                                      int stride_out, int threads, int stages);
+
+/* scripts/gemm_nf24_i16_avx512_tail.c:8-49: any N (e.g. 5 for cam_out_layer). */
+int triposplat_gemm_rnf8_avx512_tail(const float* x, const uint8_t* codes0_t,
+                                     const uint8_t* codes1_t, const uint8_t* codes2_t,
+                                     const float* scales0, const float* scales1,
+                                     const float* scales2, const float* codebook,
+                                     const float* bias, float* out, int M, int K, int N,
+                                     int stride_x, int stride_out, int threads, int stages);
+
+/* scripts/gemm_nf24_i16_avx512.c:222-228: rows per output tile; residual
+ * mode id (4 = nf24_i16, checked by the Python patch). */
+int triposplat_gemm_rnf8_avx512_row_tile(void);
+int triposplat_gemm_rnf8_avx512_residual_mode(void);
+
+/* Asynchronous NF24 GEMM on `stream` (no counterpart in the reference; the
+ * range form above without the 16-alignment rule). */
+int tsplat_nf24_gemm_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,
+                           const float* scale, const float* bias, float* out, int M, int K, int N,
+                           int output_start, int output_count, int stride_x, int stride_out,
+                           void* stream);
+
+/* ---------------- exact SDPA (head dim 64, scale 1/8) ------------------ */
+
+/* scripts/native_sdpa_avx512_exact_q8t512.c:137-332.  q [B,H,Lq,64],
+ * k/v [B,H,Lk,64], key_bias [Lk] shared by all (b,h) when has_key_bias,
+ * out [B,H,Lq,64].  D must be 64; key_bias_len must equal Lk. */
+int triposplat_sdpa_f32_avx512_exact_q8t512(const float* q, const float* k, const float* v,
+                                            const float* key_bias_or_null, float* out, int B,
+                                            int H, int Lq, int Lk, int D, int has_key_bias,
+                                            int key_bias_len, int threads);
+/* q8t512.c:334-351 alias, and the legacy symbol name that
+ * scripts/native_sdpa_ctypes.py:10-11 binds by default (same ABI and math). */
+int triposplat_sdpa_f32(const float* q, const float* k, const float* v,
+                        const float* key_bias_or_null, float* out, int B, int H, int Lq, int Lk,
+                        int D, int has_key_bias, int key_bias_len, int threads);
+int triposplat_sdpa_f32_avx512_exact_q8(const float* q, const float* k, const float* v,
+                                        const float* key_bias_or_null, float* out, int B, int H,
+                                        int Lq, int Lk, int D, int has_key_bias,
+                                        int key_bias_len, int threads);
+
+/* scripts/native_sdpa_avx512_exact_q8t512_packed.c:3-158: k/v pre-packed
+ * [B,H,64,Lkp] (Lkp >= Lk, multiple of 16, tail keys zero), output BLHD
+ * [B,Lq,H,64]. */
+int triposplat_sdpa_f32_avx512_exact_q8t512_packed_blhd(
+    const float* q, const float* packed_k, const float* packed_v, const float* key_bias_or_null,
+    float* out_blhd, int B, int H, int Lq, int Lk, int D, int Lkp, int has_key_bias,
+    int key_bias_len, int threads);
+
+/* q8t512.c:51-100 and packed.c:160-162 metadata/profile probes.  Key tile
+ * and query block report this library's tiles (64 keys, 128 queries).
+ * Profile: calls and wall time of the blocking calls (allocate/pack/free
+ * report 0: there is no per-call workspace or pack step). */
+int triposplat_sdpa_key_tile(void);
+int triposplat_sdpa_query_block(void);
+int triposplat_sdpa_packed_output_is_blhd(void);
+void triposplat_sdpa_q8t512_profile_reset(void);
+int triposplat_sdpa_q8t512_profile_get(uint64_t* calls, uint64_t* allocate_ns, uint64_t* pack_ns,
+                                       uint64_t* compute_ns, uint64_t* free_ns);
+int triposplat_sdpa_q8t512_workspace_stats(uint64_t* allocations, uint64_t* capacity_bytes);
+void triposplat_sdpa_q8t512_workspace_release(void);
+
+/* Asynchronous SDPA on `stream` (extension of the two entries above):
+ * kv_packed selects k/v [B,H,64,Lkp] instead of [B,H,Lk,64]; out_blhd
+ * selects [B,Lq,H,64] output; bias_head_stride = 0 shares one [Lk] bias
+ * row, = Lk reads a [H,Lk] per-head bias. */
+int tsplat_sdpa_async(const float* q, const float* k, const float* v,
+                      const float* key_bias_or_null, float* out, int B, int H, int Lq, int Lk,
+                      int D, int has_key_bias, int key_bias_len, int64_t bias_head_stride,
+                      int kv_packed, int Lkp, int out_blhd, void* stream);
+
+/* ---------------- QKV RoPE -> RMSNorm -> pack -------------------------- */
+
+/* scripts/native_qkv_postprocess_v2_avx512.c:45-105.  qkv [B*L, 3*H*64]
+ * -> q [B,H,L,64], packed k/v [B,H,64,L_padded]; frequencies
+ * [frequency_batches, L, H, 64] as (cos, sin) pairs; gammas [H,64]. */
+int triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2(const float* qkv, const float* frequencies,
+                                                   const float* q_gamma, const float* k_gamma,
+                                                   float* q_bhld, float* packed_k,
+                                                   float* packed_v, int B, int L, int H, int D,
+                                                   int L_padded, int frequency_batches,
+                                                   int threads);
+
+/* scripts/gemm_nf24_qkv_direct_avx512.c:87-199: NF24 QKV GEMM (N = 3*H*64)
+ * followed by the postprocess above, without returning the [B*L, N]
+ * projection to the caller. */
+int triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512(
+    const float* x, const uint8_t* codes0_t, const uint8_t* codes1_t, const uint8_t* codes2_t,
+    const float* scales0, const float* scales1, const float* scales2, const float* codebook,
+    const float* bias, const float* frequencies, const float* q_gamma, const float* k_gamma,
+    float* q_bhld, float* packed_k, float* packed_v, int B, int L, int K, int N, int H, int D,
+    int L_padded, int frequency_batches, int threads, int stages);
+/* gemm_nf24_qkv_direct_avx512.c:201-207 probes. */
+int triposplat_gemm_nf24_qkv_direct_row_tile(void);
+int triposplat_gemm_nf24_qkv_direct_residual_mode(void);
+
+/* Asynchronous forms of the two QKV entries. */
+int tsplat_qkv_postprocess_async(const float* qkv, const float* frequencies, const float* q_gamma,
+                                 const float* k_gamma, float* q_bhld, float* packed_k,
+                                 float* packed_v, int B, int L, int H, int D, int L_padded,
+                                 int frequency_batches, void* stream);
+int tsplat_gemm_nf24_qkv_direct_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,
+                                      const float* scale, const float* bias,
+                                      const float* frequencies, const float* q_gamma,
+                                      const float* k_gamma, float* q_bhld, float* packed_k,
+                                      float* packed_v, int B, int L, int K, int N, int H, int D,
+                                      int L_padded, int frequency_batches, void* stream);
+
+/* ---------------- NF24 packer ------------------------------------------ */
+
+/* scripts/native_linear_rnf8_avx512_patch.py:14-87 (quantize_nf24_i16_per_output_channel),
+ * on the device: weight fp32 [out_features, in_features] -> code01_t int16
+ * [in, out], q2_t int8 [in, out], scale fp32 [out] (= max|row|/127/1024).
+ * alphabet: the sorted NF8-derived integer levels (fp32, 2..256 entries);
+ * base_workspace: [out_features] fp32 scratch.  Asynchronous on `stream`. */
+int tsplat_nf24_pack_async(const float* weight, int out_features, int in_features,
+                           const float* alphabet, int alphabet_len, float* base_workspace,
+                           int16_t* code01_t, int8_t* q2_t, float* scale, void* stream);
+
+/* ---------------- library ------------------------------------------------ */
+int tsplat_abi_version(void);         /* bumped on any ABI change */
+int tsplat_last_hip_error(void);      /* last hipError_t seen by this library */
+const char* tsplat_build_arch(void);  /* "gfx950" */
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TSPLAT_HIP_H */

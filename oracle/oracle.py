@@ -1,0 +1,364 @@
+"""CPU oracle for the NF24 GEMM and exact SDPA paths.
+
+TEST INFRASTRUCTURE ONLY: tests/, ``__graft_entry__.smoke()`` and bench.py's
+``cpu_baseline`` leg are the only callers.  The product package never imports
+this module.
+
+Two parts:
+
+* ``tsplat_oracle.c`` (built to ``libtsplat_oracle.so`` by the Makefile here) --
+  scalar C restatements of the reference kernels, bit-identical to them;
+  wrapped below with NumPy in/out.
+* a NumPy restatement of the reference's NF24 packer and its NF8-derived
+  alphabet (scripts/native_linear_rnf8_avx512_patch.py:14-87,
+  scripts/native_linear_nf8_avx512_patch.py:12-20).
+
+Pinning: see the header of tsplat_oracle.c and tests/test_oracle.py.  The
+packer is pinned by the alphabet closed form (erfinv quantiles, each
+127*level at least 1e-4 away from a rounding tie) and by brute-force
+nearest-level / round-half-up checks on small matrices.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_LIB = HERE / "libtsplat_oracle.so"
+REF_DIR = HERE / "_ref"
+
+_c_float_p = ctypes.POINTER(ctypes.c_float)
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+_LIB = None
+
+
+def lib():
+    """Load (building if needed) the oracle shared library."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not ORACLE_LIB.is_file():
+        import subprocess
+
+        subprocess.run(["make", "-s", "-C", str(HERE), "oracle"], check=True)
+    L = ctypes.CDLL(str(ORACLE_LIB))
+    L.oracle_nf24_gemm_range.argtypes = [_vp] * 6 + [_i] * 8
+    L.oracle_nf24_gemm_range.restype = _i
+    L.oracle_sdpa_q8t512.argtypes = [_vp] * 5 + [_i] * 7 + [ctypes.c_int64]
+    L.oracle_sdpa_q8t512.restype = _i
+    L.oracle_sdpa_q8t512_packed_blhd.argtypes = [_vp] * 5 + [_i] * 8
+    L.oracle_sdpa_q8t512_packed_blhd.restype = _i
+    L.oracle_qkv_rope_rmsnorm_pack.argtypes = [_vp] * 7 + [_i] * 6
+    L.oracle_qkv_rope_rmsnorm_pack.restype = _i
+    L.oracle_gemm_nf24_qkv_direct.argtypes = [_vp] * 11 + [_i] * 8
+    L.oracle_gemm_nf24_qkv_direct.restype = _i
+    L.oracle_exp512.argtypes = [ctypes.c_float]
+    L.oracle_exp512.restype = ctypes.c_float
+    L.oracle_nf24_decode.argtypes = [_i, _i, ctypes.c_float]
+    L.oracle_nf24_decode.restype = ctypes.c_float
+    L.oracle_reduce_add16.argtypes = [_vp]
+    L.oracle_reduce_add16.restype = ctypes.c_float
+    L.oracle_rope_rmsnorm64.argtypes = [_vp] * 4
+    L.oracle_rope_rmsnorm64.restype = None
+    L.oracle_threads.argtypes = []
+    L.oracle_threads.restype = _i
+    _LIB = L
+    return L
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# --------------------------------------------------------------------------
+# NF24 GEMM
+def nf24_gemm(x, code01_t, q2_t, scale, bias, output_start=0, output_count=None,
+              require_aligned=False):
+    """out[M, count] = bias + x @ decode(code01_t, q2_t, scale)[:, start:start+count].
+
+    Restates scripts/gemm_nf24_i16_avx512.c:151-197 (status codes included).
+    """
+    x = _f32(x)
+    code01_t = np.ascontiguousarray(code01_t, dtype=np.int16)
+    q2_t = np.ascontiguousarray(q2_t, dtype=np.int8)
+    scale, bias = _f32(scale), _f32(bias)
+    M, K = x.shape
+    N = code01_t.shape[1]
+    count = N - output_start if output_count is None else output_count
+    out = np.empty((M, max(count, 1)), dtype=np.float32)
+    st = lib().oracle_nf24_gemm_range(_ptr(x), _ptr(code01_t), _ptr(q2_t), _ptr(scale),
+                                      _ptr(bias), _ptr(out), M, K, N, output_start, count, K,
+                                      out.shape[1], int(require_aligned))
+    if st != 0:
+        raise RuntimeError(f"oracle NF24 GEMM status {st}")
+    return out
+
+
+def decode_nf24(code01_t, q2_t, scale):
+    """Exact fp32 decode in the [in, out] layout (prepacked.py:17-31)."""
+    q = code01_t.astype(np.int32) * 256 + q2_t.astype(np.int32)
+    return q.astype(np.float32) * np.asarray(scale, dtype=np.float32)[None, :]
+
+
+# --------------------------------------------------------------------------
+# SDPA
+def sdpa_q8t512(q, k, v, key_bias=None, bias_head_stride=0):
+    """Exact SDPA of scripts/native_sdpa_avx512_exact_q8t512.c:137-332.
+
+    q [B,H,Lq,64], k/v [B,H,Lk,64]; key_bias [Lk] shared, or [H,Lk] with
+    bias_head_stride=Lk (extension: one bias row per head).
+    """
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, H, Lq, D = q.shape
+    Lk = k.shape[2]
+    out = np.empty((B, H, Lq, D), dtype=np.float32)
+    kb = None if key_bias is None else _f32(key_bias)
+    st = lib().oracle_sdpa_q8t512(_ptr(q), _ptr(k), _ptr(v), _ptr(kb), _ptr(out), B, H, Lq, Lk,
+                                  D, int(kb is not None), 0 if kb is None else Lk,
+                                  int(bias_head_stride))
+    if st != 0:
+        raise RuntimeError(f"oracle SDPA status {st}")
+    return out
+
+
+def sdpa_q8t512_packed_blhd(q, packed_k, packed_v, Lk, key_bias=None):
+    """scripts/native_sdpa_avx512_exact_q8t512_packed.c:3-158 -> out [B,Lq,H,64]."""
+    q, pk, pv = _f32(q), _f32(packed_k), _f32(packed_v)
+    B, H, Lq, D = q.shape
+    Lkp = pk.shape[3]
+    out = np.empty((B, Lq, H, D), dtype=np.float32)
+    kb = None if key_bias is None else _f32(key_bias)
+    st = lib().oracle_sdpa_q8t512_packed_blhd(_ptr(q), _ptr(pk), _ptr(pv), _ptr(kb), _ptr(out), B,
+                                              H, Lq, Lk, D, Lkp, int(kb is not None),
+                                              0 if kb is None else Lk)
+    if st != 0:
+        raise RuntimeError(f"oracle packed SDPA status {st}")
+    return out
+
+
+def qkv_rope_rmsnorm_pack(qkv, freqs, q_gamma, k_gamma, B, L, H, L_padded=None):
+    """scripts/native_qkv_postprocess_v2_avx512.c:45-105."""
+    qkv, freqs = _f32(qkv), _f32(freqs)
+    q_gamma, k_gamma = _f32(q_gamma), _f32(k_gamma)
+    D = 64
+    Lp = ((L + 15) // 16) * 16 if L_padded is None else L_padded
+    fb = freqs.shape[0]
+    q = np.empty((B, H, L, D), np.float32)
+    pk = np.empty((B, H, D, Lp), np.float32)
+    pv = np.empty((B, H, D, Lp), np.float32)
+    st = lib().oracle_qkv_rope_rmsnorm_pack(_ptr(qkv), _ptr(freqs), _ptr(q_gamma), _ptr(k_gamma),
+                                            _ptr(q), _ptr(pk), _ptr(pv), B, L, H, D, Lp, fb)
+    if st != 0:
+        raise RuntimeError(f"oracle postprocess status {st}")
+    return q, pk, pv
+
+
+def gemm_nf24_qkv_direct(x, code01_t, q2_t, scale, bias, freqs, q_gamma, k_gamma, B, L, H,
+                         L_padded=None):
+    """scripts/gemm_nf24_qkv_direct_avx512.c:87-199."""
+    x = _f32(x)
+    code01_t = np.ascontiguousarray(code01_t, dtype=np.int16)
+    q2_t = np.ascontiguousarray(q2_t, dtype=np.int8)
+    scale, bias, freqs = _f32(scale), _f32(bias), _f32(freqs)
+    q_gamma, k_gamma = _f32(q_gamma), _f32(k_gamma)
+    K = x.shape[1]
+    N = code01_t.shape[1]
+    D = 64
+    Lp = ((L + 15) // 16) * 16 if L_padded is None else L_padded
+    q = np.empty((B, H, L, D), np.float32)
+    pk = np.empty((B, H, D, Lp), np.float32)
+    pv = np.empty((B, H, D, Lp), np.float32)
+    st = lib().oracle_gemm_nf24_qkv_direct(_ptr(x), _ptr(code01_t), _ptr(q2_t), _ptr(scale),
+                                           _ptr(bias), _ptr(freqs), _ptr(q_gamma), _ptr(k_gamma),
+                                           _ptr(q), _ptr(pk), _ptr(pv), B, L, K, N, H, D, Lp,
+                                           freqs.shape[0])
+    if st != 0:
+        raise RuntimeError(f"oracle QKV direct status {st}")
+    return q, pk, pv
+
+
+def exp512(x):
+    f = lib().oracle_exp512
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32).reshape(-1)], np.float32)
+
+
+def threads():
+    return int(lib().oracle_threads())
+
+
+# --------------------------------------------------------------------------
+# NF24 packer (NumPy restatement).
+def nf8_levels_f64():
+    """The 256 NF8 levels in float64: 255 normal quantiles (p = (i+0.5)/255)
+    scaled to max |level| = 1, plus a duplicate zero, sorted
+    (scripts/native_linear_nf8_avx512_patch.py:12-20)."""
+    from scipy.special import erfinv
+
+    p = (np.arange(255, dtype=np.float64) + 0.5) / 255.0
+    levels = math.sqrt(2.0) * erfinv(2.0 * p - 1.0)
+    levels = levels / np.abs(levels).max()
+    return np.sort(np.concatenate([levels, np.zeros(1)]))
+
+
+def nf24_alphabet():
+    """Integer alphabet unique(round(127 * codebook_f32)) clamped to +-127,
+    as fp32 (native_linear_rnf8_avx512_patch.py:24)."""
+    cb = nf8_levels_f64().astype(np.float32)
+    scaled = cb * np.float32(127.0)
+    return np.unique(np.clip(np.rint(scaled), -127, 127)).astype(np.float32)
+
+
+def alphabet_tie_margin():
+    """Smallest distance of any 127*level from a rounding tie (x.5)."""
+    scaled = nf8_levels_f64() * 127.0
+    frac = np.abs(scaled - np.floor(scaled) - 0.5)
+    return float(frac.min())
+
+
+def quantize_nf24_i16(weight):
+    """Pack fp32 W [out, in] -> (code01_t int16 [in,out], q2_t int8 [in,out],
+    scale fp32 [out]) with scale = max|w_row| / 127 / 1024.
+
+    Restates native_linear_rnf8_avx512_patch.py:14-87 in fp32 NumPy.
+    """
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    tiny = np.finfo(np.float32).tiny
+    max_abs = np.maximum(np.abs(w).max(axis=1), np.float32(tiny)).astype(np.float32)
+    base = (max_abs / np.float32(127.0)).astype(np.float32)
+    alphabet = nf24_alphabet()
+    mid = ((alphabet[:-1] + alphabet[1:]) * np.float32(0.5)).astype(np.float32)
+    norm = (w / base[:, None]).astype(np.float32)
+    q0 = alphabet[np.searchsorted(mid, norm, side="left")]
+    r1 = (w - (q0 * base[:, None]).astype(np.float32)).astype(np.float32)
+    s1 = (base / np.float32(4.0)).astype(np.float32)
+    q1 = np.clip(np.floor((r1 / s1[:, None]).astype(np.float32) + np.float32(0.5)), -128, 127)
+    q1 = q1.astype(np.float32)
+    r2 = (r1 - (q1 * s1[:, None]).astype(np.float32)).astype(np.float32)
+    final = (base / np.float32(1024.0)).astype(np.float32)
+    q2 = np.clip(np.floor((r2 / final[:, None]).astype(np.float32) + np.float32(0.5)), -128, 127)
+    code01 = (q0.astype(np.int16) * 4 + q1.astype(np.int16)).astype(np.int16)
+    return (np.ascontiguousarray(code01.T), np.ascontiguousarray(q2.astype(np.int8).T),
+            final.astype(np.float32))
+
+
+# --------------------------------------------------------------------------
+# Reference build (oracle/_ref) loaders, used to pin the oracle.
+def ref_available():
+    return (REF_DIR / "libref_gemm_nf24_i16.so").is_file()
+
+
+def ref_lib(name):
+    return ctypes.CDLL(str(REF_DIR / name))
+
+
+def ref_nf24_gemm(x, code01_t, q2_t, scale, bias, threads=0, output_start=0, output_count=None,
+                  tail=False):
+    L = ref_lib("libref_gemm_nf24_i16.so")
+    x = _f32(x)
+    code01_t = np.ascontiguousarray(code01_t, dtype=np.int16)
+    q2_t = np.ascontiguousarray(q2_t, dtype=np.int8)
+    scale, bias = _f32(scale), _f32(bias)
+    M, K = x.shape
+    N = code01_t.shape[1]
+    codebook = np.zeros(256, np.float32)
+    if tail:
+        fn = L.triposplat_gemm_rnf8_avx512_tail
+        fn.argtypes = [_vp] * 10 + [_i] * 7
+        out = np.empty((M, N), np.float32)
+        st = fn(_ptr(x), _ptr(code01_t), _ptr(q2_t), _ptr(q2_t), _ptr(scale), _ptr(scale),
+                _ptr(scale), _ptr(codebook), _ptr(bias), _ptr(out), M, K, N, K, N, threads, 3)
+    else:
+        count = N - output_start if output_count is None else output_count
+        fn = L.triposplat_gemm_rnf8_avx512_range
+        fn.argtypes = [_vp] * 10 + [_i] * 9
+        out = np.empty((M, count), np.float32)
+        st = fn(_ptr(x), _ptr(code01_t), _ptr(q2_t), _ptr(q2_t), _ptr(scale), _ptr(scale),
+                _ptr(scale), _ptr(codebook), _ptr(bias), _ptr(out), M, K, N, output_start, count,
+                K, count, threads, 3)
+    if st != 0:
+        raise RuntimeError(f"reference GEMM status {st}")
+    return out
+
+
+def ref_sdpa_q8t512(q, k, v, key_bias=None, threads=0):
+    L = ref_lib("libref_sdpa_q8t512.so")
+    fn = L.triposplat_sdpa_f32_avx512_exact_q8t512
+    fn.argtypes = [_vp] * 5 + [_i] * 8
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, H, Lq, D = q.shape
+    Lk = k.shape[2]
+    out = np.empty_like(q)
+    kb = None if key_bias is None else _f32(key_bias)
+    st = fn(_ptr(q), _ptr(k), _ptr(v), _ptr(kb), _ptr(out), B, H, Lq, Lk, D, int(kb is not None),
+            0 if kb is None else kb.size, threads)
+    if st != 0:
+        raise RuntimeError(f"reference SDPA status {st}")
+    return out
+
+
+def ref_sdpa_packed_blhd(q, packed_k, packed_v, Lk, key_bias=None, threads=0):
+    L = ref_lib("libref_sdpa_q8t512_packed.so")
+    fn = L.triposplat_sdpa_f32_avx512_exact_q8t512_packed_blhd
+    fn.argtypes = [_vp] * 5 + [_i] * 9
+    q, pk, pv = _f32(q), _f32(packed_k), _f32(packed_v)
+    B, H, Lq, D = q.shape
+    out = np.empty((B, Lq, H, D), np.float32)
+    kb = None if key_bias is None else _f32(key_bias)
+    st = fn(_ptr(q), _ptr(pk), _ptr(pv), _ptr(kb), _ptr(out), B, H, Lq, Lk, D, pk.shape[3],
+            int(kb is not None), 0 if kb is None else kb.size, threads)
+    if st != 0:
+        raise RuntimeError(f"reference packed SDPA status {st}")
+    return out
+
+
+def ref_qkv_postprocess_v2(qkv, freqs, q_gamma, k_gamma, B, L, H, threads=0):
+    Lib = ref_lib("libref_qkv_postprocess_v2.so")
+    fn = Lib.triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2
+    fn.argtypes = [_vp] * 7 + [_i] * 7
+    qkv, freqs = _f32(qkv), _f32(freqs)
+    q_gamma, k_gamma = _f32(q_gamma), _f32(k_gamma)
+    Lp = ((L + 15) // 16) * 16
+    q = np.empty((B, H, L, 64), np.float32)
+    pk = np.empty((B, H, 64, Lp), np.float32)
+    pv = np.empty((B, H, 64, Lp), np.float32)
+    st = fn(_ptr(qkv), _ptr(freqs), _ptr(q_gamma), _ptr(k_gamma), _ptr(q), _ptr(pk), _ptr(pv), B,
+            L, H, 64, Lp, freqs.shape[0], threads)
+    if st != 0:
+        raise RuntimeError(f"reference postprocess status {st}")
+    return q, pk, pv
+
+
+def ref_gemm_nf24_qkv_direct(x, code01_t, q2_t, scale, bias, freqs, q_gamma, k_gamma, B, L, H,
+                             threads=0):
+    Lib = ref_lib("libref_gemm_nf24_qkv_direct.so")
+    fn = Lib.triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512
+    fn.argtypes = [_vp] * 15 + [_i] * 10
+    x = _f32(x)
+    code01_t = np.ascontiguousarray(code01_t, dtype=np.int16)
+    q2_t = np.ascontiguousarray(q2_t, dtype=np.int8)
+    scale, bias, freqs = _f32(scale), _f32(bias), _f32(freqs)
+    q_gamma, k_gamma = _f32(q_gamma), _f32(k_gamma)
+    K = x.shape[1]
+    N = code01_t.shape[1]
+    Lp = ((L + 15) // 16) * 16
+    cb = np.zeros(256, np.float32)
+    q = np.empty((B, H, L, 64), np.float32)
+    pk = np.empty((B, H, 64, Lp), np.float32)
+    pv = np.empty((B, H, 64, Lp), np.float32)
+    st = fn(_ptr(x), _ptr(code01_t), _ptr(q2_t), _ptr(q2_t), _ptr(scale), _ptr(scale),
+            _ptr(scale), _ptr(cb), _ptr(bias), _ptr(freqs), _ptr(q_gamma), _ptr(k_gamma), _ptr(q),
+            _ptr(pk), _ptr(pv), B, L, K, N, H, 64, Lp, freqs.shape[0], threads, 3)
+    if st != 0:
+        raise RuntimeError(f"reference QKV direct status {st}")
+    return q, pk, pv

@@ -1,0 +1,155 @@
+"""GPU parity of the NF24 GEMM (libtsplat_hip.so) against the CPU oracle.
+
+The oracle (oracle/tsplat_oracle.c) is the reference's scalar fmaf chain,
+bit-exact with scripts/gemm_nf24_i16_avx512.c; the device sums the same
+decoded products with fp32 MFMA, so agreement is bounded by the
+order-of-summation bound in _parity.gemm_order_bound (stated there).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from _parity import gemm_f64, gemm_order_bound, seeded_linear, stats
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(torch, a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def _run_async(torch, hiplib, device, x, c01, q2, s, b, start=0, count=None, stride_x=None,
+               stride_out=None):
+    M, K = x.shape
+    N = c01.shape[1]
+    count = N - start if count is None else count
+    sx = K if stride_x is None else stride_x
+    so = count if stride_out is None else stride_out
+    xs = np.zeros((M, sx), np.float32)
+    xs[:, :K] = x
+    # keep every device buffer referenced until the asynchronous kernel is done
+    d = [_dev(torch, a, device) for a in (xs, c01, q2, s, b)]
+    out = torch.full((M, so), float("nan"), dtype=torch.float32, device=device)
+    st = hiplib.tsplat_nf24_gemm_async(
+        d[0].data_ptr(), d[1].data_ptr(), d[2].data_ptr(), d[3].data_ptr(), d[4].data_ptr(),
+        out.data_ptr(), M, K, N, start, count, sx, so, torch.cuda.current_stream(device).cuda_stream)
+    assert st == 0, st
+    torch.cuda.synchronize(device)
+    return out.cpu().numpy()
+
+
+def _check(oracle, x, c01, q2, s, b, got, start=0):
+    count = got.shape[1]
+    ref = oracle.nf24_gemm(x, c01, q2, s, b, output_start=start, output_count=count)
+    w_t = oracle.decode_nf24(c01, q2, s)[:, start:start + count]
+    bound = gemm_order_bound(x, w_t, b[start:start + count])
+    diff = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    assert np.all(np.isfinite(got))
+    assert np.all(diff <= bound), (float(diff.max()), float((diff - bound).max()))
+    exact = gemm_f64(x, w_t, b[start:start + count])
+    e_dev, e_ref = stats(got, exact), stats(ref, exact)
+    # statistically the device sum is no worse than the sequential chain
+    assert e_dev["rmse"] <= 2.0 * e_ref["rmse"] + 1e-9, (e_dev, e_ref)
+    return e_dev, e_ref
+
+
+# The reference smoke shapes (scripts/smoke_native_rnf8_avx512.py:72-79),
+# including the N=5 tail, plus skinny and ragged shapes.
+SHAPES = [(25, 96, 64), (40, 96, 64), (10, 96, 64), (3, 96, 5), (1, 1024, 3072), (2, 1024, 256),
+          (8, 4096, 64), (16, 64, 1024), (33, 130, 48), (129, 257, 200), (200, 64, 129),
+          (7, 3, 17), (300, 1024, 96)]
+
+
+@pytest.mark.parametrize("M,K,N", SHAPES)
+def test_gemm_matches_oracle(oracle, cuda, hiplib, M, K, N):
+    import torch
+
+    print(f"gemm M={M} K={K} N={N}", flush=True)
+    x, w, b = seeded_linear(19 + N, M, K, N)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    got = _run_async(torch, hiplib, cuda, x, c01, q2, s, b)
+    _check(oracle, x, c01, q2, s, b, got)
+
+
+def test_gemm_reference_smoke_tolerance(oracle, cuda, hiplib):
+    """scripts/smoke_native_rnf8_avx512.py:58: assert_close(rtol=2e-5, atol=2e-5)
+    against F.linear on the exactly reconstructed weight."""
+    import torch
+
+    for (M, K, N) in [(25, 96, 64), (40, 96, 64), (10, 96, 64), (3, 96, 5)]:
+        x, w, b = seeded_linear(19 + 3 + N, M, K, N)
+        c01, q2, s = oracle.quantize_nf24_i16(w)
+        got = _run_async(torch, hiplib, cuda, x, c01, q2, s, b)
+        w_hat = oracle.decode_nf24(c01, q2, s)
+        ref = torch.nn.functional.linear(torch.from_numpy(x), torch.from_numpy(w_hat.T.copy()),
+                                         torch.from_numpy(b))
+        torch.testing.assert_close(torch.from_numpy(got), ref, rtol=2e-5, atol=2e-5)
+
+
+@pytest.mark.parametrize("start,count", [(0, 16), (16, 32), (48, 80), (5, 7), (100, 28)])
+def test_gemm_range_and_strides(oracle, cuda, hiplib, start, count):
+    import torch
+
+    M, K, N = 37, 96, 128
+    x, w, b = seeded_linear(7, M, K, N)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    got = _run_async(torch, hiplib, cuda, x, c01, q2, s, b, start, count, stride_x=K + 8,
+                     stride_out=count + 3)[:, :count]
+    _check(oracle, x, c01, q2, s, b, got, start)
+    # range == the corresponding columns of the full product (same kernel, same order)
+    full = _run_async(torch, hiplib, cuda, x, c01, q2, s, b)
+    assert np.array_equal(got, full[:, start:start + count])
+
+
+def test_gemm_config1_sampled_rows(oracle, cuda, hiplib):
+    """Config 1 (4096x1024 @ 1024x3072, QKV): full GPU GEMM, oracle on 48
+    sampled rows (rows are independent, so the oracle's rows are exact)."""
+    import torch
+
+    M, K, N = 4096, 1024, 3072
+    r = np.random.default_rng(0)
+    x = r.standard_normal((M, K), dtype=np.float32)
+    w = (np.random.default_rng(1).standard_normal((N, K), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    b = (np.random.default_rng(2).standard_normal(N, dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    got = _run_async(torch, hiplib, cuda, x, c01, q2, s, b)
+    rows = np.sort(r.choice(M, 48, replace=False))
+    rows[0], rows[-1] = 0, M - 1
+    e_dev, e_ref = _check(oracle, x[rows], c01, q2, s, b, got[rows])
+    print("config1 sampled rows", e_dev, e_ref)
+
+
+def test_reference_named_entry_points(oracle, cuda, hiplib):
+    """The blocking reference-named symbols take device pointers and keep the
+    reference's status codes (scripts/gemm_nf24_i16_avx512.c:171-175)."""
+    import torch
+
+    M, K, N = 40, 96, 64
+    x, w, b = seeded_linear(3, M, K, N)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    d = {k: _dev(torch, v, cuda) for k, v in dict(x=x, c01=c01, q2=q2, s=s, b=b).items()}
+    cb = torch.zeros(256, dtype=torch.float32, device=cuda)
+    out = torch.empty((M, N), dtype=torch.float32, device=cuda)
+    ptrs = [d["x"].data_ptr(), d["c01"].data_ptr(), d["q2"].data_ptr(), d["q2"].data_ptr(),
+            d["s"].data_ptr(), d["s"].data_ptr(), d["s"].data_ptr(), cb.data_ptr(), d["b"].data_ptr(),
+            out.data_ptr()]
+    assert hiplib.triposplat_gemm_rnf8_avx512(*ptrs, M, K, N, K, N, 4, 3) == 0
+    _check(oracle, x, c01, q2, s, b, out.cpu().numpy())
+    out2 = torch.empty((M, N), dtype=torch.float32, device=cuda)
+    ptrs2 = ptrs[:-1] + [out2.data_ptr()]
+    assert hiplib.triposplat_gemm_rnf8_avx512_tail(*ptrs2, M, K, N, K, N, 4, 3) == 0
+    assert torch.equal(out, out2)
+    # status codes
+    assert hiplib.triposplat_gemm_rnf8_avx512(*ptrs, M, K, N, K, N, 4, 2) == -2        # stages
+    assert hiplib.triposplat_gemm_rnf8_avx512_range(*ptrs, M, K, N, 8, 16, K, 16, 4, 3) == -4
+    assert hiplib.triposplat_gemm_rnf8_avx512_range(*ptrs, M, K, N, 48, 32, K, 32, 4, 3) == -3
+    nullp = list(ptrs)
+    nullp[7] = None
+    assert hiplib.triposplat_gemm_rnf8_avx512(*nullp, M, K, N, K, N, 4, 3) == -1
+    host = np.zeros((M, N), np.float32)
+    hostp = ptrs[:-1] + [host.ctypes.data_as(ctypes.c_void_p).value]
+    assert hiplib.triposplat_gemm_rnf8_avx512(*hostp, M, K, N, K, N, 4, 3) == -6
+    assert hiplib.triposplat_gemm_rnf8_avx512_residual_mode() == 4

@@ -1,0 +1,103 @@
+"""GPU parity of the QKV postprocess (RoPE -> RMSNorm -> pack), the fused NF24
+QKV projection and the device NF24 packer, against the oracle.
+
+Postprocess: the device applies the same fmaf RoPE form as
+scripts/native_qkv_postprocess_v2_avx512.c and differs only in the order of
+the 64-term sum of squares, a relative change of at most 64 u in ||y||^2,
+i.e. |dy| <= 8 * 32 u * max|gamma| * (1 + 1e-6); stated tolerance 1e-5.
+Fused projection: the GEMM part is bounded as in test_gpu_gemm; RMSNorm maps
+an input perturbation dx to |dy| <= 8 * ||dx|| / ||x|| * max|gamma|.
+Packer: integer codes and scales must be bit-identical.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _parity import gemm_order_bound
+
+pytestmark = pytest.mark.gpu
+
+
+def _freqs(B, L, H, seed):
+    ang = np.random.default_rng(seed).standard_normal((B, L, H, 32)).astype(np.float32)
+    return np.stack([np.cos(ang), np.sin(ang)], -1).reshape(B, L, H, 64).astype(np.float32)
+
+
+def _gammas(H, seed):
+    r = np.random.default_rng(seed)
+    return ((r.standard_normal((H, 64)) * 0.05 + 1.0).astype(np.float32),
+            (r.standard_normal((H, 64)) * 0.05 + 1.0).astype(np.float32))
+
+
+@pytest.mark.parametrize("B,L,H,fb", [(1, 37, 2, 1), (2, 20, 3, 2), (1, 130, 16, 1), (2, 64, 4, 1)])
+def test_qkv_postprocess(oracle, cuda, B, L, H, fb):
+    import torch
+    from tsplat.qkv import qkv_rope_rmsnorm_pack
+
+    C = H * 64
+    qkv = np.random.default_rng(L).standard_normal((B * L, 3 * C), dtype=np.float32)
+    fr = _freqs(fb, L, H, 3)
+    qg, kg = _gammas(H, 4)
+    t = lambda a: torch.from_numpy(a).to(cuda)
+    got = qkv_rope_rmsnorm_pack(t(qkv), t(fr), t(qg), t(kg), B, L, H)
+    ref = oracle.qkv_rope_rmsnorm_pack(qkv, fr, qg, kg, B, L, H)
+    for g, r_ in zip(got, ref):
+        g = g.cpu().numpy()
+        assert g.shape == r_.shape
+        assert float(np.abs(g - r_).max()) <= 1e-5
+    # v is a pure copy; tail tokens are zero
+    assert np.array_equal(got[2].cpu().numpy(), ref[2])
+    Lp = ref[1].shape[-1]
+    if Lp > L:
+        assert not got[1].cpu().numpy()[..., L:].any()
+
+
+def test_qkv_direct(oracle, cuda):
+    import torch
+    from tsplat.qkv import gemm_nf24_qkv_direct
+
+    B, L, H = 2, 45, 2
+    C = H * 64
+    r = np.random.default_rng(8)
+    x = r.standard_normal((B * L, C), dtype=np.float32)
+    w = (r.standard_normal((3 * C, C)) * 0.03).astype(np.float32)
+    b = (r.standard_normal(3 * C) * 0.01).astype(np.float32)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    fr = _freqs(B, L, H, 5)
+    qg, kg = _gammas(H, 6)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    got = gemm_nf24_qkv_direct(t(x), t(c01), t(q2), t(s), t(b), t(fr), t(qg), t(kg), B, L, H)
+    ref = oracle.gemm_nf24_qkv_direct(x, c01, q2, s, b, fr, qg, kg, B, L, H)
+    proj = oracle.nf24_gemm(x, c01, q2, s, b)
+    bound = gemm_order_bound(x, oracle.decode_nf24(c01, q2, s), b)  # [B*L, 3C]
+    for which, (g, r_) in enumerate(zip(got, ref)):
+        g = g.cpu().numpy()
+        part = slice(which * C, (which + 1) * C)
+        xb = bound[:, part].reshape(B, L, H, 64)
+        xn = np.linalg.norm(proj[:, part].reshape(B, L, H, 64).astype(np.float64), axis=-1)
+        if which < 2:
+            tol = 8.0 * np.linalg.norm(xb, axis=-1) / xn * 1.2 + 1e-5   # [B, L, H]
+            tol = tol.transpose(0, 2, 1)[..., None]                      # [B, H, L, 1]
+        else:
+            tol = xb.transpose(0, 2, 1, 3)                                # [B, H, L, 64]
+        if which == 0:
+            d = np.abs(g - r_)
+        else:
+            d = np.abs(g[..., :L] - r_[..., :L]).transpose(0, 1, 3, 2)   # -> [B, H, L, 64]
+        assert np.all(d <= tol), (which, float(d.max()))
+
+
+@pytest.mark.parametrize("out_f,in_f", [(64, 96), (17, 64), (3072, 1024), (5, 1024), (100, 33)])
+def test_device_packer_bit_exact(oracle, cuda, out_f, in_f):
+    import torch
+    from tsplat.nf24 import quantize_nf24_i16_per_output_channel
+
+    w = (np.random.default_rng(out_f + in_f).standard_normal((out_f, in_f)) * 0.03).astype(np.float32)
+    w[0, :] = 0.0  # an all-zero row (scale from FLT_MIN)
+    codes, scales, err = quantize_nf24_i16_per_output_channel(torch.from_numpy(w).to(cuda))
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    assert np.array_equal(codes[0].cpu().numpy(), c01)
+    assert np.array_equal(codes[1].cpu().numpy(), q2)
+    assert np.array_equal(scales[0].cpu().numpy().view(np.uint32), s.view(np.uint32))
+    assert err["weight_rmse"] < 1e-6 and err["nf8_derived_alphabet_size"] == 163

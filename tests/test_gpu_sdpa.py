@@ -1,0 +1,193 @@
+"""GPU parity of the exact SDPA (libtsplat_hip.so) against the CPU oracle.
+
+The oracle (oracle/tsplat_oracle.c) is bit-exact with
+scripts/native_sdpa_avx512_exact_q8t512.c; tolerance derivation is in
+_parity.py (SDPA_ATOL_PER_MAXV, SDPA_RMSE_PER_RMSV).  Cases follow the
+reference's smoke/bench scripts, ragged tails, the packed/BLHD variant, the
+per-head bias extension, and the full L=16384 configuration through
+sampled query rows and size-independent invariants.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from _parity import SDPA_ATOL_PER_MAXV, SDPA_RMSE_PER_RMSV, sdpa_f64, stats
+
+pytestmark = pytest.mark.gpu
+
+
+def _qkv(seed, B, H, Lq, Lk):
+    r = np.random.default_rng(seed)
+    q = r.standard_normal((B, H, Lq, 64), dtype=np.float32)
+    k = r.standard_normal((B, H, Lk, 64), dtype=np.float32)
+    v = r.standard_normal((B, H, Lk, 64), dtype=np.float32)
+    return q, k, v
+
+
+def _run(torch, device, q, k, v, bias=None, per_head=False, packed=False, blhd=False):
+    from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
+
+    q, k, v = (np.ascontiguousarray(a) for a in (q, k, v))
+    qd = torch.from_numpy(q).to(device)
+    Lk = k.shape[2]
+    if packed:
+        Lkp = (Lk + 15) // 16 * 16
+        pk = np.zeros(k.shape[:2] + (64, Lkp), np.float32)
+        pv = np.zeros_like(pk)
+        pk[..., :Lk] = k.transpose(0, 1, 3, 2)
+        pv[..., :Lk] = v.transpose(0, 1, 3, 2)
+        kd, vd = torch.from_numpy(pk).to(device), torch.from_numpy(pv).to(device)
+    else:
+        kd, vd = torch.from_numpy(k).to(device), torch.from_numpy(v).to(device)
+    kw = {}
+    if bias is not None:
+        kw["key_bias_per_head" if per_head else "key_bias"] = torch.from_numpy(bias).to(device)
+    out = native_sdpa_f32_ex(qd, kd, vd, kv_packed=packed, key_count=Lk,
+                             out_layout="blhd" if blhd else "bhld", **kw)
+    torch.cuda.synchronize(device)
+    return out.cpu().numpy()
+
+
+def _assert_close(got, ref, v):
+    s = stats(got, ref)
+    tol = SDPA_ATOL_PER_MAXV * float(np.abs(v).max())
+    assert np.all(np.isfinite(got))
+    assert s["max_abs"] <= tol, (s, tol)
+    assert s["rmse"] <= SDPA_RMSE_PER_RMSV * float(np.sqrt(np.mean(v.astype(np.float64) ** 2))), s
+    return s
+
+
+# (B, H, Lq, Lk, bias): scripts/smoke_custom_sdpa_backend.py:121-133 cases,
+# scripts/bench_native_sdpa_avx512_exact.py:146 defaults, ragged tails.
+CASES = [
+    (1, 2, 16, 16, None),
+    (1, 2, 17, 17, ("one", 0, math.log(7.0))),
+    (1, 2, 15, 19, None),
+    (1, 16, 256, 256, None),
+    (1, 16, 256, 256, ("one", 7, 2.0)),
+    (1, 16, 193, 256, None),
+    (1, 1, 1, 1, None),
+    (2, 3, 129, 63, ("uniform",)),
+    (1, 2, 300, 65, None),
+    (1, 2, 127, 127, ("uniform",)),
+    (1, 4, 64, 513, None),
+    (2, 2, 70, 1100, ("uniform",)),
+]
+
+
+def _bias(spec, Lk, H, seed):
+    if spec is None:
+        return None
+    if spec[0] == "one":
+        b = np.zeros(Lk, np.float32)
+        b[spec[1]] = np.float32(spec[2])
+        return b
+    return np.random.default_rng(seed).uniform(-2.0, 0.0, Lk).astype(np.float32)
+
+
+@pytest.mark.parametrize("B,H,Lq,Lk,bspec", CASES)
+def test_sdpa_matches_oracle(oracle, cuda, B, H, Lq, Lk, bspec):
+    import torch
+
+    print(f"sdpa B={B} H={H} Lq={Lq} Lk={Lk} bias={bspec}", flush=True)
+    q, k, v = _qkv(11 + Lq + Lk, B, H, Lq, Lk)
+    bias = _bias(bspec, Lk, H, 5)
+    got = _run(torch, cuda, q, k, v, bias)
+    ref = oracle.sdpa_q8t512(q, k, v, bias)
+    _assert_close(got, ref, v)
+    # and against the float64 textbook formula (the reference smoke gate is 1e-4)
+    assert stats(got, sdpa_f64(q, k, v, bias))["max_abs"] < 1e-4
+
+
+@pytest.mark.parametrize("B,H,Lq,Lk,bspec", [(1, 2, 15, 19, None), (1, 3, 130, 70, ("uniform",)),
+                                              (2, 2, 64, 1040, None)])
+def test_sdpa_packed_blhd(oracle, cuda, B, H, Lq, Lk, bspec):
+    import torch
+
+    q, k, v = _qkv(23 + Lk, B, H, Lq, Lk)
+    bias = _bias(bspec, Lk, H, 9)
+    got = _run(torch, cuda, q, k, v, bias, packed=True, blhd=True)
+    Lkp = (Lk + 15) // 16 * 16
+    pk = np.zeros((B, H, 64, Lkp), np.float32)
+    pv = np.zeros_like(pk)
+    pk[..., :Lk] = k.transpose(0, 1, 3, 2)
+    pv[..., :Lk] = v.transpose(0, 1, 3, 2)
+    ref = oracle.sdpa_q8t512_packed_blhd(q, pk, pv, Lk, bias)
+    _assert_close(got, ref, v)
+
+
+def test_sdpa_per_head_bias(oracle, cuda):
+    """Per-head key bias [H, Lk] (config 3), against one oracle call per head."""
+    import torch
+
+    B, H, Lq, Lk = 1, 4, 96, 200
+    q, k, v = _qkv(31, B, H, Lq, Lk)
+    bias = np.random.default_rng(13).uniform(-2.0, 0.0, (H, Lk)).astype(np.float32)
+    got = _run(torch, cuda, q, k, v, bias, per_head=True)
+    ref = oracle.sdpa_q8t512(q, k, v, bias, bias_head_stride=Lk)
+    for h in range(H):
+        ref_h = oracle.sdpa_q8t512(q[:, h:h + 1], k[:, h:h + 1], v[:, h:h + 1], bias[h])
+        assert np.array_equal(ref_h, ref[:, h:h + 1])
+    _assert_close(got, ref, v)
+
+
+def test_sdpa_invariants(cuda):
+    """log(M) bias on one key == that key repeated M times
+    (scripts/triposplat_attention_patch.py:5468-5475); permuting keys with
+    their values and bias leaves the output unchanged; Lk == 1 returns v."""
+    import torch
+
+    B, H, Lq, Lk, M = 1, 2, 80, 90, 7
+    q, k, v = _qkv(41, B, H, Lq, Lk)
+    bias = np.zeros(Lk, np.float32)
+    bias[3] = np.float32(math.log(M))
+    got = _run(torch, cuda, q, k, v, bias)
+    kk = np.concatenate([k] + [k[:, :, 3:4]] * (M - 1), axis=2)
+    vv = np.concatenate([v] + [v[:, :, 3:4]] * (M - 1), axis=2)
+    dup = _run(torch, cuda, q, kk, vv)
+    assert stats(got, dup)["max_abs"] <= 2e-5 * float(np.abs(v).max())
+    perm = np.random.default_rng(1).permutation(Lk)
+    bias2 = np.random.default_rng(2).uniform(-2, 0, Lk).astype(np.float32)
+    a = _run(torch, cuda, q, k, v, bias2)
+    b = _run(torch, cuda, q, k[:, :, perm], v[:, :, perm], bias2[perm])
+    assert stats(a, b)["max_abs"] <= 2e-5 * float(np.abs(v).max())
+    q1, k1, v1 = _qkv(43, 1, 2, 33, 1)
+    one = _run(torch, cuda, q1, k1, v1)
+    assert np.array_equal(one, np.broadcast_to(v1, one.shape))
+
+
+def _rope_rmsnorm(x, theta=10000.0):
+    """Config-2 preprocessing on the host in float64: interleaved-pair RoPE
+    (position = token index, freq_i = theta^(-2i/64)) then RMSNorm to norm 8."""
+    L = x.shape[2]
+    i = np.arange(32, dtype=np.float64)
+    ang = np.arange(L, dtype=np.float64)[:, None] * theta ** (-2.0 * i / 64.0)[None, :]
+    c, s = np.cos(ang), np.sin(ang)
+    x64 = x.astype(np.float64)
+    re, im = x64[..., 0::2], x64[..., 1::2]
+    y = np.empty_like(x64)
+    y[..., 0::2] = re * c - im * s
+    y[..., 1::2] = re * s + im * c
+    y *= 8.0 / np.linalg.norm(y, axis=-1, keepdims=True)
+    return y.astype(np.float32)
+
+
+def test_sdpa_config2_sampled_rows(oracle, cuda):
+    """Config 2 (B=1, H=16, L=16384, RoPE+RMSNorm q/k): full GPU call, the
+    oracle on sampled query rows of every head (rows are independent)."""
+    import torch
+
+    B, H, L = 1, 16, 16384
+    r = np.random.default_rng(10)
+    q = _rope_rmsnorm(r.standard_normal((B, H, L, 64), dtype=np.float32))
+    k = _rope_rmsnorm(np.random.default_rng(11).standard_normal((B, H, L, 64), dtype=np.float32))
+    v = np.random.default_rng(12).standard_normal((B, H, L, 64), dtype=np.float32)
+    got = _run(torch, cuda, q, k, v)
+    rows = np.sort(r.choice(L, 24, replace=False))
+    rows[0], rows[-1] = 0, L - 1
+    ref = oracle.sdpa_q8t512(q[:, :, rows], k, v)
+    s = _assert_close(got[:, :, rows], ref, v)
+    print("config2 sampled rows", s)

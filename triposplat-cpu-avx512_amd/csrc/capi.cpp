@@ -1,0 +1,405 @@
+// C-ABI layer of libtsplat_hip.so: argument validation with the reference's
+// status codes, device-pointer extent checks, and dispatch to the gfx950
+// kernels.  Declarations and the reference interface each symbol replaces
+// are in include/tsplat_hip.h.
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <chrono>
+#include <cstdint>
+
+#include "tsplat_common.h"
+#include "tsplat_launch.h"
+#include "../../include/tsplat_hip.h"
+
+using namespace tsplat;
+
+namespace {
+
+constexpr int kHeadDim = 64;
+constexpr int kAbiVersion = 1;
+
+std::atomic<int> g_last_hip_error{0};
+std::atomic<uint64_t> g_sdpa_calls{0};
+std::atomic<uint64_t> g_sdpa_ns{0};
+
+int note(hipError_t e) {
+  if (e != hipSuccess) g_last_hip_error.store((int)e);
+  return e == hipSuccess ? kOk : kErrLaunch;
+}
+
+// The allocation containing [p, p + bytes) must be device (or managed) memory
+// of the current device.  This turns a wrong pointer into a status code
+// instead of a GPU memory fault.
+int check_dev(const void* p, int64_t bytes) {
+  if (p == nullptr) return kErrNull;
+  if (bytes <= 0) return kOk;
+  hipPointerAttribute_t attr;
+  hipError_t e = hipPointerGetAttributes(&attr, p);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return kErrPointer;
+  }
+  if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged) return kErrPointer;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || attr.device != dev) return kErrPointer;
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  e = hipMemGetAddressRange(&base, &size, const_cast<void*>(p));
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return kErrPointer;
+  }
+  const char* lo = static_cast<const char*>(base);
+  const char* q = static_cast<const char*>(p);
+  if (q < lo || (uint64_t)(q - lo) + (uint64_t)bytes > (uint64_t)size) return kErrPointer;
+  return kOk;
+}
+
+#define TSPLAT_CHECK(expr)        \
+  do {                            \
+    const int st_ = (expr);       \
+    if (st_ != kOk) return st_;   \
+  } while (0)
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int sync_null_stream() { return note(hipStreamSynchronize(nullptr)); }
+
+// ---------------------------------------------------------------- GEMM
+int gemm_checked(const float* x, const int16_t* code01, const int8_t* q2, const float* scale,
+                 const float* bias, float* out, int M, int K, int N, int start, int count,
+                 int stride_x, int stride_out, hipStream_t stream) {
+  TSPLAT_CHECK(check_dev(x, ((int64_t)(M - 1) * stride_x + K) * 4));
+  TSPLAT_CHECK(check_dev(code01, (int64_t)K * N * 2));
+  TSPLAT_CHECK(check_dev(q2, (int64_t)K * N));
+  TSPLAT_CHECK(check_dev(scale, (int64_t)N * 4));
+  TSPLAT_CHECK(check_dev(bias, (int64_t)N * 4));
+  TSPLAT_CHECK(check_dev(out, ((int64_t)(M - 1) * stride_out + count) * 4));
+  GemmParams p{x, code01, q2, scale, bias, out, M, K, N, start, count, stride_x, stride_out};
+  const int st = launch_nf24_gemm(p, stream);
+  if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
+  return st;
+}
+
+bool ref_gemm_ptrs_ok(const void* a, const void* b, const void* c, const void* d, const void* e,
+                      const void* f, const void* g, const void* h, const void* i, const void* j) {
+  return a && b && c && d && e && f && g && h && i && j;
+}
+
+// ---------------------------------------------------------------- SDPA
+int sdpa_checked(const float* q, const float* k, const float* v, const float* bias, float* out,
+                 int B, int H, int Lq, int Lk, int D, int has_bias, int bias_len,
+                 int64_t bias_head_stride, int kv_packed, int Lkp, int out_blhd,
+                 hipStream_t stream) {
+  if (!q || !k || !v || !out) return kErrNull;
+  if (B <= 0 || H <= 0 || Lq <= 0 || Lk <= 0 || D != kHeadDim) return kErrDims;
+  if (kv_packed && (Lkp < Lk || (Lkp & 15) != 0)) return kErrDims;
+  if (has_bias && (bias == nullptr || bias_len != Lk)) return kErrRange;
+  if (has_bias && bias_head_stride != 0 && bias_head_stride < Lk) return kErrRange;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return kErrAlign;
+  const int64_t bh = (int64_t)B * H;
+  TSPLAT_CHECK(check_dev(q, bh * Lq * kHeadDim * 4));
+  const int64_t kv_elems = kv_packed ? bh * kHeadDim * Lkp : bh * Lk * kHeadDim;
+  TSPLAT_CHECK(check_dev(k, kv_elems * 4));
+  TSPLAT_CHECK(check_dev(v, kv_elems * 4));
+  TSPLAT_CHECK(check_dev(out, bh * Lq * kHeadDim * 4));
+  if (has_bias) TSPLAT_CHECK(check_dev(bias, ((int64_t)(H - 1) * bias_head_stride + Lk) * 4));
+  SdpaParams p{q, k, v, has_bias ? bias : nullptr, out, B, H, Lq, Lk, kv_packed, Lkp,
+               bias_head_stride, out_blhd};
+  const int st = launch_sdpa(p, stream);
+  if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
+  return st;
+}
+
+int sdpa_blocking(const float* q, const float* k, const float* v, const float* bias, float* out,
+                  int B, int H, int Lq, int Lk, int D, int has_bias, int bias_len, int kv_packed,
+                  int Lkp, int out_blhd) {
+  const auto t0 = std::chrono::steady_clock::now();
+  int st = sdpa_checked(q, k, v, bias, out, B, H, Lq, Lk, D, has_bias, bias_len, 0, kv_packed,
+                        Lkp, out_blhd, nullptr);
+  if (st == kOk) st = sync_null_stream();
+  if (st == kOk) {
+    const auto t1 = std::chrono::steady_clock::now();
+    g_sdpa_calls.fetch_add(1, std::memory_order_relaxed);
+    g_sdpa_ns.fetch_add(
+        (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count(),
+        std::memory_order_relaxed);
+  }
+  return st;
+}
+
+// ---------------------------------------------------------------- QKV
+int post_checked(const float* qkv, const float* freqs, const float* qg, const float* kg,
+                 float* q, float* pk, float* pv, int B, int L, int H, int D, int Lp, int fb,
+                 hipStream_t stream) {
+  if (!qkv || !freqs || !qg || !kg || !q || !pk || !pv) return kErrNull;
+  if (B <= 0 || L <= 0 || H <= 0 || D != kHeadDim || Lp < L || (Lp & 15) != 0 ||
+      (fb != 1 && fb != B))
+    return kErrDims;
+  if (!aligned16(qkv) || !aligned16(freqs) || !aligned16(qg) || !aligned16(kg) ||
+      !aligned16(q) || !aligned16(pk) || !aligned16(pv))
+    return kErrAlign;
+  const int64_t C = (int64_t)H * kHeadDim;
+  TSPLAT_CHECK(check_dev(qkv, (int64_t)B * L * 3 * C * 4));
+  TSPLAT_CHECK(check_dev(freqs, (int64_t)fb * L * C * 4));
+  TSPLAT_CHECK(check_dev(qg, C * 4));
+  TSPLAT_CHECK(check_dev(kg, C * 4));
+  TSPLAT_CHECK(check_dev(q, (int64_t)B * L * C * 4));
+  TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * Lp * 4));
+  TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lp * 4));
+  QkvPostParams p{qkv, freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb};
+  const int st = launch_qkv_postprocess(p, stream);
+  if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
+  return st;
+}
+
+int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
+                       const float* scale, const float* bias, const float* freqs,
+                       const float* qg, const float* kg, float* q, float* pk, float* pv, int B,
+                       int L, int K, int N, int H, int D, int Lp, int fb, hipStream_t stream) {
+  if (!x || !code01 || !q2 || !scale || !bias || !freqs || !qg || !kg || !q || !pk || !pv)
+    return kErrNull;
+  if (B <= 0 || L <= 0 || K <= 0 || H <= 0 || D != kHeadDim || N != 3 * H * D || Lp < L ||
+      (Lp & 15) != 0 || (fb != 1 && fb != B))
+    return kErrDims;
+  const int64_t M = (int64_t)B * L;
+  if (M > 0x7fffffff) return kErrDims;
+  // The [B*L, N] projection lives only for the duration of the call, in
+  // stream-ordered device memory.
+  float* qkv = nullptr;
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&qkv), (size_t)M * N * 4, stream);
+  if (e != hipSuccess || qkv == nullptr) {
+    (void)hipGetLastError();
+    return kErrWorkspace;
+  }
+  int st = gemm_checked(x, code01, q2, scale, bias, qkv, (int)M, K, N, 0, N, K, N, stream);
+  if (st == kOk) st = post_checked(qkv, freqs, qg, kg, q, pk, pv, B, L, H, D, Lp, fb, stream);
+  const int fst = note(hipFreeAsync(qkv, stream));
+  return st != kOk ? st : fst;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ------------------------------------------------------------------ GEMM
+int triposplat_gemm_rnf8_avx512_range(const float* x, const uint8_t* codes0_t,
+                                      const uint8_t* codes1_t, const uint8_t* codes2_t,
+                                      const float* scales0, const float* scales1,
+                                      const float* scales2, const float* codebook,
+                                      const float* bias, float* out, int M, int K, int N,
+                                      int output_start, int output_count, int stride_x,
+                                      int stride_out, int threads, int stages) {
+  (void)threads;
+  if (!ref_gemm_ptrs_ok(x, codes0_t, codes1_t, codes2_t, scales0, scales1, scales2, codebook,
+                        bias, out))
+    return kErrNull;
+  if (M <= 0 || K <= 0 || N <= 0 || output_start < 0 || output_count <= 0 || stages != 3)
+    return kErrDims;
+  if (output_start + output_count > N || stride_x < K || stride_out < output_count)
+    return kErrRange;
+  if ((output_start & 15) != 0 || (output_count & 15) != 0) return kErrAlign;
+  int st = gemm_checked(x, reinterpret_cast<const int16_t*>(codes0_t),
+                        reinterpret_cast<const int8_t*>(codes1_t), scales0, bias, out, M, K, N,
+                        output_start, output_count, stride_x, stride_out, nullptr);
+  return st == kOk ? sync_null_stream() : st;
+}
+
+int triposplat_gemm_rnf8_avx512(const float* x, const uint8_t* codes0_t, const uint8_t* codes1_t,
+                                const uint8_t* codes2_t, const float* scales0,
+                                const float* scales1, const float* scales2, const float* codebook,
+                                const float* bias, float* out, int M, int K, int N, int stride_x,
+                                int stride_out, int threads, int stages) {
+  return triposplat_gemm_rnf8_avx512_range(x, codes0_t, codes1_t, codes2_t, scales0, scales1,
+                                           scales2, codebook, bias, out, M, K, N, 0, N, stride_x,
+                                           stride_out, threads, stages);
+}
+
+int triposplat_gemm_rnf8_avx512_tail(const float* x, const uint8_t* codes0_t,
+                                     const uint8_t* codes1_t, const uint8_t* codes2_t,
+                                     const float* scales0, const float* scales1,
+                                     const float* scales2, const float* codebook,
+                                     const float* bias, float* out, int M, int K, int N,
+                                     int stride_x, int stride_out, int threads, int stages) {
+  (void)threads;
+  if (!ref_gemm_ptrs_ok(x, codes0_t, codes1_t, codes2_t, scales0, scales1, scales2, codebook,
+                        bias, out))
+    return kErrNull;
+  if (M <= 0 || K <= 0 || N <= 0 || stride_x < K || stride_out < N || stages != 3)
+    return kErrDims;
+  int st = gemm_checked(x, reinterpret_cast<const int16_t*>(codes0_t),
+                        reinterpret_cast<const int8_t*>(codes1_t), scales0, bias, out, M, K, N,
+                        0, N, stride_x, stride_out, nullptr);
+  return st == kOk ? sync_null_stream() : st;
+}
+
+int triposplat_gemm_rnf8_avx512_row_tile(void) { return 128; }
+int triposplat_gemm_rnf8_avx512_residual_mode(void) { return 4; }
+
+int tsplat_nf24_gemm_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,
+                           const float* scale, const float* bias, float* out, int M, int K, int N,
+                           int output_start, int output_count, int stride_x, int stride_out,
+                           void* stream) {
+  if (!x || !code01_t || !q2_t || !scale || !bias || !out) return kErrNull;
+  if (M <= 0 || K <= 0 || N <= 0 || output_start < 0 || output_count <= 0) return kErrDims;
+  if (output_start + output_count > N || stride_x < K || stride_out < output_count)
+    return kErrRange;
+  return gemm_checked(x, code01_t, q2_t, scale, bias, out, M, K, N, output_start, output_count,
+                      stride_x, stride_out, static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------------------ SDPA
+int triposplat_sdpa_f32_avx512_exact_q8t512(const float* q, const float* k, const float* v,
+                                            const float* key_bias_or_null, float* out, int B,
+                                            int H, int Lq, int Lk, int D, int has_key_bias,
+                                            int key_bias_len, int threads) {
+  (void)threads;
+  return sdpa_blocking(q, k, v, key_bias_or_null, out, B, H, Lq, Lk, D, has_key_bias,
+                       key_bias_len, 0, 0, 0);
+}
+
+int triposplat_sdpa_f32(const float* q, const float* k, const float* v,
+                        const float* key_bias_or_null, float* out, int B, int H, int Lq, int Lk,
+                        int D, int has_key_bias, int key_bias_len, int threads) {
+  return triposplat_sdpa_f32_avx512_exact_q8t512(q, k, v, key_bias_or_null, out, B, H, Lq, Lk, D,
+                                                 has_key_bias, key_bias_len, threads);
+}
+
+int triposplat_sdpa_f32_avx512_exact_q8(const float* q, const float* k, const float* v,
+                                        const float* key_bias_or_null, float* out, int B, int H,
+                                        int Lq, int Lk, int D, int has_key_bias,
+                                        int key_bias_len, int threads) {
+  return triposplat_sdpa_f32_avx512_exact_q8t512(q, k, v, key_bias_or_null, out, B, H, Lq, Lk, D,
+                                                 has_key_bias, key_bias_len, threads);
+}
+
+int triposplat_sdpa_f32_avx512_exact_q8t512_packed_blhd(
+    const float* q, const float* packed_k, const float* packed_v, const float* key_bias_or_null,
+    float* out_blhd, int B, int H, int Lq, int Lk, int D, int Lkp, int has_key_bias,
+    int key_bias_len, int threads) {
+  (void)threads;
+  return sdpa_blocking(q, packed_k, packed_v, key_bias_or_null, out_blhd, B, H, Lq, Lk, D,
+                       has_key_bias, key_bias_len, 1, Lkp, 1);
+}
+
+int triposplat_sdpa_key_tile(void) { return 64; }
+int triposplat_sdpa_query_block(void) { return 128; }
+int triposplat_sdpa_packed_output_is_blhd(void) { return 1; }
+
+void triposplat_sdpa_q8t512_profile_reset(void) {
+  g_sdpa_calls.store(0);
+  g_sdpa_ns.store(0);
+}
+
+int triposplat_sdpa_q8t512_profile_get(uint64_t* calls, uint64_t* allocate_ns, uint64_t* pack_ns,
+                                       uint64_t* compute_ns, uint64_t* free_ns) {
+  if (!calls || !allocate_ns || !pack_ns || !compute_ns || !free_ns) return kErrNull;
+  *calls = g_sdpa_calls.load();
+  *allocate_ns = 0;
+  *pack_ns = 0;
+  *compute_ns = g_sdpa_ns.load();
+  *free_ns = 0;
+  return kOk;
+}
+
+int triposplat_sdpa_q8t512_workspace_stats(uint64_t* allocations, uint64_t* capacity_bytes) {
+  if (!allocations || !capacity_bytes) return kErrNull;
+  *allocations = 0;
+  *capacity_bytes = 0;
+  return kOk;
+}
+
+void triposplat_sdpa_q8t512_workspace_release(void) {}
+
+int tsplat_sdpa_async(const float* q, const float* k, const float* v,
+                      const float* key_bias_or_null, float* out, int B, int H, int Lq, int Lk,
+                      int D, int has_key_bias, int key_bias_len, int64_t bias_head_stride,
+                      int kv_packed, int Lkp, int out_blhd, void* stream) {
+  return sdpa_checked(q, k, v, key_bias_or_null, out, B, H, Lq, Lk, D, has_key_bias,
+                      key_bias_len, bias_head_stride, kv_packed, Lkp, out_blhd,
+                      static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------------------ QKV
+int triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2(const float* qkv, const float* frequencies,
+                                                   const float* q_gamma, const float* k_gamma,
+                                                   float* q_bhld, float* packed_k,
+                                                   float* packed_v, int B, int L, int H, int D,
+                                                   int L_padded, int frequency_batches,
+                                                   int threads) {
+  (void)threads;
+  int st = post_checked(qkv, frequencies, q_gamma, k_gamma, q_bhld, packed_k, packed_v, B, L, H,
+                        D, L_padded, frequency_batches, nullptr);
+  return st == kOk ? sync_null_stream() : st;
+}
+
+int triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512(
+    const float* x, const uint8_t* codes0_t, const uint8_t* codes1_t, const uint8_t* codes2_t,
+    const float* scales0, const float* scales1, const float* scales2, const float* codebook,
+    const float* bias, const float* frequencies, const float* q_gamma, const float* k_gamma,
+    float* q_bhld, float* packed_k, float* packed_v, int B, int L, int K, int N, int H, int D,
+    int L_padded, int frequency_batches, int threads, int stages) {
+  (void)threads;
+  if (!ref_gemm_ptrs_ok(x, codes0_t, codes1_t, codes2_t, scales0, scales1, scales2, codebook,
+                        bias, frequencies) ||
+      !q_gamma || !k_gamma || !q_bhld || !packed_k || !packed_v)
+    return kErrNull;
+  if (stages != 3) return kErrDims;
+  int st = qkv_direct_checked(x, reinterpret_cast<const int16_t*>(codes0_t),
+                              reinterpret_cast<const int8_t*>(codes1_t), scales0, bias,
+                              frequencies, q_gamma, k_gamma, q_bhld, packed_k, packed_v, B, L, K,
+                              N, H, D, L_padded, frequency_batches, nullptr);
+  return st == kOk ? sync_null_stream() : st;
+}
+
+int triposplat_gemm_nf24_qkv_direct_row_tile(void) { return 128; }
+int triposplat_gemm_nf24_qkv_direct_residual_mode(void) { return 4; }
+
+int tsplat_qkv_postprocess_async(const float* qkv, const float* frequencies, const float* q_gamma,
+                                 const float* k_gamma, float* q_bhld, float* packed_k,
+                                 float* packed_v, int B, int L, int H, int D, int L_padded,
+                                 int frequency_batches, void* stream) {
+  return post_checked(qkv, frequencies, q_gamma, k_gamma, q_bhld, packed_k, packed_v, B, L, H, D,
+                      L_padded, frequency_batches, static_cast<hipStream_t>(stream));
+}
+
+int tsplat_gemm_nf24_qkv_direct_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,
+                                      const float* scale, const float* bias,
+                                      const float* frequencies, const float* q_gamma,
+                                      const float* k_gamma, float* q_bhld, float* packed_k,
+                                      float* packed_v, int B, int L, int K, int N, int H, int D,
+                                      int L_padded, int frequency_batches, void* stream) {
+  return qkv_direct_checked(x, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, q_bhld,
+                            packed_k, packed_v, B, L, K, N, H, D, L_padded, frequency_batches,
+                            static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------------------ packer
+int tsplat_nf24_pack_async(const float* weight, int out_features, int in_features,
+                           const float* alphabet, int alphabet_len, float* base_workspace,
+                           int16_t* code01_t, int8_t* q2_t, float* scale, void* stream) {
+  if (!weight || !alphabet || !base_workspace || !code01_t || !q2_t || !scale) return kErrNull;
+  if (out_features <= 0 || in_features <= 0 || alphabet_len < 2 || alphabet_len > 256)
+    return kErrDims;
+  const int64_t count = (int64_t)out_features * in_features;
+  TSPLAT_CHECK(check_dev(weight, count * 4));
+  TSPLAT_CHECK(check_dev(alphabet, (int64_t)alphabet_len * 4));
+  TSPLAT_CHECK(check_dev(base_workspace, (int64_t)out_features * 4));
+  TSPLAT_CHECK(check_dev(code01_t, count * 2));
+  TSPLAT_CHECK(check_dev(q2_t, count));
+  TSPLAT_CHECK(check_dev(scale, (int64_t)out_features * 4));
+  const int st = launch_nf24_pack(weight, out_features, in_features, alphabet, alphabet_len,
+                                  base_workspace, code01_t, q2_t, scale,
+                                  static_cast<hipStream_t>(stream));
+  if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
+  return st;
+}
+
+// ------------------------------------------------------------------ library
+int tsplat_abi_version(void) { return kAbiVersion; }
+int tsplat_last_hip_error(void) { return g_last_hip_error.load(); }
+const char* tsplat_build_arch(void) { return "gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,236 @@
+// NF24 packed-weight GEMM for gfx950: out = bias + X * decode(W).
+//
+// Reference semantics: scripts/gemm_nf24_i16_avx512.c:26-33 (decode16) and
+// :35-197 (kernel_mx16 / range API).  Each weight is decoded exactly as the
+// reference does -- fp32((int32)q01 * 256 + q2) * scale[n], one rounding --
+// in registers, right after the packed codes arrive from HBM; no fp32
+// weight copy ever exists in HBM.  The products are accumulated with fp32
+// MFMA (v_mfma_f32_32x32x2_f32), so only the summation order differs from
+// the reference's sequential fmaf chain.
+//
+// Tiling: a workgroup computes a BM x BN output tile with WM x WN waves; a
+// wave owns (BM/WM) x (BN/WN) = MB x NB blocks of 32x32.  Per K step of BK,
+// the X tile (fp32) and the decoded W tile (fp32) are staged in LDS, both
+// stored k-contiguous ([row][k] and [col][k]) so that every lane fetches
+// four consecutive k of its row/column with one ds_read_b128.  The K index
+// inside an 8-wide slice is permuted: MFMA step t of slice kk reads
+// k = 8*kk + 4*(lane/32) + t, the same permutation for A and B, which keeps
+// the dot product exact while turning 4 scalar LDS reads into one.
+// The next K step's codes and X are fetched into registers while the MFMAs
+// of the current step run (double-buffered LDS, one barrier per step).
+
+#include "tsplat_common.h"
+#include "tsplat_launch.h"
+
+namespace tsplat {
+namespace {
+
+template <int BM_, int BN_, int BK_, int WM_, int WN_>
+struct GemmCfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  static constexpr int kThreads = WM * WN * 64;
+  static constexpr int kTM = BM / WM, kTN = BN / WN;
+  static constexpr int kMB = kTM / 32, kNB = kTN / 32;
+  static constexpr int kS = BK + 4;  // LDS row stride in floats (bank spread)
+  static constexpr int kXVec = BM * BK / 4 / kThreads;  // X float4 per thread
+  static constexpr int kPairs = BN / 2;                  // W column pairs
+  static constexpr int kKGroups = kThreads / kPairs;
+  static constexpr int kKPT = BK / kKGroups;             // k per thread for W
+  static_assert(kTM % 32 == 0 && kTN % 32 == 0, "wave tile must be 32-aligned");
+  static_assert(BK % 8 == 0, "BK must be a multiple of 8");
+  static_assert(kXVec * 4 * kThreads == BM * BK, "X tile split");
+  static_assert(kKGroups * kPairs == kThreads && kKPT % 4 == 0, "W tile split");
+};
+
+struct GemmArgs {
+  const float* x;
+  const int16_t* code01;
+  const int8_t* q2;
+  const float* scale;
+  const float* bias;
+  float* out;
+  int M, K, N, n_start, n_count, stride_x, stride_out;
+};
+
+// kVec: x rows 16-byte aligned with K % 4 == 0, and N, n_start, n_count even
+// (so a column pair is loaded with one 32-bit / 16-bit access).
+template <class C, bool kVec>
+__global__ __launch_bounds__(C::kThreads) void nf24_gemm_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) float xs[2][C::BM * C::kS];
+  __shared__ __attribute__((aligned(16))) float ws[2][C::BN * C::kS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int g = lane >> 5;
+  const int l32 = lane & 31;
+
+  const int tiles_n = (a.n_count + C::BN - 1) / C::BN;
+  const int tile = xcd_tile_index(blockIdx.x, gridDim.x);
+  const int m0 = (tile / tiles_n) * C::BM;
+  const int c0 = (tile % tiles_n) * C::BN;
+
+  // W assignment: this thread decodes columns (lc, lc+1) for kKPT k values.
+  const int pair = tid % C::kPairs;
+  const int kg = tid / C::kPairs;
+  const int lc = c0 + 2 * pair;
+  const bool ok0 = lc < a.n_count;
+  const bool ok1 = lc + 1 < a.n_count;
+  const int n_abs = a.n_start + lc;
+  const float sc0 = ok0 ? a.scale[n_abs] : 0.0f;
+  const float sc1 = ok1 ? a.scale[n_abs + 1] : 0.0f;
+
+  floatx4 xr[C::kXVec];
+  uint32_t cr[C::kKPT];  // two int16 codes (columns lc, lc+1)
+  uint32_t qr[C::kKPT];  // two int8 codes in the low 16 bits
+
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < C::kXVec; ++j) {
+      const int idx = tid + j * C::kThreads;
+      const int row = idx / (C::BK / 4);
+      const int kc = idx % (C::BK / 4);
+      const int gm = m0 + row;
+      const int gk = k0 + 4 * kc;
+      const float* src = a.x + (int64_t)gm * a.stride_x + gk;
+      if (kVec) {
+        xr[j] = (gm < a.M && gk < a.K) ? *reinterpret_cast<const floatx4*>(src) : floatx4{0, 0, 0, 0};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xr[j][e] = (gm < a.M && gk + e < a.K) ? src[e] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < C::kKPT; ++i) {
+      const int gk = k0 + kg * C::kKPT + i;
+      const int64_t off = (int64_t)gk * a.N + n_abs;
+      if (kVec) {
+        const bool ok = ok0 && gk < a.K;
+        cr[i] = ok ? *reinterpret_cast<const uint32_t*>(a.code01 + off) : 0u;
+        qr[i] = ok ? (uint32_t)*reinterpret_cast<const uint16_t*>(a.q2 + off) : 0u;
+      } else {
+        const bool k_ok = gk < a.K;
+        const uint32_t c_lo = (k_ok && ok0) ? (uint16_t)a.code01[off] : 0u;
+        const uint32_t c_hi = (k_ok && ok1) ? (uint16_t)a.code01[off + 1] : 0u;
+        const uint32_t q_lo = (k_ok && ok0) ? (uint8_t)a.q2[off] : 0u;
+        const uint32_t q_hi = (k_ok && ok1) ? (uint8_t)a.q2[off + 1] : 0u;
+        cr[i] = c_lo | (c_hi << 16);
+        qr[i] = q_lo | (q_hi << 8);
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < C::kXVec; ++j) {
+      const int idx = tid + j * C::kThreads;
+      const int row = idx / (C::BK / 4);
+      const int kc = idx % (C::BK / 4);
+      *reinterpret_cast<floatx4*>(&xs[buf][row * C::kS + 4 * kc]) = xr[j];
+    }
+#pragma unroll
+    for (int i4 = 0; i4 < C::kKPT; i4 += 4) {
+      floatx4 w0, w1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t c = cr[i4 + e];
+        const uint32_t q = qr[i4 + e];
+        const int32_t qa = (int32_t)(int16_t)(c & 0xffffu) * 256 + (int32_t)(int8_t)(q & 0xffu);
+        const int32_t qb = (int32_t)(int16_t)(c >> 16) * 256 + (int32_t)(int8_t)((q >> 8) & 0xffu);
+        w0[e] = (float)qa * sc0;
+        w1[e] = (float)qb * sc1;
+      }
+      *reinterpret_cast<floatx4*>(&ws[buf][(2 * pair) * C::kS + kg * C::kKPT + i4]) = w0;
+      *reinterpret_cast<floatx4*>(&ws[buf][(2 * pair + 1) * C::kS + kg * C::kKPT + i4]) = w1;
+    }
+  };
+
+  // Accumulators start at the bias, as the reference's chain does.
+  floatx16 acc[C::kMB][C::kNB];
+#pragma unroll
+  for (int nb = 0; nb < C::kNB; ++nb) {
+    const int col = c0 + wn * C::kTN + nb * 32 + l32;
+    const float bv = col < a.n_count ? a.bias[a.n_start + col] : 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < C::kMB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = bv;
+  }
+
+  const int nk = (a.K + C::BK - 1) / C::BK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) load_tile((kt + 1) * C::BK);
+    const float* xb = xs[buf];
+    const float* wb = ws[buf];
+#pragma unroll
+    for (int kk = 0; kk < C::BK / 8; ++kk) {
+      floatx4 af[C::kMB], bf[C::kNB];
+#pragma unroll
+      for (int mb = 0; mb < C::kMB; ++mb)
+        af[mb] = *reinterpret_cast<const floatx4*>(
+            &xb[(wm * C::kTM + mb * 32 + l32) * C::kS + 8 * kk + 4 * g]);
+#pragma unroll
+      for (int nb = 0; nb < C::kNB; ++nb)
+        bf[nb] = *reinterpret_cast<const floatx4*>(
+            &wb[(wn * C::kTN + nb * 32 + l32) * C::kS + 8 * kk + 4 * g]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int mb = 0; mb < C::kMB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < C::kNB; ++nb)
+            acc[mb][nb] = mfma32x32x2(af[mb][t], bf[nb][t], acc[mb][nb]);
+    }
+    if (kt + 1 < nk) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int mb = 0; mb < C::kMB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < C::kNB; ++nb) {
+      const int col = c0 + wn * C::kTN + nb * 32 + l32;
+      if (col >= a.n_count) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * C::kTM + mb * 32 + 8 * (r / 4) + 4 * g + (r % 4);
+        if (row < a.M) a.out[(int64_t)row * a.stride_out + col] = acc[mb][nb][r];
+      }
+    }
+}
+
+template <class C>
+int launch_cfg(const GemmParams& p, hipStream_t stream) {
+  GemmArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out,
+             p.M, p.K, p.N, p.n_start, p.n_count, p.stride_x, p.stride_out};
+  const int64_t tiles = (int64_t)((p.M + C::BM - 1) / C::BM) * ((p.n_count + C::BN - 1) / C::BN);
+  if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
+  const bool vec = (reinterpret_cast<uintptr_t>(p.x) % 16 == 0) && (p.stride_x % 4 == 0) &&
+                   (p.K % 4 == 0) && (p.N % 2 == 0) && (p.n_start % 2 == 0) &&
+                   (p.n_count % 2 == 0) && (reinterpret_cast<uintptr_t>(p.code01) % 4 == 0) &&
+                   (reinterpret_cast<uintptr_t>(p.q2) % 2 == 0);
+  dim3 grid((unsigned)tiles), block(C::kThreads);
+  if (vec)
+    hipLaunchKernelGGL((nf24_gemm_kernel<C, true>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((nf24_gemm_kernel<C, false>), grid, block, 0, stream, a);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+using CfgMain = GemmCfg<128, 128, 16, 2, 2>;
+using CfgSkinny = GemmCfg<32, 128, 32, 1, 4>;
+
+}  // namespace
+
+int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
+  if (p.M <= 32) return launch_cfg<CfgSkinny>(p, stream);
+  return launch_cfg<CfgMain>(p, stream);
+}
+
+}  // namespace tsplat

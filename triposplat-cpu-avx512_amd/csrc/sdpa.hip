@@ -1,0 +1,287 @@
+// Exact online-softmax SDPA for gfx950 (head dim 64, fp32 throughout).
+//
+// Reference semantics: scripts/native_sdpa_avx512_exact_q8t512.c:137-332 and
+// the packed/BLHD variant scripts/native_sdpa_avx512_exact_q8t512_packed.c:3-158:
+// out[q] = sum_j softmax_j(q.k_j * 0.125 + bias[j]) v_j, exact, with a
+// running (max, sum) merged tile by tile; no Lq x Lk matrix, no pruning.
+//
+// Mapping.  A workgroup owns 128 queries of one (b, h): four waves, 32
+// queries each, Q resident in registers.  Keys stream through LDS in
+// double-buffered tiles of 64 (K and V, plus the bias row).  Each wave
+// computes the transposed score block S^T = K Q^T with
+// v_mfma_f32_32x32x2_f32, which leaves every lane holding 32 keys of ONE
+// query (its own column): the row max and row sum are in-lane reductions
+// plus one v_permlane32_swap with the partner half-wave, and the
+// exponentiated block is already laid out as the B operand of the second
+// MFMA, O^T += V^T P^T, so P never leaves registers.  The head dimension
+// inside each 8-wide slice is permuted (step t of slice hh reads
+// d = 8*hh + 4*(lane/32) + t) identically for Q and K, so K fragments load
+// as ds_read_b128.
+//
+// Scores are kept in log2 units: x = (q.k) * (0.125 * log2 e) + bias * log2 e,
+// p = exp2(x - m) with v_exp_f32.  This is the reference's exp(s - m) up to
+// fp32 rounding of the argument; the merge is the usual rescale by
+// exp2(m_old - m_new).
+
+#include "tsplat_common.h"
+#include "tsplat_launch.h"
+
+namespace tsplat {
+namespace {
+
+constexpr int kD = 64;
+constexpr int kBQ = 128;   // queries per workgroup
+constexpr int kBKV = 64;   // keys per tile
+constexpr int kThreads = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct SdpaArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* bias;
+  float* out;
+  int B, H, Lq, Lk, Lkp;
+  int64_t bias_head_stride;
+  int out_blhd;
+};
+
+// max / sum of a value with the same register of lane l ^ 32.  Both lanes of
+// a pair obtain the identical result (the swap returns both halves).
+__device__ __forceinline__ float pair_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// kPacked: k/v are [B, H, 64, Lkp] (key-contiguous rows per dimension), as
+// the reference's packed kernel takes them; otherwise [B, H, Lk, 64].
+template <bool kPacked, bool kBias>
+__global__ __launch_bounds__(kThreads) void sdpa_kernel(SdpaArgs a) {
+  // LDS rows: unpacked K [key][d], packed K [d][key]; V likewise.
+  constexpr int kKS = kD + 4;                  // both K layouts: 64 + 4 pad
+  constexpr int kVS = kPacked ? kBKV + 4 : kD; // packed V is read as b128
+  __shared__ __attribute__((aligned(16))) float kbuf[2][64 * kKS];
+  __shared__ __attribute__((aligned(16))) float vbuf[2][64 * kVS];
+  __shared__ __attribute__((aligned(16))) float bbuf[2][kBKV];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 5;
+  const int l32 = lane & 31;
+
+  const int qblocks = (a.Lq + kBQ - 1) / kBQ;
+  const int tile = xcd_tile_index(blockIdx.x, gridDim.x);
+  const int bh = tile / qblocks;
+  const int qb = tile % qblocks;
+  const int h = bh % a.H;
+  const int b = bh / a.H;
+  const int qrow = qb * kBQ + wave * 32 + l32;
+  const bool q_ok = qrow < a.Lq;
+
+  // Q fragment for this lane's query: qf[hh][t] = q[8*hh + 4*g + t].
+  floatx4 qf[8];
+  {
+    const float* qp = a.q + ((int64_t)bh * a.Lq + (q_ok ? qrow : 0)) * kD + 4 * g;
+#pragma unroll
+    for (int hh = 0; hh < 8; ++hh)
+      qf[hh] = q_ok ? *reinterpret_cast<const floatx4*>(qp + 8 * hh) : floatx4{0, 0, 0, 0};
+  }
+
+  const float* kbase = a.k + (int64_t)bh * (kPacked ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
+  const float* vbase = a.v + (int64_t)bh * (kPacked ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
+  const float* brow = kBias ? a.bias + (int64_t)h * a.bias_head_stride : nullptr;
+
+  // Tile staging: 64 rows x 16 float4 for K and for V, 4 of each per thread.
+  floatx4 kr[4], vr[4];
+  float br = 0.0f;
+  auto load = [&](int key0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int idx = tid + j * kThreads;
+      const int row = idx >> 4;
+      const int c = idx & 15;
+      if (!kPacked) {
+        const int key = key0 + row;
+        const bool ok = key < a.Lk;
+        const int64_t off = (int64_t)(ok ? key : 0) * kD + 4 * c;
+        kr[j] = ok ? *reinterpret_cast<const floatx4*>(kbase + off) : floatx4{0, 0, 0, 0};
+        vr[j] = ok ? *reinterpret_cast<const floatx4*>(vbase + off) : floatx4{0, 0, 0, 0};
+      } else {
+        const int key = key0 + 4 * c;  // row = dimension
+        const bool ok = key < a.Lk;
+        const int64_t off = (int64_t)row * a.Lkp + (ok ? key : 0);
+        floatx4 kk = ok ? *reinterpret_cast<const floatx4*>(kbase + off) : floatx4{0, 0, 0, 0};
+        floatx4 vv = ok ? *reinterpret_cast<const floatx4*>(vbase + off) : floatx4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (key + e >= a.Lk) { kk[e] = 0.0f; vv[e] = 0.0f; }
+        kr[j] = kk;
+        vr[j] = vv;
+      }
+    }
+    if (kBias && tid < kBKV) {
+      const int key = key0 + tid;
+      br = key < a.Lk ? brow[key] * kLog2e : 0.0f;
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int idx = tid + j * kThreads;
+      const int row = idx >> 4;
+      const int c = idx & 15;
+      *reinterpret_cast<floatx4*>(&kbuf[buf][row * kKS + 4 * c]) = kr[j];
+      *reinterpret_cast<floatx4*>(&vbuf[buf][row * kVS + 4 * c]) = vr[j];
+    }
+    if (kBias && tid < kBKV) bbuf[buf][tid] = br;
+  };
+
+  floatx16 o[2];
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+  const float c1 = 0.125f * kLog2e;
+
+  const int ntiles = (a.Lk + kBKV - 1) / kBKV;
+  load(0);
+  store(0);
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const int key0 = t * kBKV;
+    if (t + 1 < ntiles) load(key0 + kBKV);
+    const float* kb_ = kbuf[buf];
+    const float* vb_ = vbuf[buf];
+
+    // S^T[key][query] for keys key0 + 32*kb + (8*(r/4) + 4*g + r%4).
+    floatx16 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
+#pragma unroll
+    for (int hh = 0; hh < 8; ++hh) {
+      floatx4 kf[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        if (!kPacked) {
+          kf[kb] = *reinterpret_cast<const floatx4*>(&kb_[(kb * 32 + l32) * kKS + 8 * hh + 4 * g]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) kf[kb][e] = kb_[(8 * hh + 4 * g + e) * kKS + kb * 32 + l32];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) s[kb] = mfma32x32x2(kf[kb][e], qf[hh][e], s[kb]);
+    }
+
+    // Scale (+ bias) in log2 units, mask keys past Lk, running max.
+    const bool tail = key0 + kBKV > a.Lk;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        floatx4 bb = {0, 0, 0, 0};
+        if (kBias) bb = *reinterpret_cast<const floatx4*>(&bbuf[buf][kb * 32 + 8 * r4 + 4 * g]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * r4 + e;
+          float x = kBias ? fmaf(s[kb][r], c1, bb[e]) : s[kb][r] * c1;
+          if (tail && key0 + kb * 32 + 8 * r4 + 4 * g + e >= a.Lk) x = -INFINITY;
+          s[kb][r] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+    mx = pair_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    float ls = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(s[kb][r] - m_new);
+        s[kb][r] = p;
+        ls += p;
+      }
+    l_run = fmaf(l_run, alpha, ls);
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+
+    // O^T[d][query] += V^T P^T over the 64 keys of the tile.
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh) {
+        floatx4 vf[2];
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          if (!kPacked) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              vf[db][e] = vb_[(kb * 32 + 8 * hh + 4 * g + e) * kVS + db * 32 + l32];
+          } else {
+            vf[db] = *reinterpret_cast<const floatx4*>(
+                &vb_[(db * 32 + l32) * kVS + kb * 32 + 8 * hh + 4 * g]);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int db = 0; db < 2; ++db) o[db] = mfma32x32x2(vf[db][e], s[kb][4 * hh + e], o[db]);
+      }
+
+    if (t + 1 < ntiles) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (!q_ok) return;
+  const float inv = 1.0f / pair_sum(l_run);
+  float* dst = a.out_blhd ? a.out + (((int64_t)b * a.Lq + qrow) * a.H + h) * kD
+                          : a.out + ((int64_t)bh * a.Lq + qrow) * kD;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      floatx4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = o[db][4 * r4 + e] * inv;
+      *reinterpret_cast<floatx4*>(dst + db * 32 + 8 * r4 + 4 * g) = y;
+    }
+}
+
+}  // namespace
+
+int launch_sdpa(const SdpaParams& p, hipStream_t stream) {
+  SdpaArgs a{p.q, p.k, p.v, p.bias, p.out, p.B, p.H, p.Lq, p.Lk, p.Lkp, p.bias_head_stride,
+             p.out_blhd};
+  const int64_t tiles = (int64_t)p.B * p.H * ((p.Lq + kBQ - 1) / kBQ);
+  if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
+  dim3 grid((unsigned)tiles), block(kThreads);
+  const bool bias = p.bias != nullptr;
+  if (p.kv_packed) {
+    if (bias) hipLaunchKernelGGL((sdpa_kernel<true, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((sdpa_kernel<true, false>), grid, block, 0, stream, a);
+  } else {
+    if (bias) hipLaunchKernelGGL((sdpa_kernel<false, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((sdpa_kernel<false, false>), grid, block, 0, stream, a);
+  }
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // namespace tsplat

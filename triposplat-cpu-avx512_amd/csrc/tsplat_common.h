@@ -1,0 +1,41 @@
+// Shared definitions for the gfx950 kernels of the NF24 GEMM / exact SDPA path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tsplat {
+
+// Status codes.  -1..-5 keep the meaning the reference kernels give them
+// (scripts/gemm_nf24_i16_avx512.c:171-175, native_sdpa_avx512_exact_q8t512.c:151-166);
+// -6 and -7 are the device-side failures a CPU kernel cannot have.
+enum Status : int {
+  kOk = 0,
+  kErrNull = -1,        // a required pointer is null
+  kErrDims = -2,        // bad sizes / stages / head dim
+  kErrRange = -3,       // range, stride or key-bias length mismatch
+  kErrAlign = -4,       // range not a multiple of 16 (range API)
+  kErrWorkspace = -5,   // device workspace could not be allocated
+  kErrPointer = -6,     // pointer is not device memory, or its allocation is too small
+  kErrLaunch = -7,      // HIP launch / runtime error
+};
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// One MFMA step: D(32x32) += A(32x2) * B(2x32), fp32 in, fp32 accumulate.
+// Lane l supplies A[l%32][l/32] and B[l/32][l%32]; D register r of lane l
+// holds D[8*(r/4) + 4*(l/32) + r%4][l%32].
+__device__ __forceinline__ floatx16 mfma32x32x2(float a, float b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Workgroup i of a launch is placed on XCD i % 8.  Renumber so that each XCD
+// receives one contiguous run of tile indices (neighbouring tiles share L2).
+__device__ __forceinline__ int xcd_tile_index(int id, int count) {
+  constexpr int kXcds = 8;
+  if (count % kXcds != 0) return id;
+  return (id % kXcds) * (count / kXcds) + id / kXcds;
+}
+
+}  // namespace tsplat

@@ -1,0 +1,104 @@
+"""Loader for libtsplat_hip.so (gfx950 kernels behind a C ABI).
+
+torch is imported before the library is opened so that the HIP runtime torch
+already loaded (SONAME libamdhip64.so.7) is the one the library binds to.
+There is no fallback: if the library is missing, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+DEFAULT_LIBRARY = PACKAGE_DIR / "lib" / "libtsplat_hip.so"
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+
+# name -> (argtypes, restype); the C declarations are in include/tsplat_hip.h.
+SIGNATURES = {
+    "triposplat_gemm_rnf8_avx512": ([_vp] * 10 + [_i] * 7, _i),
+    "triposplat_gemm_rnf8_avx512_range": ([_vp] * 10 + [_i] * 9, _i),
+    "triposplat_gemm_rnf8_avx512_tail": ([_vp] * 10 + [_i] * 7, _i),
+    "triposplat_gemm_rnf8_avx512_row_tile": ([], _i),
+    "triposplat_gemm_rnf8_avx512_residual_mode": ([], _i),
+    "tsplat_nf24_gemm_async": ([_vp] * 6 + [_i] * 7 + [_vp], _i),
+    "triposplat_sdpa_f32_avx512_exact_q8t512": ([_vp] * 5 + [_i] * 8, _i),
+    "triposplat_sdpa_f32": ([_vp] * 5 + [_i] * 8, _i),
+    "triposplat_sdpa_f32_avx512_exact_q8": ([_vp] * 5 + [_i] * 8, _i),
+    "triposplat_sdpa_f32_avx512_exact_q8t512_packed_blhd": ([_vp] * 5 + [_i] * 9, _i),
+    "triposplat_sdpa_key_tile": ([], _i),
+    "triposplat_sdpa_query_block": ([], _i),
+    "triposplat_sdpa_packed_output_is_blhd": ([], _i),
+    "triposplat_sdpa_q8t512_profile_reset": ([], None),
+    "triposplat_sdpa_q8t512_profile_get": ([ctypes.POINTER(ctypes.c_uint64)] * 5, _i),
+    "triposplat_sdpa_q8t512_workspace_stats": ([ctypes.POINTER(ctypes.c_uint64)] * 2, _i),
+    "triposplat_sdpa_q8t512_workspace_release": ([], None),
+    "tsplat_sdpa_async": ([_vp] * 5 + [_i] * 7 + [_i64] + [_i] * 3 + [_vp], _i),
+    "triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2": ([_vp] * 7 + [_i] * 7, _i),
+    "triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512": ([_vp] * 15 + [_i] * 10, _i),
+    "triposplat_gemm_nf24_qkv_direct_row_tile": ([], _i),
+    "triposplat_gemm_nf24_qkv_direct_residual_mode": ([], _i),
+    "tsplat_qkv_postprocess_async": ([_vp] * 7 + [_i] * 6 + [_vp], _i),
+    "tsplat_gemm_nf24_qkv_direct_async": ([_vp] * 11 + [_i] * 8 + [_vp], _i),
+    "tsplat_nf24_pack_async": ([_vp, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp], _i),
+    "tsplat_abi_version": ([], _i),
+    "tsplat_last_hip_error": ([], _i),
+    "tsplat_build_arch": ([], ctypes.c_char_p),
+}
+
+STATUS_TEXT = {
+    -1: "null pointer",
+    -2: "bad sizes / stages / head dim",
+    -3: "range, stride or key-bias length mismatch",
+    -4: "range not 16-aligned or pointer not 16-byte aligned",
+    -5: "device workspace allocation failed",
+    -6: "not device memory of the current device, or allocation too small",
+    -7: "HIP launch / runtime error",
+}
+
+_CACHE: dict[str, ctypes.CDLL] = {}
+
+
+def library_path(path: str | os.PathLike | None = None) -> Path:
+    if path is not None:
+        return Path(path).resolve()
+    env = os.environ.get("TSPLAT_HIP_LIBRARY")
+    return Path(env).resolve() if env else DEFAULT_LIBRARY
+
+
+def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Open libtsplat_hip.so once per path and set every argtypes/restype."""
+    import torch  # noqa: F401  (binds the library to torch's HIP runtime)
+
+    resolved = library_path(path)
+    key = resolved.as_posix()
+    lib = _CACHE.get(key)
+    if lib is not None:
+        return lib
+    if not resolved.is_file():
+        raise FileNotFoundError(
+            f"libtsplat_hip.so not found at {resolved}; build it with "
+            "`make -C triposplat-cpu-avx512_amd` (there is no CPU fallback)"
+        )
+    lib = ctypes.CDLL(key)
+    for name, (argtypes, restype) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+    _CACHE[key] = lib
+    return lib
+
+
+def check_status(status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what} returned status {status} ({STATUS_TEXT.get(status, 'unknown')})")
+
+
+def current_stream_handle(device) -> int:
+    """Raw hipStream_t of torch's current stream on `device`."""
+    import torch
+
+    return int(torch.cuda.current_stream(device).cuda_stream)

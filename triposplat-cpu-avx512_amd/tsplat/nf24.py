@@ -1,0 +1,146 @@
+"""NF24 weight format on the device: alphabet, packer, decode, GEMM call.
+
+Format (residual mode id 4, "nf24_i16"), as the reference defines it in
+scripts/native_linear_rnf8_avx512_patch.py:14-87 and
+scripts/native_linear_nf24_prepacked.py:17-31:
+
+    w[k, n] = fp32((int32)code01_t[k, n] * 256 + q2_t[k, n]) * scale[n]
+
+code01_t int16 [in, out] holds 4*q0 + q1, q2_t int8 [in, out], scale fp32
+[out] = max|W[n, :]| / 127 / 1024.  q0 is the nearest level of an integer
+alphabet derived from a 256-entry normal-float codebook; q1 and q2 are
+round-half-up residual digits in radix 4 and 256.
+"""
+from __future__ import annotations
+
+import math
+from statistics import NormalDist
+
+from ._lib import check_status, current_stream_handle, load_library
+
+RESIDUAL_MODE_ID = 4
+FORMAT_NAME = "nf24_i16"
+
+
+def nf8_levels():
+    """The 256 normal-float levels as Python floats (float64): the 255
+    quantiles sqrt(2)*erfinv(2p-1) at p = (i + 0.5)/255, scaled so that
+    max |level| = 1, plus a second zero, sorted
+    (scripts/native_linear_nf8_avx512_patch.py:12-20)."""
+    nd = NormalDist()
+    levels = [nd.inv_cdf((i + 0.5) / 255.0) for i in range(255)]
+    peak = max(abs(x) for x in levels)
+    levels = [x / peak for x in levels] + [0.0]
+    return sorted(levels)
+
+
+def make_nf8_codebook(torch_module):
+    """fp32 codebook tensor [256] (the reference's make_nf8_codebook)."""
+    return torch_module.tensor(nf8_levels(), dtype=torch_module.float64).float().contiguous()
+
+
+def nf24_alphabet(torch_module, device=None):
+    """unique(round(127 * codebook_f32)).clamp(-127, 127) as fp32
+    (native_linear_rnf8_avx512_patch.py:24).  Every 127*level lies at least
+    8e-3 away from a rounding tie, so float64 quantile error cannot move it."""
+    torch = torch_module
+    cb = make_nf8_codebook(torch)
+    alphabet = torch.unique(torch.round(cb * 127.0).clamp_(-127, 127)).to(torch.float32)
+    return alphabet.to(device) if device is not None else alphabet
+
+
+def quantize_nf24_i16_per_output_channel(weight, codebook=None):
+    """Pack an fp32 weight [out, in] on the GPU.
+
+    Returns ([code01_t, q2_t, q2_t], [scale, scale, scale], error) with the
+    reference's layout (native_linear_rnf8_avx512_patch.py:75-87).  The
+    packing itself runs in the tsplat_nf24_pack_async kernel; ``error``
+    reports the decoded-weight error against the source weight.
+    """
+    import torch
+
+    if weight.dtype != torch.float32 or weight.ndim != 2:
+        raise ValueError("NF24 packing requires a float32 2D weight")
+    device = weight.device if weight.device.type == "cuda" else torch.device("cuda", torch.cuda.current_device())
+    w = weight.detach().to(device).contiguous()
+    out_f, in_f = (int(s) for s in w.shape)
+    alphabet = nf24_alphabet(torch, device)
+    base = torch.empty(out_f, dtype=torch.float32, device=device)
+    code01_t = torch.empty((in_f, out_f), dtype=torch.int16, device=device)
+    q2_t = torch.empty((in_f, out_f), dtype=torch.int8, device=device)
+    scale = torch.empty(out_f, dtype=torch.float32, device=device)
+    lib = load_library()
+    with torch.cuda.device(device):
+        status = lib.tsplat_nf24_pack_async(
+            w.data_ptr(), out_f, in_f, alphabet.data_ptr(), int(alphabet.numel()), base.data_ptr(),
+            code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), current_stream_handle(device),
+        )
+    check_status(status, "tsplat_nf24_pack_async")
+    decoded = decode_nf24_i16_weight(code01_t, q2_t, scale)
+    diff = decoded - w
+    weight_rms = float(torch.sqrt(torch.mean(w * w)).item())
+    rmse = float(torch.sqrt(torch.mean(diff * diff)).item())
+    error = {
+        "weight_rmse": rmse,
+        "weight_max_abs": float(diff.abs().max().item()),
+        "weight_rms": weight_rms,
+        "weight_relative_rmse": rmse / max(weight_rms, 1.0e-30),
+        "residual_mode": FORMAT_NAME,
+        "storage_layout": "int16(q0*4+q1) + int8(q2)",
+        "nf8_derived_alphabet_size": int(alphabet.numel()),
+    }
+    return [code01_t, q2_t, q2_t], [scale, scale, scale], error
+
+
+def decode_nf24_i16_weight_t(code01_t, q2_t, scale):
+    """Exact fp32 weights in the GEMM's [in, out] layout
+    (scripts/native_linear_nf24_prepacked.py:17-31)."""
+    import torch
+
+    if code01_t.dtype != torch.int16 or q2_t.dtype != torch.int8:
+        raise ValueError("NF24 decode requires int16 code01_t and int8 q2_t")
+    if tuple(code01_t.shape) != tuple(q2_t.shape):
+        raise ValueError("NF24 code tensor shape mismatch")
+    if scale.dtype != torch.float32 or scale.ndim != 1 or scale.numel() != code01_t.shape[1]:
+        raise ValueError("NF24 scale shape mismatch")
+    combined = torch.bitwise_left_shift(code01_t.to(torch.int32), 8)
+    combined.add_(q2_t.to(torch.int32))
+    weight_t = combined.to(torch.float32)
+    weight_t.mul_(scale.reshape(1, -1))
+    return weight_t
+
+
+def decode_nf24_i16_weight(code01_t, q2_t, scale):
+    """Exact fp32 weights as a contiguous [out, in] Linear weight."""
+    return decode_nf24_i16_weight_t(code01_t, q2_t, scale).t().contiguous()
+
+
+def nf24_linear(x2, code01_t, q2_t, scale, bias, *, output_start=0, output_count=None, out=None,
+                library=None):
+    """out[M, count] = bias[start:start+count] + x2[M, K] @ W[:, start:start+count]
+    on torch's current stream.  x2 must be a contiguous fp32 GPU matrix."""
+    import torch
+
+    M, K = (int(s) for s in x2.shape)
+    N = int(code01_t.shape[1])
+    count = N - int(output_start) if output_count is None else int(output_count)
+    if out is None:
+        out = torch.empty((M, count), dtype=torch.float32, device=x2.device)
+    lib = load_library(library)
+    with torch.cuda.device(x2.device):
+        status = lib.tsplat_nf24_gemm_async(
+            x2.data_ptr(), code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), bias.data_ptr(),
+            out.data_ptr(), M, K, N, int(output_start), count, int(x2.stride(0)), int(out.stride(0)),
+            current_stream_handle(x2.device),
+        )
+    check_status(status, "tsplat_nf24_gemm_async")
+    return out
+
+
+def alphabet_tie_margin() -> float:
+    """Smallest distance of any 127*level from a rounding tie."""
+    margins = []
+    for level in nf8_levels():
+        scaled = 127.0 * level
+        margins.append(abs(scaled - math.floor(scaled) - 0.5))
+    return min(margins)

@@ -1,0 +1,70 @@
+"""QKV postprocess and the fused NF24 QKV projection on the device.
+
+Counterparts of scripts/native_qkv_postprocess_v2_avx512.c:45-105
+(``triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2``) and
+scripts/gemm_nf24_qkv_direct_avx512.c:87-199
+(``triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512``), as called by
+scripts/native_qkv_packed_attention_patch_v3.py:93-158: RoPE first, then
+RMSNorm (``y * 8 / max(||y||, 1e-12) * gamma``) on q and k; q comes back as
+[B, H, L, 64], k and v packed key-contiguous [B, H, 64, L_padded] with the
+tail tokens zero -- the layout the packed SDPA consumes.
+"""
+from __future__ import annotations
+
+from ._lib import check_status, current_stream_handle, load_library
+
+
+def padded_length(L: int) -> int:
+    return (int(L) + 15) & ~15
+
+
+def _outputs(torch, B, L, H, Lp, device):
+    q = torch.empty((B, H, L, 64), dtype=torch.float32, device=device)
+    pk = torch.empty((B, H, 64, Lp), dtype=torch.float32, device=device)
+    pv = torch.empty((B, H, 64, Lp), dtype=torch.float32, device=device)
+    return q, pk, pv
+
+
+def _check(torch, name, t):
+    if t.device.type != "cuda" or t.dtype != torch.float32 or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous fp32 GPU tensor")
+
+
+def qkv_rope_rmsnorm_pack(qkv, frequencies, q_gamma, k_gamma, B, L, H, *, L_padded=None, library=None):
+    """qkv [B*L, 3*H*64]; frequencies [fb, L, H, 64] (cos, sin pairs), fb in {1, B}."""
+    import torch
+
+    for name, t in (("qkv", qkv), ("frequencies", frequencies), ("q_gamma", q_gamma), ("k_gamma", k_gamma)):
+        _check(torch, name, t)
+    Lp = padded_length(L) if L_padded is None else int(L_padded)
+    q, pk, pv = _outputs(torch, B, L, H, Lp, qkv.device)
+    lib = load_library(library)
+    with torch.cuda.device(qkv.device):
+        status = lib.tsplat_qkv_postprocess_async(
+            qkv.data_ptr(), frequencies.data_ptr(), q_gamma.data_ptr(), k_gamma.data_ptr(),
+            q.data_ptr(), pk.data_ptr(), pv.data_ptr(), int(B), int(L), int(H), 64, Lp,
+            int(frequencies.shape[0]), current_stream_handle(qkv.device),
+        )
+    check_status(status, "tsplat_qkv_postprocess_async")
+    return q, pk, pv
+
+
+def gemm_nf24_qkv_direct(x2, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, B, L, H, *,
+                         L_padded=None, library=None):
+    """NF24 QKV projection of x2 [B*L, K] (N = 3*H*64) then the postprocess."""
+    import torch
+
+    for name, t in (("x", x2), ("frequencies", frequencies), ("q_gamma", q_gamma), ("k_gamma", k_gamma)):
+        _check(torch, name, t)
+    Lp = padded_length(L) if L_padded is None else int(L_padded)
+    q, pk, pv = _outputs(torch, B, L, H, Lp, x2.device)
+    lib = load_library(library)
+    with torch.cuda.device(x2.device):
+        status = lib.tsplat_gemm_nf24_qkv_direct_async(
+            x2.data_ptr(), code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), bias.data_ptr(),
+            frequencies.data_ptr(), q_gamma.data_ptr(), k_gamma.data_ptr(), q.data_ptr(), pk.data_ptr(),
+            pv.data_ptr(), int(B), int(L), int(x2.shape[1]), int(code01_t.shape[1]), int(H), 64, Lp,
+            int(frequencies.shape[0]), current_stream_handle(x2.device),
+        )
+    check_status(status, "tsplat_gemm_nf24_qkv_direct_async")
+    return q, pk, pv
