@@ -1,0 +1,134 @@
+"""C-ABI and host-side checks that need no GPU.
+
+* libtsplat_hip.so loads and exports every function include/tsplat_hip.h
+  declares (and the Python signature table covers exactly that set);
+* pure query symbols return the reference's values;
+* argument validation returns the reference's status codes before any
+  device call (scripts/gemm_nf24_i16_avx512.c:171-175,
+  scripts/native_sdpa_avx512_exact_q8t512.c:151-153);
+* the Python wrappers keep the reference's error behaviour, with the device
+  check flipped (CPU tensors are rejected).
+"""
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tsplat_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\(", text)
+    skip = {"if", "defined"}
+    return sorted({n for n in names if n not in skip and (n.startswith("triposplat_") or n.startswith("tsplat_"))})
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from tsplat import load_library
+
+    return load_library()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    from tsplat._lib import SIGNATURES
+
+    declared = _declared()
+    assert len(declared) >= 25
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(SIGNATURES) == set(declared)
+
+
+def test_query_symbols(lib):
+    assert lib.triposplat_gemm_rnf8_avx512_residual_mode() == 4
+    assert lib.triposplat_gemm_nf24_qkv_direct_residual_mode() == 4
+    assert lib.triposplat_gemm_rnf8_avx512_row_tile() > 0
+    assert lib.triposplat_sdpa_packed_output_is_blhd() == 1
+    assert lib.triposplat_sdpa_key_tile() == 64
+    assert lib.triposplat_sdpa_query_block() == 128
+    assert lib.tsplat_abi_version() >= 1
+    assert lib.tsplat_build_arch() == b"gfx950"
+    import ctypes
+
+    vals = [ctypes.c_uint64(7) for _ in range(5)]
+    lib.triposplat_sdpa_q8t512_profile_reset()
+    assert lib.triposplat_sdpa_q8t512_profile_get(*[ctypes.byref(v) for v in vals]) == 0
+    assert [v.value for v in vals] == [0, 0, 0, 0, 0]
+    assert lib.triposplat_sdpa_q8t512_profile_get(None, None, None, None, None) == -1
+
+
+def test_status_codes_before_any_device_call(lib):
+    """Validation order and codes of the reference; dummy non-null pointers
+    are never dereferenced because every case fails validation first."""
+    P = [0x1000 + 16 * i for i in range(10)]
+    g = lib.triposplat_gemm_rnf8_avx512_range
+    nul = list(P)
+    nul[7] = None  # codebook
+    assert g(*nul, 4, 8, 32, 0, 32, 8, 32, 1, 3) == -1
+    assert g(*P, 0, 8, 32, 0, 32, 8, 32, 1, 3) == -2        # M <= 0
+    assert g(*P, 4, 8, 32, 0, 32, 8, 32, 1, 2) == -2        # stages != 3
+    assert g(*P, 4, 8, 32, 16, 32, 8, 32, 1, 3) == -3       # start + count > N
+    assert g(*P, 4, 8, 32, 0, 32, 7, 32, 1, 3) == -3        # stride_x < K
+    assert g(*P, 4, 8, 32, 8, 16, 8, 16, 1, 3) == -4        # start % 16
+    assert lib.triposplat_gemm_rnf8_avx512(*P, 4, 8, 40, 8, 40, 1, 3) == -4   # N % 16 -> use _tail
+    assert lib.triposplat_gemm_rnf8_avx512_tail(*P, 4, 8, 40, 8, 39, 1, 3) == -2
+    s = lib.triposplat_sdpa_f32_avx512_exact_q8t512
+    assert s(None, P[1], P[2], None, P[4], 1, 2, 16, 16, 64, 0, 0, 1) == -1
+    assert s(P[0], P[1], P[2], None, P[4], 1, 2, 16, 16, 32, 0, 0, 1) == -2   # D != 64
+    assert s(P[0], P[1], P[2], None, P[4], 1, 2, 16, 16, 64, 1, 16, 1) == -3  # bias null
+    assert s(P[0], P[1], P[2], P[3], P[4], 1, 2, 16, 16, 64, 1, 15, 1) == -3  # bias len
+    pk = lib.triposplat_sdpa_f32_avx512_exact_q8t512_packed_blhd
+    assert pk(P[0], P[1], P[2], None, P[4], 1, 2, 16, 20, 64, 24, 0, 0, 1) == -2  # Lkp % 16
+    assert pk(P[0], P[1], P[2], None, P[4], 1, 2, 16, 20, 64, 16, 0, 0, 1) == -2  # Lkp < Lk
+    post = lib.triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2
+    assert post(*P[:7], 1, 20, 2, 64, 24, 1, 1) == -2      # L_padded % 16
+    assert post(*P[:7], 2, 20, 2, 64, 32, 3, 1) == -2      # frequency_batches
+    d = lib.triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512
+    assert d(*(P + P[:5]), 1, 20, 128, 384, 2, 64, 32, 1, 1, 2) == -2   # stages
+    assert d(*(P + P[:5]), 1, 20, 128, 380, 2, 64, 32, 1, 1, 3) == -2   # N != 3*H*64
+
+
+def test_wrappers_reject_cpu_tensors():
+    import torch
+    from tsplat.native_sdpa_ctypes import native_sdpa_f32, native_sdpa_f32_ex
+
+    q = torch.zeros(1, 2, 16, 64)
+    with pytest.raises(ValueError, match="GPU-only"):
+        native_sdpa_f32(q, q, q)
+    with pytest.raises(ValueError, match="GPU"):
+        native_sdpa_f32_ex(q, q, q)
+
+
+def test_patch_rejects_other_residual_modes():
+    """Asking for a mode the library does not implement raises the
+    reference's mismatch error (native_linear_rnf8_avx512_patch.py:196-200)."""
+    import torch.nn as nn
+    from tsplat.native_linear_rnf8_patch import apply_triposplat_native_rnf8_avx512_patch as patch
+
+    m = nn.Sequential(nn.Linear(8, 16))
+    assert patch(m, enabled=False) == {"enabled": False}
+    with pytest.raises(ValueError):
+        patch(m, enabled=True, strict=False)
+    with pytest.raises(ValueError):
+        patch(m, enabled=True, residual_mode="nf24_i16", stages=2)
+    with pytest.raises(RuntimeError, match="mismatch"):
+        patch(m, enabled=True, residual_mode="nf8", stages=2)
+
+
+def test_nf8_codebook_matches_closed_form():
+    import torch
+    from tsplat.nf24 import make_nf8_codebook, nf8_levels
+
+    cb = make_nf8_codebook(torch).numpy()
+    assert cb.shape == (256,) and cb.dtype == np.float32
+    assert cb[0] == -1.0 and cb[-1] == 1.0 and np.count_nonzero(cb == 0.0) == 2
+    assert np.all(np.diff(cb) >= 0)
+    lv = np.array(nf8_levels())
+    assert np.allclose(lv, -lv[::-1], atol=1e-15)
