@@ -127,23 +127,104 @@ def cpu_baseline_sdpa(q, k, v, budget_s=12.0):
     }
 
 
+def sdpa_inputs(torch, dev):
+    import numpy as np
+
+    B, H, L, D = 1, 16, 16384, 64
+    q_h = rope_rmsnorm_host(np.random.default_rng(10).standard_normal((B, H, L, D), dtype=np.float32))
+    k_h = rope_rmsnorm_host(np.random.default_rng(11).standard_normal((B, H, L, D), dtype=np.float32))
+    v_h = np.random.default_rng(12).standard_normal((B, H, L, D), dtype=np.float32)
+    return q_h, k_h, v_h
+
+
+def run_sdpa(torch, dev, steps, warmup, host):
+    """one exact SDPA call per step; returns (wall s/step, kernel ms)."""
+    from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
+
+    q_h, k_h, v_h = host
+    B, H, L, D = q_h.shape
+    q = torch.from_numpy(q_h).to(dev)
+    k = torch.from_numpy(k_h).to(dev)
+    v = torch.from_numpy(v_h).to(dev)
+    out = torch.empty((B, L, H, D), dtype=torch.float32, device=dev)
+
+    def step():
+        native_sdpa_f32_ex(q, k, v, out=out, out_layout="blhd")
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    kernel_ms = time_events(torch, step, max(3, steps))
+    assert torch.isfinite(out).all().item()
+    return wall, kernel_ms
+
+
+def run_gemm(torch, dev, iters):
+    """NF24 Linear 4096x1024 @ 1024x3072 (+ bias)."""
+    import numpy as np
+    from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
+
+    M, K, N = 4096, 1024, 3072
+    x = torch.from_numpy(np.random.default_rng(0).standard_normal((M, K), dtype=np.float32)).to(dev)
+    w = torch.from_numpy((np.random.default_rng(1).standard_normal((N, K), dtype=np.float32)
+                          * np.float32(0.02)).astype(np.float32)).to(dev)
+    bias = torch.from_numpy((np.random.default_rng(2).standard_normal(N, dtype=np.float32)
+                             * np.float32(0.01)).astype(np.float32)).to(dev)
+    codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+    gout = torch.empty((M, N), dtype=torch.float32, device=dev)
+
+    def step():
+        nf24_linear(x, codes[0], codes[1], scales[0], bias, out=gout)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    g_ms = time_events(torch, step, iters)
+    g_flop = 2.0 * M * N * K
+    g_tf = g_flop / (g_ms * 1e-3) / 1e12
+    return {
+        "workload": "configs[0] NF24 Linear X[4096x1024] @ W[1024x3072] + bias, fp32 MFMA accumulate",
+        "ms": g_ms,
+        "tflops": g_tf,
+        "frac_fp32_mfma_peak": g_tf / PEAK_FP32_MFMA,
+        "algorithmic_bytes": float(M * K * 4 + K * N * 3 + N * 8 + M * N * 4),
+        "traffic": load_traffic("nf24_gemm_config0"),
+    }
+
+
+def run_copy(torch, dev, iters):
+    """Calibration kernel for the HBM counters: a plain 256 MiB device copy."""
+    n = 64 << 20
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ms = time_events(torch, lambda: dst.copy_(src), iters)
+    return {"bytes_read": n * 4, "bytes_written": n * 4, "ms": ms, "GBps": 2 * n * 4 / (ms * 1e-3) / 1e9}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--only", choices=("sdpa", "gemm", "copy"), default=None,
+                    help="run one workload alone (for profiler runs) and print its figures")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                           "(multi-GPU sharding is a design note, not implemented)"}))
         return 2
 
-    import numpy as np
     import torch
     from tsplat import load_library
-    from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -152,67 +233,24 @@ def main():
     torch.cuda.set_device(dev)
     load_library()
 
-    # ---------------- exact SDPA, L = 16384 ----------------
-    B, H, L, D = 1, 16, 16384, 64
-    q_h = rope_rmsnorm_host(np.random.default_rng(10).standard_normal((B, H, L, D), dtype=np.float32))
-    k_h = rope_rmsnorm_host(np.random.default_rng(11).standard_normal((B, H, L, D), dtype=np.float32))
-    v_h = np.random.default_rng(12).standard_normal((B, H, L, D), dtype=np.float32)
-    q = torch.from_numpy(q_h).to(dev)
-    k = torch.from_numpy(k_h).to(dev)
-    v = torch.from_numpy(v_h).to(dev)
-    out = torch.empty((B, L, H, D), dtype=torch.float32, device=dev)
+    if args.only == "gemm":
+        print(json.dumps(run_gemm(torch, dev, max(3, args.steps))))
+        return 0
+    if args.only == "copy":
+        print(json.dumps(run_copy(torch, dev, max(3, args.steps))))
+        return 0
 
-    def sdpa_step():
-        native_sdpa_f32_ex(q, k, v, out=out, out_layout="blhd")
-
-    for _ in range(args.warmup):
-        sdpa_step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        sdpa_step()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / args.steps
+    host = sdpa_inputs(torch, dev)
+    B, H, L, D = host[0].shape
+    wall, kernel_ms = run_sdpa(torch, dev, args.steps, args.warmup, host)
     sdpa_flop = 4.0 * B * H * L * L * D
-    kernel_ms = time_events(torch, sdpa_step, max(3, args.steps))
     achieved = sdpa_flop / (kernel_ms * 1e-3) / 1e12
-    assert torch.isfinite(out).all().item()
+    if args.only == "sdpa":
+        print(json.dumps({"sdpa_ms": kernel_ms, "tflops": achieved}))
+        return 0
 
-    # ---------------- NF24 GEMM 4096x1024x3072 -------------
-    gemm = None
-    if not args.no_gemm:
-        from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
-
-        M, K, N = 4096, 1024, 3072
-        x = torch.from_numpy(np.random.default_rng(0).standard_normal((M, K), dtype=np.float32)).to(dev)
-        w = torch.from_numpy((np.random.default_rng(1).standard_normal((N, K), dtype=np.float32)
-                              * np.float32(0.02)).astype(np.float32)).to(dev)
-        bias = torch.from_numpy((np.random.default_rng(2).standard_normal(N, dtype=np.float32)
-                                 * np.float32(0.01)).astype(np.float32)).to(dev)
-        codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
-        gout = torch.empty((M, N), dtype=torch.float32, device=dev)
-
-        def gemm_step():
-            nf24_linear(x, codes[0], codes[1], scales[0], bias, out=gout)
-
-        for _ in range(3):
-            gemm_step()
-        torch.cuda.synchronize()
-        g_ms = time_events(torch, gemm_step, 20)
-        g_flop = 2.0 * M * N * K
-        g_tf = g_flop / (g_ms * 1e-3) / 1e12
-        gemm = {
-            "workload": "configs[0] NF24 Linear X[4096x1024] @ W[1024x3072] + bias, fp32 MFMA accumulate",
-            "ms": g_ms,
-            "tflops": g_tf,
-            "frac_fp32_mfma_peak": g_tf / PEAK_FP32_MFMA,
-            "algorithmic_bytes": float(M * K * 4 + K * N * 3 + N * 8 + M * N * 4),
-            "traffic": load_traffic("nf24_gemm_config1"),
-        }
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline_sdpa(q_h, k_h, v_h)
+    gemm = run_gemm(torch, dev, 20)
+    cpu = None if args.no_cpu_baseline else cpu_baseline_sdpa(*host)
 
     line = {
         "metric": METRIC,
@@ -237,7 +275,7 @@ def main():
             "peak": PEAK_FP32_MFMA,
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_FP32_MFMA,
-            "traffic": load_traffic("sdpa_config2"),
+            "traffic": load_traffic("sdpa_config1"),
             "kernel_ms": kernel_ms,
             "flop_per_launch": sdpa_flop,
         },
