@@ -197,6 +197,93 @@ def run_gemm(torch, dev, iters):
     }
 
 
+def flow_inputs(cfg):
+    import numpy as np
+
+    z = np.random.default_rng(20).standard_normal((cfg.latent_tokens, cfg.hidden), dtype=np.float32)
+    c = np.random.default_rng(21).standard_normal((cfg.cond_tokens, cfg.hidden), dtype=np.float32)
+    return z, c
+
+
+def run_flow(torch, dev, steps, with_cpu, validate):
+    """configs[3] (one block, one branch) and configs[4] (28 blocks, CFG pair,
+    one Euler step) of the frozen synthetic flow graph (tsplat/flow.py)."""
+    import numpy as np
+    from tsplat.flow import FlowConfig, FlowModel
+
+    cfg = FlowConfig()
+    C, L, Lc = cfg.hidden, cfg.latent_tokens, cfg.cond_tokens
+    t0 = time.perf_counter()
+    model = FlowModel(cfg, dev)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t0
+    z_h, c_h = flow_inputs(cfg)
+    z = torch.from_numpy(z_h).to(dev)
+    c = torch.from_numpy(c_h).to(dev)
+
+    # configs[3]: one block on one branch, t_mod from the step-0 timestep
+    t_emb, t_mod = model.timestep(torch.full((1,), 1000.0, device=dev))
+    x1, c1 = z[None].contiguous(), c[None].contiguous()
+    for _ in range(2):
+        model.block_forward(model.blocks[0], x1, c1, t_mod)
+    torch.cuda.synchronize()
+    blk_ms = time_events(torch, lambda: model.block_forward(model.blocks[0], x1, c1, t_mod), 5)
+    per_branch_flop = 2.0 * L * C * (3 * C + C + C + C + 4 * C + 4 * C) + 2.0 * Lc * C * 2 * C \
+        + 4.0 * cfg.heads * L * L * 64 + 4.0 * cfg.heads * L * Lc * 64
+
+    # configs[4]: one CFG Euler step over all 28 blocks
+    for _ in range(1):
+        model.euler_cfg_step(z, c)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(max(1, steps)):
+        t0 = time.perf_counter()
+        zn, v = model.euler_cfg_step(z, c)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    step_s = sorted(times)[len(times) // 2]
+    step_flop = 2 * cfg.blocks * per_branch_flop
+    out = {
+        "config3_block": {"workload": "configs[3] one flow block, L=16384 latent + 2048 condition tokens, one branch",
+                          "ms": blk_ms, "tflops": per_branch_flop / (blk_ms * 1e-3) / 1e12},
+        "config4_step": {"workload": "configs[4] 28 blocks, CFG batch 2, one Euler step (guidance 3, shift 3)",
+                         "s_per_denoise_step": step_s, "tflops": step_flop / step_s / 1e12,
+                         "model_setup_s": setup_s, "finite": bool(torch.isfinite(zn).all().item())},
+    }
+    if with_cpu or validate:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+        from flow_ref import CpuFlow, combined_rmse
+
+        threads = len(os.sched_getaffinity(0))
+        backend = "reference" if O.ref_available() else "oracle"
+        params = model.host()
+        cpu = CpuFlow(params, cfg, backend=backend, threads=threads)
+        if with_cpu:
+            # bounded sample: one block on both CFG branches, timed once after a warmup
+            ts = cpu.schedule()
+            t_h = np.full(2, ts[0] * 1000.0, np.float32)
+            _, tm = cpu.timestep(t_h)
+            xx, cc = np.stack((z_h, z_h)), np.stack((c_h, np.zeros_like(c_h)))
+            cpu.block(params["blocks"][0], xx[:, :256], cc, tm)
+            t0 = time.perf_counter()
+            cpu.block(params["blocks"][0], xx, cc, tm)
+            blk_cpu = time.perf_counter() - t0
+            est = blk_cpu * cfg.blocks
+            out["config4_step"]["cpu_baseline"] = {
+                "kind": "reference" if backend == "reference" else "port", "cores": threads,
+                "sample": "one full-size block on both CFG branches (reference AVX-512 NF24 GEMM, "
+                          "QKV-direct and SDPA kernels + NumPy elementwise), x 28 blocks",
+                "block_s": blk_cpu, "s_per_denoise_step_estimated": est,
+                "speedup_gpu_vs_cpu": est / step_s,
+            }
+        if validate:
+            zc, vc = cpu.euler_cfg_step(z_h, c_h)
+            out["config4_step"]["latent_rmse_vs_cpu"] = combined_rmse(zn.cpu().numpy(), zc)
+            out["config4_step"]["velocity_rmse_vs_cpu"] = combined_rmse(v.cpu().numpy(), vc)
+    return out
+
+
 def run_copy(torch, dev, iters):
     """Calibration kernel for the HBM counters: a plain 256 MiB device copy."""
     n = 64 << 20
@@ -215,8 +302,11 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=("sdpa", "gemm", "copy"), default=None,
+    ap.add_argument("--only", choices=("sdpa", "gemm", "copy", "flow"), default=None,
                     help="run one workload alone (for profiler runs) and print its figures")
+    ap.add_argument("--no-flow", action="store_true", help="skip configs[3]/[4] (flow block / step)")
+    ap.add_argument("--validate-flow", action="store_true",
+                    help="also run the full CPU step and report latent RMSE (minutes of CPU time)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -239,6 +329,9 @@ def main():
     if args.only == "copy":
         print(json.dumps(run_copy(torch, dev, max(3, args.steps))))
         return 0
+    if args.only == "flow":
+        print(json.dumps(run_flow(torch, dev, 3, not args.no_cpu_baseline, args.validate_flow)))
+        return 0
 
     host = sdpa_inputs(torch, dev)
     B, H, L, D = host[0].shape
@@ -250,6 +343,7 @@ def main():
         return 0
 
     gemm = run_gemm(torch, dev, 20)
+    flow = None if args.no_flow else run_flow(torch, dev, 3, not args.no_cpu_baseline, args.validate_flow)
     cpu = None if args.no_cpu_baseline else cpu_baseline_sdpa(*host)
 
     line = {
@@ -281,6 +375,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "gemm_config0": gemm,
+        "flow": flow,
     }
     print(json.dumps(line))
     return 0

@@ -1,0 +1,155 @@
+"""CPU fp32 restatement of the synthetic flow model (BASELINE configs 4/5).
+
+TEST INFRASTRUCTURE ONLY (tests/ and bench.py's cpu_baseline leg).  The graph
+is the one frozen in triposplat-cpu-avx512_amd/tsplat/flow.py; here every
+NF24 Linear, the fused QKV projection and both SDPAs run through the CPU
+kernels -- the oracle restatement (`backend="oracle"`) or the reference's
+own AVX-512 build in oracle/_ref (`backend="reference"`) -- and the
+elementwise work is NumPy float32.  Parameters come from FlowModel.host(),
+so both sides use bit-identical packed weights.
+
+Model-level parity is "unpinned at the upstream boundary": the upstream
+TripoSplat model is absent; this restatement is checked against the device
+graph, not against the real model.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+import oracle as O
+
+
+class CpuFlow:
+    def __init__(self, params, cfg, backend="oracle", threads=0):
+        self.p = params
+        self.cfg = cfg
+        self.backend = backend
+        self.threads = threads
+        if backend == "reference" and not O.ref_available():
+            raise RuntimeError("oracle/_ref not built")
+
+    # ---------------------------------------------------------- kernels
+    def linear(self, x2, lin):
+        x2 = np.ascontiguousarray(x2, np.float32)
+        if self.backend == "reference" and lin["code01_t"].shape[1] % 16 == 0:
+            return O.ref_nf24_gemm(x2, lin["code01_t"], lin["q2_t"], lin["scale"], lin["bias"], self.threads)
+        return O.nf24_gemm(x2, lin["code01_t"], lin["q2_t"], lin["scale"], lin["bias"])
+
+    def qkv_direct(self, x2, lin, freqs, qg, kg, B, L, H):
+        if self.backend == "reference":
+            return O.ref_gemm_nf24_qkv_direct(x2, lin["code01_t"], lin["q2_t"], lin["scale"], lin["bias"],
+                                              freqs, qg, kg, B, L, H, self.threads)
+        return O.gemm_nf24_qkv_direct(x2, lin["code01_t"], lin["q2_t"], lin["scale"], lin["bias"],
+                                      freqs, qg, kg, B, L, H)
+
+    def sdpa_packed_blhd(self, q, pk, pv, Lk):
+        if self.backend == "reference":
+            return O.ref_sdpa_packed_blhd(q, pk, pv, Lk, None, self.threads)
+        return O.sdpa_q8t512_packed_blhd(q, pk, pv, Lk)
+
+    def sdpa_bhld(self, q, k, v):
+        if self.backend == "reference":
+            return O.ref_sdpa_q8t512(q, k, v, None, self.threads)
+        return O.sdpa_q8t512(q, k, v)
+
+    # ---------------------------------------------------------- elementwise
+    @staticmethod
+    def layer_norm(x, eps, w=None, b=None):
+        x = x.astype(np.float32)
+        mean = x.mean(axis=-1, keepdims=True, dtype=np.float32)
+        d = x - mean
+        var = (d * d).mean(axis=-1, keepdims=True, dtype=np.float32)
+        y = d / np.sqrt(var + np.float32(eps))
+        if w is not None:
+            y = y * w + b
+        return y.astype(np.float32)
+
+    @staticmethod
+    def gelu_tanh(x):
+        c = np.float32(math.sqrt(2.0 / math.pi))
+        return (np.float32(0.5) * x * (np.float32(1.0) + np.tanh(c * (x + np.float32(0.044715) * x * x * x)))).astype(np.float32)
+
+    @staticmethod
+    def silu(x):
+        return (x / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
+
+    @staticmethod
+    def head_rmsnorm(y, gamma):
+        n = np.maximum(np.sqrt((y.astype(np.float64) ** 2).sum(-1, keepdims=True)), 1e-12).astype(np.float32)
+        return (y * (np.float32(8.0) / n) * gamma).astype(np.float32)
+
+    def freqs(self, L):
+        H = self.cfg.heads
+        i = np.arange(32, dtype=np.float64)
+        ang = np.arange(L, dtype=np.float64)[:, None] * self.cfg.rope_theta ** (-2.0 * i / 64.0)[None, :]
+        f = np.stack((np.cos(ang), np.sin(ang)), -1).reshape(L, 64).astype(np.float32)
+        return np.ascontiguousarray(np.broadcast_to(f[None, :, None, :], (1, L, H, 64)))
+
+    def timestep(self, t):
+        half = self.cfg.freq_dim // 2
+        freqs = np.exp(-math.log(10000.0) * np.arange(half, dtype=np.float32) / np.float32(half)).astype(np.float32)
+        args = (np.asarray(t, np.float32)[:, None] * freqs[None, :]).astype(np.float32)
+        emb = np.concatenate((np.cos(args), np.sin(args)), -1).astype(np.float32)
+        t_emb = self.linear(self.silu(self.linear(emb, self.p["t_fc1"])), self.p["t_fc2"])
+        t_mod = self.linear(self.silu(t_emb), self.p["adaln"])
+        return t_emb, t_mod
+
+    # ---------------------------------------------------------- graph
+    def block(self, bp, x, cond, t_mod):
+        cfg = self.cfg
+        B, L, C = x.shape
+        Lc = cond.shape[1]
+        H = cfg.heads
+        mod = (t_mod + bp["shift_table"])[:, None, :]
+        sm, cm, gm, s2, c2, g2 = np.split(mod, 6, axis=-1)
+        h = (self.layer_norm(x, cfg.ln_eps) * (np.float32(1) + cm) + sm).astype(np.float32)
+        q, pk, pv = self.qkv_direct(h.reshape(B * L, C), bp["qkv"], self.freqs(L), bp["q_gamma"],
+                                    bp["k_gamma"], B, L, H)
+        a = self.sdpa_packed_blhd(q, pk, pv, L).reshape(B * L, C)
+        x = (x + gm * self.linear(a, bp["out"]).reshape(B, L, C)).astype(np.float32)
+        h = self.layer_norm(x, cfg.ln_eps, bp["xnorm_w"], bp["xnorm_b"])
+        xq = self.head_rmsnorm(self.linear(h.reshape(B * L, C), bp["xq"]).reshape(B, L, H, 64), bp["xq_gamma"])
+        kv = self.linear(cond.reshape(B * Lc, C), bp["xkv"]).reshape(B, Lc, 2, H, 64)
+        xk = self.head_rmsnorm(kv[:, :, 0], bp["xk_gamma"])
+        xv = kv[:, :, 1]
+        a = self.sdpa_bhld(np.ascontiguousarray(xq.transpose(0, 2, 1, 3)), np.ascontiguousarray(xk.transpose(0, 2, 1, 3)),
+                           np.ascontiguousarray(xv.transpose(0, 2, 1, 3)))
+        a = np.ascontiguousarray(a.transpose(0, 2, 1, 3)).reshape(B * L, C)
+        x = (x + self.linear(a, bp["xout"]).reshape(B, L, C)).astype(np.float32)
+        h = (self.layer_norm(x, cfg.ln_eps) * (np.float32(1) + c2) + s2).astype(np.float32)
+        h = self.gelu_tanh(self.linear(h.reshape(B * L, C), bp["fc1"]))
+        h = self.linear(h, bp["fc2"]).reshape(B, L, C)
+        return (x + g2 * h).astype(np.float32)
+
+    def velocity(self, z, cond, t):
+        B, L, C = z.shape
+        t_emb, t_mod = self.timestep(t)
+        x = self.linear(z.reshape(B * L, C), self.p["input_layer"]).reshape(B, L, C)
+        for bp in self.p["blocks"]:
+            x = self.block(bp, x, cond, t_mod)
+        fs = self.p["final_shift_table"][None] + t_emb[:, None, :]
+        shift, scale = fs[:, 0], fs[:, 1]
+        h = (self.layer_norm(x, self.cfg.final_ln_eps) * (np.float32(1) + scale[:, None]) + shift[:, None]).astype(np.float32)
+        return self.linear(h.reshape(B * L, C), self.p["out_layer"]).reshape(B, L, C)
+
+    def schedule(self):
+        s = self.cfg.shift
+        u = np.linspace(1.0, 0.0, self.cfg.steps + 1, dtype=np.float64)
+        return s * u / (1.0 + (s - 1.0) * u)
+
+    def euler_cfg_step(self, z, cond, step=0):
+        ts = self.schedule()
+        t = np.full(2, ts[step] * 1000.0, np.float32)
+        dt = np.float32(ts[step] - ts[step + 1])
+        v = self.velocity(np.stack((z, z)), np.stack((cond, np.zeros_like(cond))), t)
+        g = np.float32(self.cfg.guidance)
+        v_cfg = (g * v[0] - (g - np.float32(1)) * v[1]).astype(np.float32)
+        return (z - dt * v_cfg).astype(np.float32), v_cfg
+
+
+def combined_rmse(a, b):
+    """RMSE as scripts/compare_latent_npz.py:22-48 reports it (float64)."""
+    d = np.asarray(a, np.float64) - np.asarray(b, np.float64)
+    return float(np.sqrt(np.mean(d * d)))

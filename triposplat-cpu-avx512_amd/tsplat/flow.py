@@ -1,0 +1,258 @@
+"""Synthetic flow transformer (BASELINE configs 4 and 5) on the device.
+
+The upstream TripoSplat model is not available offline, so this module
+freezes a graph with the block structure of the reference's unified block
+(scripts/triposplat_attention_patch.py:4978-5033: shift-table modulation,
+LN -> modulate -> attention -> gated residual -> LN -> modulate -> MLP ->
+gated residual; attention as in :4323-4437, RoPE before q/k RMSNorm) and the
+literal layer list of config 4: NF24 QKV + self SDPA + NF24 out, cross
+attention (NF24 q on the latent, NF24 kv on the condition tokens, NF24 out),
+NF24 MLP fc1 / GELU(tanh) / fc2.  Every Linear is an NF24 packed weight run
+by the gfx950 GEMM; self attention uses the fused NF24 QKV projection +
+RoPE/RMSNorm/pack and the packed exact SDPA; elementwise work (LayerNorm,
+modulation, GELU, residuals, cross q/k RMSNorm) is torch on the device.
+
+Frozen choices (not pinned by the reference; recorded here and in DESIGN):
+  * LayerNorm eps 1e-6; norm1/norm3 without affine, the cross-attention
+    norm with affine weight/bias; the final LayerNorm eps 1e-5
+    (attention_patch.py:59);
+  * cross attention has no RoPE; q and k get the per-head RMSNorm
+    y * 8 / max(||y||, 1e-12) * gamma;
+  * RoPE: interleaved (cos, sin) pairs, position = latent token index,
+    freq_i = theta^(-2i/64), theta = 10000;
+  * timestep: t * 1000 -> sinusoidal [cos | sin] (256) -> NF24 Linear
+    256->C -> SiLU -> NF24 Linear C->C = t_emb; shared modulation
+    t_mod = NF24 Linear(SiLU(t_emb)) [6C]; block mod = t_mod + shift_table;
+  * input layer NF24 C->C on the latent; output: final LN, modulation with
+    (shift_table_final + t_emb), NF24 C->C = velocity;
+  * CFG pair (condition, zero condition) in one batch of 2; guidance 3,
+    schedule t_i = s*u/(1 + (s-1)*u), u = linspace(1, 0, steps+1), s = 3
+    (scripts/triposplat_quantized_sampler.py:398-414); v = g*v_c - (g-1)*v_u,
+    x -= dt * v (scripts/native_sampler_avx512.c:41-49, 78-84).
+Weights: W ~ N(0, 0.02), bias ~ N(0, 0.01), gammas 1 + N(0, 0.05), shift
+tables N(0, 0.02); Linear i uses torch seed 1000 + i.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+from .native_sdpa_ctypes import native_sdpa_f32_ex
+from .nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
+from .qkv import gemm_nf24_qkv_direct
+
+
+@dataclass(frozen=True)
+class FlowConfig:
+    hidden: int = 1024
+    heads: int = 16
+    head_dim: int = 64
+    mlp_ratio: int = 4
+    blocks: int = 28
+    latent_tokens: int = 16384
+    cond_tokens: int = 2048
+    freq_dim: int = 256
+    ln_eps: float = 1e-6
+    final_ln_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    guidance: float = 3.0
+    shift: float = 3.0
+    steps: int = 20
+
+    def __post_init__(self):
+        if self.hidden != self.heads * self.head_dim or self.head_dim != 64:
+            raise ValueError("hidden must be heads * 64")
+
+
+# Linear layout: name -> (in, out) per block, in this order.
+BLOCK_LINEARS = (("qkv", 1, 3), ("out", 1, 1), ("xq", 1, 1), ("xkv", 1, 2), ("xout", 1, 1),
+                 ("fc1", 1, 4), ("fc2", 4, 1))
+
+
+class PackedLinear:
+    """An NF24-packed Linear on the device (code01_t, q2_t, scale, bias)."""
+
+    def __init__(self, code01_t, q2_t, scale, bias):
+        self.code01_t, self.q2_t, self.scale, self.bias = code01_t, q2_t, scale, bias
+        self.in_features = int(code01_t.shape[0])
+        self.out_features = int(code01_t.shape[1])
+
+    @classmethod
+    def random(cls, torch, in_f, out_f, seed, device):
+        g = torch.Generator(device=device).manual_seed(int(seed))
+        w = torch.randn((out_f, in_f), generator=g, device=device, dtype=torch.float32) * 0.02
+        b = torch.randn((out_f,), generator=g, device=device, dtype=torch.float32) * 0.01
+        codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+        return cls(codes[0], codes[1], scales[0], b)
+
+    def __call__(self, x2, out=None):
+        return nf24_linear(x2, self.code01_t, self.q2_t, self.scale, self.bias, out=out)
+
+    def host(self):
+        return {k: getattr(self, k).cpu().numpy() for k in ("code01_t", "q2_t", "scale", "bias")}
+
+
+def _randn(torch, shape, seed, device, std, mean=0.0):
+    g = torch.Generator(device=device).manual_seed(int(seed))
+    return torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std + mean
+
+
+class FlowBlock:
+    def __init__(self, torch, cfg: FlowConfig, index: int, device, seed_base: int):
+        C = cfg.hidden
+        self.cfg = cfg
+        self.lin = {}
+        for j, (name, a, b) in enumerate(BLOCK_LINEARS):
+            self.lin[name] = PackedLinear.random(torch, a * C, b * C, seed_base + j, device)
+        s = 50000 + 16 * index
+        H = cfg.heads
+        self.shift_table = _randn(torch, (6 * C,), s, device, 0.02)
+        self.q_gamma = _randn(torch, (H, 64), s + 1, device, 0.05, 1.0)
+        self.k_gamma = _randn(torch, (H, 64), s + 2, device, 0.05, 1.0)
+        self.xq_gamma = _randn(torch, (H, 64), s + 3, device, 0.05, 1.0)
+        self.xk_gamma = _randn(torch, (H, 64), s + 4, device, 0.05, 1.0)
+        self.xnorm_w = _randn(torch, (C,), s + 5, device, 0.05, 1.0)
+        self.xnorm_b = _randn(torch, (C,), s + 6, device, 0.02)
+
+    def host(self):
+        out = {name: lin.host() for name, lin in self.lin.items()}
+        for k in ("shift_table", "q_gamma", "k_gamma", "xq_gamma", "xk_gamma", "xnorm_w", "xnorm_b"):
+            out[k] = getattr(self, k).cpu().numpy()
+        return out
+
+
+def head_rmsnorm(torch, y, gamma):
+    """[..., H, 64]: y * 8 / max(||y||, 1e-12) * gamma[h]."""
+    n = torch.linalg.vector_norm(y, dim=-1, keepdim=True).clamp_min(1e-12)
+    return y * (8.0 / n) * gamma
+
+
+def rope_frequencies(torch, L, H, theta, device):
+    """[1, L, H, 64] interleaved (cos, sin) of position * theta^(-2i/64)."""
+    i = torch.arange(32, dtype=torch.float64, device=device)
+    pos = torch.arange(L, dtype=torch.float64, device=device)
+    ang = pos[:, None] * theta ** (-2.0 * i / 64.0)[None, :]
+    f = torch.stack((torch.cos(ang), torch.sin(ang)), dim=-1).reshape(L, 64).to(torch.float32)
+    return f[None, :, None, :].expand(1, L, H, 64).contiguous()
+
+
+def timestep_embedding(torch, t, dim, device):
+    """[cos | sin] of t * exp(-ln(1e4) * i / half), i < half (the reference's
+    triposplat_timestep_embedding_f32_avx512 layout: cos first)."""
+    half = dim // 2
+    freqs = torch.exp(-math.log(10000.0) * torch.arange(half, dtype=torch.float32, device=device) / half)
+    args = t.to(torch.float32)[:, None] * freqs[None, :]
+    return torch.cat((torch.cos(args), torch.sin(args)), dim=-1)
+
+
+class FlowModel:
+    """The frozen synthetic flow model; forward() is one CFG-paired velocity."""
+
+    def __init__(self, cfg: FlowConfig, device, blocks: int | None = None):
+        import torch
+
+        self.torch = torch
+        self.cfg = cfg
+        self.device = device
+        C = cfg.hidden
+        nb = cfg.blocks if blocks is None else blocks
+        self.t_fc1 = PackedLinear.random(torch, cfg.freq_dim, C, 1000, device)
+        self.t_fc2 = PackedLinear.random(torch, C, C, 1001, device)
+        self.adaln = PackedLinear.random(torch, C, 6 * C, 1002, device)
+        self.input_layer = PackedLinear.random(torch, C, C, 1003, device)
+        self.out_layer = PackedLinear.random(torch, C, C, 1004, device)
+        self.final_shift_table = _randn(torch, (2, C), 49999, device, 0.02)
+        self.blocks = [FlowBlock(torch, cfg, i, device, 1010 + 10 * i) for i in range(nb)]
+        self._freqs = {}
+
+    def freqs(self, L):
+        if L not in self._freqs:
+            self._freqs[L] = rope_frequencies(self.torch, L, self.cfg.heads, self.cfg.rope_theta, self.device)
+        return self._freqs[L]
+
+    # -------------------------------------------------------------- pieces
+    def timestep(self, t):
+        torch = self.torch
+        F = torch.nn.functional
+        emb = timestep_embedding(torch, t, self.cfg.freq_dim, self.device).contiguous()
+        t_emb = self.t_fc2(F.silu(self.t_fc1(emb)).contiguous())
+        t_mod = self.adaln(F.silu(t_emb).contiguous())
+        return t_emb, t_mod
+
+    def block_forward(self, blk: FlowBlock, x, cond, t_mod):
+        """x [B, L, C], cond [B, Lc, C], t_mod [B, 6C] -> x (new tensor)."""
+        torch = self.torch
+        F = torch.nn.functional
+        cfg = self.cfg
+        B, L, C = (int(s) for s in x.shape)
+        Lc = int(cond.shape[1])
+        H = cfg.heads
+        mod = (t_mod + blk.shift_table).unsqueeze(1)  # [B, 1, 6C]
+        shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = mod.chunk(6, dim=-1)
+
+        # self attention: fused NF24 QKV + RoPE/RMSNorm/pack, packed exact SDPA, NF24 out
+        h = F.layer_norm(x, (C,), eps=cfg.ln_eps) * (1 + scale_msa) + shift_msa
+        lin = blk.lin
+        q, pk, pv = gemm_nf24_qkv_direct(h.reshape(B * L, C), lin["qkv"].code01_t, lin["qkv"].q2_t,
+                                         lin["qkv"].scale, lin["qkv"].bias, self.freqs(L),
+                                         blk.q_gamma, blk.k_gamma, B, L, H)
+        a = native_sdpa_f32_ex(q, pk, pv, kv_packed=True, key_count=L, out_layout="blhd")
+        a = lin["out"](a.view(B * L, C)).view(B, L, C)
+        x = x + gate_msa * a
+
+        # cross attention to the condition tokens
+        h = F.layer_norm(x, (C,), weight=blk.xnorm_w, bias=blk.xnorm_b, eps=cfg.ln_eps)
+        xq = lin["xq"](h.reshape(B * L, C)).view(B, L, H, 64)
+        xq = head_rmsnorm(torch, xq, blk.xq_gamma).permute(0, 2, 1, 3).contiguous()
+        kv = lin["xkv"](cond.reshape(B * Lc, C)).view(B, Lc, 2, H, 64)
+        xk = head_rmsnorm(torch, kv[:, :, 0], blk.xk_gamma).permute(0, 2, 1, 3).contiguous()
+        xv = kv[:, :, 1].permute(0, 2, 1, 3).contiguous()
+        a = native_sdpa_f32_ex(xq, xk, xv, out_layout="blhd")
+        x = x + lin["xout"](a.view(B * L, C)).view(B, L, C)
+
+        # MLP
+        h = F.layer_norm(x, (C,), eps=cfg.ln_eps) * (1 + scale_mlp) + shift_mlp
+        h = lin["fc1"](h.reshape(B * L, C))
+        h = F.gelu(h, approximate="tanh")
+        h = lin["fc2"](h).view(B, L, C)
+        return x + gate_mlp * h
+
+    def velocity(self, z, cond, t):
+        """z [B, L, C], cond [B, Lc, C], t [B] (already x1000) -> v [B, L, C]."""
+        torch = self.torch
+        F = torch.nn.functional
+        B, L, C = (int(s) for s in z.shape)
+        t_emb, t_mod = self.timestep(t)
+        x = self.input_layer(z.reshape(B * L, C)).view(B, L, C)
+        for blk in self.blocks:
+            x = self.block_forward(blk, x, cond, t_mod)
+        shift, scale = (self.final_shift_table[None] + t_emb[:, None, :]).unbind(1)
+        h = F.layer_norm(x, (C,), eps=self.cfg.final_ln_eps) * (1 + scale[:, None]) + shift[:, None]
+        return self.out_layer(h.reshape(B * L, C)).view(B, L, C)
+
+    def schedule(self):
+        s = self.cfg.shift
+        u = [1.0 - i / self.cfg.steps for i in range(self.cfg.steps + 1)]
+        return [s * x / (1.0 + (s - 1.0) * x) for x in u]
+
+    def euler_cfg_step(self, z, cond, step=0):
+        """One sampler step with CFG: z [L, C], cond [Lc, C] -> (z_next, v)."""
+        torch = self.torch
+        ts = self.schedule()
+        t = torch.full((2,), ts[step] * 1000.0, dtype=torch.float32, device=self.device)
+        dt = float(ts[step] - ts[step + 1])
+        zz = torch.stack((z, z))
+        cc = torch.stack((cond, torch.zeros_like(cond)))
+        v = self.velocity(zz, cc, t)
+        g = self.cfg.guidance
+        v_cfg = g * v[0] - (g - 1.0) * v[1]
+        return z - dt * v_cfg, v_cfg
+
+    def host(self):
+        """All parameters as NumPy arrays (for the CPU restatement)."""
+        return {
+            "t_fc1": self.t_fc1.host(), "t_fc2": self.t_fc2.host(), "adaln": self.adaln.host(),
+            "input_layer": self.input_layer.host(), "out_layer": self.out_layer.host(),
+            "final_shift_table": self.final_shift_table.cpu().numpy(),
+            "blocks": [b.host() for b in self.blocks],
+        }
