@@ -3,10 +3,12 @@
 TEST INFRASTRUCTURE ONLY (tests/ and bench.py's cpu_baseline leg).  The graph
 is the one frozen in triposplat-cpu-avx512_amd/tsplat/flow.py; here every
 NF24 Linear, the fused QKV projection and both SDPAs run through the CPU
-kernels -- the oracle restatement (`backend="oracle"`) or the reference's
-own AVX-512 build in oracle/_ref (`backend="reference"`) -- and the
-elementwise work is NumPy float32.  Parameters come from FlowModel.host(),
-so both sides use bit-identical packed weights.
+kernels -- the oracle restatement (`backend="oracle"`, elementwise work in
+NumPy float32) or the reference's own AVX-512 build in oracle/_ref
+(`backend="reference"`: its NF24 GEMM, QKV-direct and SDPA kernels and its
+LayerNorm / modulate / gated-residual / GELU / SiLU / RMSNorm / CFG / Euler
+kernels, i.e. the repository's CPU pipeline).  Parameters come from
+FlowModel.host(), so both sides use bit-identical packed weights.
 
 Model-level parity is "unpinned at the upstream boundary": the upstream
 TripoSplat model is absent; this restatement is checked against the device
@@ -92,36 +94,70 @@ class CpuFlow:
         freqs = np.exp(-math.log(10000.0) * np.arange(half, dtype=np.float32) / np.float32(half)).astype(np.float32)
         args = (np.asarray(t, np.float32)[:, None] * freqs[None, :]).astype(np.float32)
         emb = np.concatenate((np.cos(args), np.sin(args)), -1).astype(np.float32)
-        t_emb = self.linear(self.silu(self.linear(emb, self.p["t_fc1"])), self.p["t_fc2"])
-        t_mod = self.linear(self.silu(t_emb), self.p["adaln"])
+        t_emb = self.linear(self._silu(self.linear(emb, self.p["t_fc1"])), self.p["t_fc2"])
+        t_mod = self.linear(self._silu(t_emb), self.p["adaln"])
         return t_emb, t_mod
 
     # ---------------------------------------------------------- graph
+    # Elementwise dispatch: NumPy fp32 for the oracle backend, the reference's
+    # own AVX-512 kernels for the reference backend.
+    def _ln(self, x, eps, w=None, b=None):
+        if self.backend == "reference":
+            return O.ref_layernorm(x, eps, w, b, self.threads)
+        return self.layer_norm(x, eps, w, b)
+
+    def _modulate(self, h, scale, shift):
+        if self.backend == "reference":
+            return O.ref_modulate_inplace(h, scale, shift, self.threads)
+        return (h * (np.float32(1) + scale[:, None, :]) + shift[:, None, :]).astype(np.float32)
+
+    def _gated(self, x, h, gate):
+        if self.backend == "reference":
+            return O.ref_gated_residual_inplace(x, np.ascontiguousarray(h), gate, self.threads)
+        return (x + gate[:, None, :] * h).astype(np.float32)
+
+    def _add(self, x, d):
+        if self.backend == "reference":
+            return O.ref_add_inplace(x, d, self.threads)
+        return (x + d).astype(np.float32)
+
+    def _gelu(self, x):
+        return O.ref_gelu_tanh(x, self.threads) if self.backend == "reference" else self.gelu_tanh(x)
+
+    def _silu(self, x):
+        return O.ref_silu(x, self.threads) if self.backend == "reference" else self.silu(x)
+
+    def _rmsnorm(self, y, gamma):
+        if self.backend == "reference":
+            return O.ref_multihead_rmsnorm(y, gamma, 1e-12, self.threads)
+        return self.head_rmsnorm(y, gamma)
+
     def block(self, bp, x, cond, t_mod):
         cfg = self.cfg
         B, L, C = x.shape
         Lc = cond.shape[1]
         H = cfg.heads
-        mod = (t_mod + bp["shift_table"])[:, None, :]
-        sm, cm, gm, s2, c2, g2 = np.split(mod, 6, axis=-1)
-        h = (self.layer_norm(x, cfg.ln_eps) * (np.float32(1) + cm) + sm).astype(np.float32)
+        x = np.array(x, dtype=np.float32, copy=True)
+        mod = (t_mod + bp["shift_table"]).astype(np.float32)
+        sm, cm, gm, s2, c2, g2 = (np.ascontiguousarray(a) for a in np.split(mod, 6, axis=-1))
+        h = self._modulate(self._ln(x, cfg.ln_eps), cm, sm)
         q, pk, pv = self.qkv_direct(h.reshape(B * L, C), bp["qkv"], self.freqs(L), bp["q_gamma"],
                                     bp["k_gamma"], B, L, H)
         a = self.sdpa_packed_blhd(q, pk, pv, L).reshape(B * L, C)
-        x = (x + gm * self.linear(a, bp["out"]).reshape(B, L, C)).astype(np.float32)
-        h = self.layer_norm(x, cfg.ln_eps, bp["xnorm_w"], bp["xnorm_b"])
-        xq = self.head_rmsnorm(self.linear(h.reshape(B * L, C), bp["xq"]).reshape(B, L, H, 64), bp["xq_gamma"])
+        x = self._gated(x, self.linear(a, bp["out"]).reshape(B, L, C), gm)
+        h = self._ln(x, cfg.ln_eps, bp["xnorm_w"], bp["xnorm_b"])
+        xq = self._rmsnorm(self.linear(h.reshape(B * L, C), bp["xq"]).reshape(B, L, H, 64), bp["xq_gamma"])
         kv = self.linear(cond.reshape(B * Lc, C), bp["xkv"]).reshape(B, Lc, 2, H, 64)
-        xk = self.head_rmsnorm(kv[:, :, 0], bp["xk_gamma"])
+        xk = self._rmsnorm(np.ascontiguousarray(kv[:, :, 0]), bp["xk_gamma"])
         xv = kv[:, :, 1]
         a = self.sdpa_bhld(np.ascontiguousarray(xq.transpose(0, 2, 1, 3)), np.ascontiguousarray(xk.transpose(0, 2, 1, 3)),
                            np.ascontiguousarray(xv.transpose(0, 2, 1, 3)))
         a = np.ascontiguousarray(a.transpose(0, 2, 1, 3)).reshape(B * L, C)
-        x = (x + self.linear(a, bp["xout"]).reshape(B, L, C)).astype(np.float32)
-        h = (self.layer_norm(x, cfg.ln_eps) * (np.float32(1) + c2) + s2).astype(np.float32)
-        h = self.gelu_tanh(self.linear(h.reshape(B * L, C), bp["fc1"]))
+        x = self._add(x, self.linear(a, bp["xout"]).reshape(B, L, C))
+        h = self._modulate(self._ln(x, cfg.ln_eps), c2, s2)
+        h = self._gelu(self.linear(h.reshape(B * L, C), bp["fc1"]))
         h = self.linear(h, bp["fc2"]).reshape(B, L, C)
-        return (x + g2 * h).astype(np.float32)
+        return self._gated(x, h, g2)
 
     def velocity(self, z, cond, t):
         B, L, C = z.shape
@@ -129,9 +165,9 @@ class CpuFlow:
         x = self.linear(z.reshape(B * L, C), self.p["input_layer"]).reshape(B, L, C)
         for bp in self.p["blocks"]:
             x = self.block(bp, x, cond, t_mod)
-        fs = self.p["final_shift_table"][None] + t_emb[:, None, :]
-        shift, scale = fs[:, 0], fs[:, 1]
-        h = (self.layer_norm(x, self.cfg.final_ln_eps) * (np.float32(1) + scale[:, None]) + shift[:, None]).astype(np.float32)
+        fs = (self.p["final_shift_table"][None] + t_emb[:, None, :]).astype(np.float32)
+        shift, scale = np.ascontiguousarray(fs[:, 0]), np.ascontiguousarray(fs[:, 1])
+        h = self._modulate(self._ln(x, self.cfg.final_ln_eps), scale, shift)
         return self.linear(h.reshape(B * L, C), self.p["out_layer"]).reshape(B, L, C)
 
     def schedule(self):
@@ -144,6 +180,8 @@ class CpuFlow:
         t = np.full(2, ts[step] * 1000.0, np.float32)
         dt = np.float32(ts[step] - ts[step + 1])
         v = self.velocity(np.stack((z, z)), np.stack((cond, np.zeros_like(cond))), t)
+        if self.backend == "reference":
+            return O.ref_cfg_euler(z, v[0], v[1], self.cfg.guidance, float(dt), self.threads)
         g = np.float32(self.cfg.guidance)
         v_cfg = (g * v[0] - (g - np.float32(1)) * v[1]).astype(np.float32)
         return (z - dt * v_cfg).astype(np.float32), v_cfg

@@ -362,3 +362,123 @@ def ref_gemm_nf24_qkv_direct(x, code01_t, q2_t, scale, bias, freqs, q_gamma, k_g
     if st != 0:
         raise RuntimeError(f"reference QKV direct status {st}")
     return q, pk, pv
+
+
+# --------------------------------------------------------------------------
+# The reference's elementwise AVX-512 kernels (oracle/_ref), used by the
+# reference backend of flow_ref.CpuFlow so the CPU baseline of the model-level
+# configurations is the repository's own AVX-512 pipeline.
+_REF_EW = {}
+
+
+def _ref_ew(lib_name, sym, argtypes):
+    key = (lib_name, sym)
+    if key not in _REF_EW:
+        fn = getattr(ref_lib(lib_name), sym)
+        fn.argtypes = argtypes
+        fn.restype = _i
+        _REF_EW[key] = fn
+    return _REF_EW[key]
+
+
+_i64t = ctypes.c_int64
+
+
+def ref_layernorm(x, eps, weight=None, bias=None, threads=0):
+    """scripts/native_norm_rope_avx512.c:13-49 (rows x cols, optional affine)."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    cols = x.shape[-1]
+    fn = _ref_ew("libref_norm_rope.so", "triposplat_layernorm_f32_avx512",
+                 [_vp] * 4 + [_i64t, _i, ctypes.c_float, _i, _i])
+    w = None if weight is None else _f32(weight)
+    b = None if bias is None else _f32(bias)
+    st = fn(_ptr(x), _ptr(w), _ptr(b), _ptr(out), x.size // cols, cols, float(eps), int(w is not None), threads)
+    if st != 0:
+        raise RuntimeError(f"reference layernorm status {st}")
+    return out
+
+
+def ref_multihead_rmsnorm(x, gamma, eps=1e-12, threads=0):
+    """native_norm_rope_avx512.c:51-83: x [..., H, D] * sqrt(D)/max(||x||, eps) * gamma[H, D]."""
+    x = _f32(x)
+    gamma = _f32(gamma)
+    H, D = gamma.shape
+    out = np.empty_like(x)
+    fn = _ref_ew("libref_norm_rope.so", "triposplat_multihead_rmsnorm_f32_avx512",
+                 [_vp] * 3 + [_i64t, _i, _i, ctypes.c_float, _i])
+    st = fn(_ptr(x), _ptr(gamma), _ptr(out), x.size // (H * D), H, D, float(eps), threads)
+    if st != 0:
+        raise RuntimeError(f"reference rmsnorm status {st}")
+    return out
+
+
+def ref_modulate_inplace(h, scale, shift, threads=0):
+    """native_block_elementwise_avx512.c:9-22: h[b] = h[b] * (1 + scale[b]) + shift[b]."""
+    B, L, C = h.shape
+    fn = _ref_ew("libref_block_elementwise.so", "triposplat_modulate_inplace_f32_avx512",
+                 [_vp] * 3 + [_i] * 4)
+    sc, sh = _f32(scale), _f32(shift)
+    st = fn(_ptr(h), _ptr(sc), _ptr(sh), B, L, C, threads)
+    if st != 0:
+        raise RuntimeError(f"reference modulate status {st}")
+    return h
+
+
+def ref_gated_residual_inplace(x, h, gate, threads=0):
+    """native_block_elementwise_avx512.c:24-35: h *= gate; x += h."""
+    B, L, C = x.shape
+    fn = _ref_ew("libref_block_elementwise.so", "triposplat_gated_residual_inplace_f32_avx512",
+                 [_vp] * 3 + [_i] * 4)
+    g = _f32(gate)
+    st = fn(_ptr(x), _ptr(h), _ptr(g), B, L, C, threads)
+    if st != 0:
+        raise RuntimeError(f"reference gated residual status {st}")
+    return x
+
+
+def ref_add_inplace(x, d, threads=0):
+    fn = _ref_ew("libref_block_elementwise.so", "triposplat_add_inplace_f32_avx512", [_vp, _vp, _i64t, _i])
+    d = _f32(d)
+    st = fn(_ptr(x), _ptr(d), x.size, threads)
+    if st != 0:
+        raise RuntimeError(f"reference add status {st}")
+    return x
+
+
+def ref_gelu_tanh(x, threads=0):
+    x = _f32(x)
+    out = np.empty_like(x)
+    fn = _ref_ew("libref_activations.so", "triposplat_gelu_tanh_f32_avx512", [_vp, _vp, _i64t, _i])
+    st = fn(_ptr(x), _ptr(out), x.size, threads)
+    if st != 0:
+        raise RuntimeError(f"reference gelu status {st}")
+    return out
+
+
+def ref_silu(x, threads=0):
+    x = _f32(x)
+    out = np.empty_like(x)
+    fn = _ref_ew("libref_activations.so", "triposplat_silu_f32_avx512", [_vp, _vp, _i64t, _i])
+    st = fn(_ptr(x), _ptr(out), x.size, threads)
+    if st != 0:
+        raise RuntimeError(f"reference silu status {st}")
+    return out
+
+
+def ref_cfg_euler(z, v_pos, v_neg, guidance, dt, threads=0):
+    """native_sampler_avx512.c:19-89: v = g*v_pos - (g-1)*v_neg; z -= dt*v."""
+    pos = _f32(v_pos).copy()
+    neg = _f32(v_neg)
+    g = np.array([guidance], np.float32)
+    fn = _ref_ew("libref_sampler.so", "triposplat_cfg_combine_inplace_f32_avx512", [_vp] * 3 + [_i, _i64t, _i])
+    st = fn(_ptr(pos), _ptr(neg), _ptr(g), 1, pos.size, threads)
+    if st != 0:
+        raise RuntimeError(f"reference cfg status {st}")
+    out = _f32(z).copy()
+    d = np.array([dt], np.float32)
+    fn = _ref_ew("libref_sampler.so", "triposplat_euler_update_inplace_f32_avx512", [_vp] * 3 + [_i, _i64t, _i])
+    st = fn(_ptr(out), _ptr(pos), _ptr(d), 1, out.size, threads)
+    if st != 0:
+        raise RuntimeError(f"reference euler status {st}")
+    return out, pos
