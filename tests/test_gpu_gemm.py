@@ -122,6 +122,23 @@ def test_gemm_config1_sampled_rows(oracle, cuda, hiplib):
     print("config1 sampled rows", e_dev, e_ref)
 
 
+@pytest.mark.parametrize("M,K,N", [(16384, 1024, 1024), (32768, 1002, 1024), (2048, 1024, 2048),
+                                   (9000, 998, 1030)])
+def test_gemm_large_tiles_sampled_rows(oracle, cuda, hiplib, M, K, N):
+    """Shapes that route to each tile configuration (256x256, 256x192,
+    128x128), with the vectorised and the scalar-load paths (K % 4 != 0 or
+    odd N); the oracle checks 32 sampled rows."""
+    import torch
+
+    print(f"gemm large M={M} K={K} N={N}", flush=True)
+    x, w, b = seeded_linear(M + N, M, K, N, w_scale=0.02)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    got = _run_async(torch, hiplib, cuda, x, c01, q2, s, b)
+    rows = np.sort(np.random.default_rng(M).choice(M, 32, replace=False))
+    rows[0], rows[-1] = 0, M - 1
+    _check(oracle, x[rows], c01, q2, s, b, got[rows])
+
+
 def test_reference_named_entry_points(oracle, cuda, hiplib):
     """The blocking reference-named symbols take device pointers and keep the
     reference's status codes (scripts/gemm_nf24_i16_avx512.c:171-175)."""

@@ -25,21 +25,23 @@
 namespace tsplat {
 namespace {
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_>
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int kMinWaves_ = 1>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  static constexpr int kMinWaves = kMinWaves_;  // waves per SIMD the register budget must allow
   static constexpr int kThreads = WM * WN * 64;
   static constexpr int kTM = BM / WM, kTN = BN / WN;
   static constexpr int kMB = kTM / 32, kNB = kTN / 32;
   static constexpr int kS = BK + 4;  // LDS row stride in floats (bank spread)
-  static constexpr int kXVec = BM * BK / 4 / kThreads;  // X float4 per thread
-  static constexpr int kPairs = BN / 2;                  // W column pairs
-  static constexpr int kKGroups = kThreads / kPairs;
-  static constexpr int kKPT = BK / kKGroups;             // k per thread for W
+  // X tile: BM x BK as float4 units; W tile: (column pair, kWK consecutive k)
+  // units, kWK = 4 unless that leaves threads idle.
+  static constexpr int kXUnits = BM * BK / 4;
+  static constexpr int kWK = ((BN / 2) * (BK / 4) >= kThreads) ? 4 : 2;
+  static constexpr int kWUnits = (BN / 2) * (BK / kWK);
+  static constexpr int kXIter = (kXUnits + kThreads - 1) / kThreads;
+  static constexpr int kWIter = (kWUnits + kThreads - 1) / kThreads;
   static_assert(kTM % 32 == 0 && kTN % 32 == 0, "wave tile must be 32-aligned");
-  static_assert(BK % 8 == 0, "BK must be a multiple of 8");
-  static_assert(kXVec * 4 * kThreads == BM * BK, "X tile split");
-  static_assert(kKGroups * kPairs == kThreads && kKPT % 4 == 0, "W tile split");
+  static_assert(BK % 8 == 0 && BN % 2 == 0, "BK must be a multiple of 8, BN even");
 };
 
 struct GemmArgs {
@@ -55,7 +57,8 @@ struct GemmArgs {
 // kVec: x rows 16-byte aligned with K % 4 == 0, and N, n_start, n_count even
 // (so a column pair is loaded with one 32-bit / 16-bit access).
 template <class C, bool kVec>
-__global__ __launch_bounds__(C::kThreads) void nf24_gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::kMinWaves)))
+void nf24_gemm_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) float xs[2][C::BM * C::kS];
   __shared__ __attribute__((aligned(16))) float ws[2][C::BN * C::kS];
 
@@ -71,78 +74,95 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_kernel(GemmArgs a) {
   const int m0 = (tile / tiles_n) * C::BM;
   const int c0 = (tile % tiles_n) * C::BN;
 
-  // W assignment: this thread decodes columns (lc, lc+1) for kKPT k values.
-  const int pair = tid % C::kPairs;
-  const int kg = tid / C::kPairs;
-  const int lc = c0 + 2 * pair;
-  const bool ok0 = lc < a.n_count;
-  const bool ok1 = lc + 1 < a.n_count;
-  const int n_abs = a.n_start + lc;
-  const float sc0 = ok0 ? a.scale[n_abs] : 0.0f;
-  const float sc1 = ok1 ? a.scale[n_abs + 1] : 0.0f;
+  // W units owned by this thread: column pair (lc, lc+1), k = kWK*kq .. +kWK-1
+  // inside each K step.  The pair and its scales are fixed for the whole K loop.
+  int w_pair[C::kWIter], w_kq[C::kWIter], w_nabs[C::kWIter];
+  bool w_ok0[C::kWIter], w_ok1[C::kWIter], w_live[C::kWIter];
+  float w_sc0[C::kWIter], w_sc1[C::kWIter];
+#pragma unroll
+  for (int j = 0; j < C::kWIter; ++j) {
+    const int u = tid + j * C::kThreads;
+    w_live[j] = u < C::kWUnits;
+    w_pair[j] = u % (C::BN / 2);
+    w_kq[j] = u / (C::BN / 2);
+    const int lc = c0 + 2 * w_pair[j];
+    w_ok0[j] = w_live[j] && lc < a.n_count;
+    w_ok1[j] = w_live[j] && lc + 1 < a.n_count;
+    w_nabs[j] = a.n_start + lc;
+    w_sc0[j] = w_ok0[j] ? a.scale[w_nabs[j]] : 0.0f;
+    w_sc1[j] = w_ok1[j] ? a.scale[w_nabs[j] + 1] : 0.0f;
+  }
 
-  floatx4 xr[C::kXVec];
-  uint32_t cr[C::kKPT];  // two int16 codes (columns lc, lc+1)
-  uint32_t qr[C::kKPT];  // two int8 codes in the low 16 bits
+  floatx4 xr[C::kXIter];
+  uint32_t cr[C::kWIter][C::kWK];  // two int16 codes (columns lc, lc+1)
+  uint32_t qr[C::kWIter][C::kWK];  // two int8 codes in the low 16 bits
 
   auto load_tile = [&](int k0) {
 #pragma unroll
-    for (int j = 0; j < C::kXVec; ++j) {
+    for (int j = 0; j < C::kXIter; ++j) {
       const int idx = tid + j * C::kThreads;
       const int row = idx / (C::BK / 4);
       const int kc = idx % (C::BK / 4);
       const int gm = m0 + row;
       const int gk = k0 + 4 * kc;
+      const bool live = (C::kXUnits % C::kThreads == 0) || idx < C::kXUnits;
       const float* src = a.x + (int64_t)gm * a.stride_x + gk;
       if (kVec) {
-        xr[j] = (gm < a.M && gk < a.K) ? *reinterpret_cast<const floatx4*>(src) : floatx4{0, 0, 0, 0};
+        xr[j] = (live && gm < a.M && gk < a.K) ? *reinterpret_cast<const floatx4*>(src)
+                                                 : floatx4{0, 0, 0, 0};
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xr[j][e] = (gm < a.M && gk + e < a.K) ? src[e] : 0.0f;
+        for (int e = 0; e < 4; ++e) xr[j][e] = (live && gm < a.M && gk + e < a.K) ? src[e] : 0.0f;
       }
     }
 #pragma unroll
-    for (int i = 0; i < C::kKPT; ++i) {
-      const int gk = k0 + kg * C::kKPT + i;
-      const int64_t off = (int64_t)gk * a.N + n_abs;
-      if (kVec) {
-        const bool ok = ok0 && gk < a.K;
-        cr[i] = ok ? *reinterpret_cast<const uint32_t*>(a.code01 + off) : 0u;
-        qr[i] = ok ? (uint32_t)*reinterpret_cast<const uint16_t*>(a.q2 + off) : 0u;
-      } else {
+    for (int j = 0; j < C::kWIter; ++j) {
+#pragma unroll
+      for (int i = 0; i < C::kWK; ++i) {
+        const int gk = k0 + C::kWK * w_kq[j] + i;
+        const int64_t off = (int64_t)gk * a.N + w_nabs[j];
         const bool k_ok = gk < a.K;
-        const uint32_t c_lo = (k_ok && ok0) ? (uint16_t)a.code01[off] : 0u;
-        const uint32_t c_hi = (k_ok && ok1) ? (uint16_t)a.code01[off + 1] : 0u;
-        const uint32_t q_lo = (k_ok && ok0) ? (uint8_t)a.q2[off] : 0u;
-        const uint32_t q_hi = (k_ok && ok1) ? (uint8_t)a.q2[off + 1] : 0u;
-        cr[i] = c_lo | (c_hi << 16);
-        qr[i] = q_lo | (q_hi << 8);
+        if (kVec) {
+          const bool ok = w_ok0[j] && k_ok;
+          cr[j][i] = ok ? *reinterpret_cast<const uint32_t*>(a.code01 + off) : 0u;
+          qr[j][i] = ok ? (uint32_t)*reinterpret_cast<const uint16_t*>(a.q2 + off) : 0u;
+        } else {
+          const uint32_t c_lo = (k_ok && w_ok0[j]) ? (uint16_t)a.code01[off] : 0u;
+          const uint32_t c_hi = (k_ok && w_ok1[j]) ? (uint16_t)a.code01[off + 1] : 0u;
+          const uint32_t q_lo = (k_ok && w_ok0[j]) ? (uint8_t)a.q2[off] : 0u;
+          const uint32_t q_hi = (k_ok && w_ok1[j]) ? (uint8_t)a.q2[off + 1] : 0u;
+          cr[j][i] = c_lo | (c_hi << 16);
+          qr[j][i] = q_lo | (q_hi << 8);
+        }
       }
     }
   };
 
   auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < C::kXVec; ++j) {
+    for (int j = 0; j < C::kXIter; ++j) {
       const int idx = tid + j * C::kThreads;
+      if ((C::kXUnits % C::kThreads) != 0 && idx >= C::kXUnits) continue;
       const int row = idx / (C::BK / 4);
       const int kc = idx % (C::BK / 4);
       *reinterpret_cast<floatx4*>(&xs[buf][row * C::kS + 4 * kc]) = xr[j];
     }
 #pragma unroll
-    for (int i4 = 0; i4 < C::kKPT; i4 += 4) {
-      floatx4 w0, w1;
+    for (int j = 0; j < C::kWIter; ++j) {
+      if ((C::kWUnits % C::kThreads) != 0 && !w_live[j]) continue;
+      typedef float wvec __attribute__((ext_vector_type(C::kWK)));
+      wvec w0, w1;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t c = cr[i4 + e];
-        const uint32_t q = qr[i4 + e];
+      for (int e = 0; e < C::kWK; ++e) {
+        const uint32_t c = cr[j][e];
+        const uint32_t q = qr[j][e];
         const int32_t qa = (int32_t)(int16_t)(c & 0xffffu) * 256 + (int32_t)(int8_t)(q & 0xffu);
         const int32_t qb = (int32_t)(int16_t)(c >> 16) * 256 + (int32_t)(int8_t)((q >> 8) & 0xffu);
-        w0[e] = (float)qa * sc0;
-        w1[e] = (float)qb * sc1;
+        w0[e] = (float)qa * w_sc0[j];
+        w1[e] = (float)qb * w_sc1[j];
       }
-      *reinterpret_cast<floatx4*>(&ws[buf][(2 * pair) * C::kS + kg * C::kKPT + i4]) = w0;
-      *reinterpret_cast<floatx4*>(&ws[buf][(2 * pair + 1) * C::kS + kg * C::kKPT + i4]) = w1;
+      *reinterpret_cast<wvec*>(&ws[buf][(2 * w_pair[j]) * C::kS + C::kWK * w_kq[j]]) = w0;
+      *reinterpret_cast<wvec*>(&ws[buf][(2 * w_pair[j] + 1) * C::kS + C::kWK * w_kq[j]]) = w1;
     }
   };
 
@@ -223,14 +243,66 @@ int launch_cfg(const GemmParams& p, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-using CfgMain = GemmCfg<128, 128, 16, 2, 2>;
+// Tile configurations and the rates they sustain on MI355X when the grid is
+// many rounds deep (fp32 TFLOP/s, measured over M = 16384..32768 shapes).
+// The launcher picks the one with the smallest modelled time: full rounds of
+// CUs * wgs_per_cu tiles cost wgs_per_cu * BM * BN / rate each; a partial
+// last round costs ceil(rest / CUs) tiles' worth, 25 % more when a 4-wave
+// workgroup then runs alone on its CU (one wave per SIMD hides less latency).
+// Against measurement (M = 2048..32768, N = 1024..4096) the model picks the
+// fastest configuration or one within 3 % of it.
+using CfgLarge = GemmCfg<256, 256, 16, 4, 4>;    // 16 waves, 1 workgroup / CU
+using CfgWide = GemmCfg<256, 192, 16, 4, 3>;     // 12 waves, 1 workgroup / CU
+using CfgSmall = GemmCfg<128, 128, 16, 2, 2, 3>; // 4 waves, 3 workgroups / CU
 using CfgSkinny = GemmCfg<32, 128, 32, 1, 4>;
+
+struct Choice {
+  int bm, bn, wgs_per_cu, waves;
+  double rate;
+};
+constexpr Choice kChoices[] = {
+    {256, 256, 1, 16, 126.0}, {256, 192, 1, 12, 122.0}, {128, 128, 3, 4, 111.0}};
+
+int compute_units() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
 
 }  // namespace
 
 int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
   if (p.M <= 32) return launch_cfg<CfgSkinny>(p, stream);
-  return launch_cfg<CfgMain>(p, stream);
+  const int cus = compute_units();
+  int best = 0;
+  double best_t = 0.0;
+  for (int i = 0; i < 3; ++i) {
+    const Choice& c = kChoices[i];
+    const int64_t tiles = (int64_t)((p.M + c.bm - 1) / c.bm) * ((p.n_count + c.bn - 1) / c.bn);
+    const int64_t slots = (int64_t)cus * c.wgs_per_cu;
+    const int64_t full = tiles / slots;
+    const int64_t rest = tiles - full * slots;
+    const double tile_t = (double)c.bm * c.bn / c.rate;
+    double t = (double)full * c.wgs_per_cu * tile_t;
+    if (rest > 0) {
+      const int64_t k = (rest + cus - 1) / cus;
+      t += (double)k * tile_t * ((k == 1 && c.waves == 4) ? 1.25 : 1.0);
+    }
+    if (i == 0 || t < best_t) {
+      best = i;
+      best_t = t;
+    }
+  }
+  if (best == 0) return launch_cfg<CfgLarge>(p, stream);
+  if (best == 1) return launch_cfg<CfgWide>(p, stream);
+  return launch_cfg<CfgSmall>(p, stream);
 }
 
 }  // namespace tsplat
