@@ -273,8 +273,9 @@ def run_flow(torch, dev, steps, with_cpu, validate):
             est = blk_cpu * cfg.blocks
             out["config4_step"]["cpu_baseline"] = {
                 "kind": "reference" if backend == "reference" else "port", "cores": threads,
-                "sample": "one full-size block on both CFG branches (reference AVX-512 NF24 GEMM, "
-                          "QKV-direct and SDPA kernels + NumPy elementwise), x 28 blocks",
+                "sample": "one full-size block on both CFG branches through the reference's own "
+                          "AVX-512 kernels (NF24 GEMM, QKV-direct, SDPA, LayerNorm, modulate, "
+                          "gated residual, GELU, RMSNorm), x 28 blocks",
                 "block_s": blk_cpu, "s_per_denoise_step_estimated": est,
                 "speedup_gpu_vs_cpu": est / step_s,
             }

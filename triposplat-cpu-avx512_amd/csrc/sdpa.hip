@@ -5,9 +5,10 @@
 // out[q] = sum_j softmax_j(q.k_j * 0.125 + bias[j]) v_j, exact, with a
 // running (max, sum) merged tile by tile; no Lq x Lk matrix, no pruning.
 //
-// Mapping.  A workgroup owns 128 queries of one (b, h): four waves, 32
-// queries each, Q resident in registers.  Keys stream through LDS in
-// double-buffered tiles of 64 (K and V, plus the bias row).  Each wave
+// Mapping.  A workgroup owns 32 queries per wave (16 waves = 512 queries for
+// large grids, 4 waves otherwise) of one (b, h), Q resident in registers.
+// Keys stream through LDS in double-buffered tiles of 64 (K and V, plus the
+// bias row), shared by all waves of the workgroup.  Each wave
 // computes the transposed score block S^T = K Q^T with
 // v_mfma_f32_32x32x2_f32, which leaves every lane holding 32 keys of ONE
 // query (its own column): the row max and row sum are in-lane reductions
@@ -30,9 +31,6 @@ namespace tsplat {
 namespace {
 
 constexpr int kD = 64;
-constexpr int kBQ = 128;   // queries per workgroup
-constexpr int kBKV = 64;   // keys per tile
-constexpr int kThreads = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct SdpaArgs {
@@ -59,13 +57,24 @@ __device__ __forceinline__ float pair_sum(float x) {
 
 // kPacked: k/v are [B, H, 64, Lkp] (key-contiguous rows per dimension), as
 // the reference's packed kernel takes them; otherwise [B, H, Lk, 64].
-template <bool kPacked, bool kBias>
-__global__ __launch_bounds__(kThreads) void sdpa_kernel(SdpaArgs a) {
-  // LDS rows: unpacked K [key][d], packed K [d][key]; V likewise.
-  constexpr int kKS = kD + 4;                  // both K layouts: 64 + 4 pad
-  constexpr int kVS = kPacked ? kBKV + 4 : kD; // packed V is read as b128
-  __shared__ __attribute__((aligned(16))) float kbuf[2][64 * kKS];
-  __shared__ __attribute__((aligned(16))) float vbuf[2][64 * kVS];
+// kWaves waves of 32 queries each share every K/V tile of kBKV keys.
+// kSplit: run scores -> softmax -> PV per 32-key block of the tile (16 score
+// registers live instead of kBKV/2), for configurations short of registers.
+template <bool kPacked, bool kBias, int kWaves, int kBKV, bool kSplit>
+__global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
+  constexpr int kThreads = kWaves * 64;
+  constexpr int kBQ = kWaves * 32;
+  constexpr int kNKB = kBKV / 32;              // 32-key blocks per tile
+  // LDS: unpacked K [key][64 + 4], V [key][64]; packed K and V [d][kBKV + 4].
+  constexpr int kKRows = kPacked ? kD : kBKV;
+  constexpr int kKS = kPacked ? kBKV + 4 : kD + 4;
+  constexpr int kVS = kPacked ? kBKV + 4 : kD;
+  constexpr int kRowUnits = kPacked ? kBKV / 4 : kD / 4;  // float4 per LDS row
+  constexpr int kLoads = kKRows * kRowUnits / kThreads;   // float4 of K (and of V) per thread
+  static_assert(kLoads * kThreads == kKRows * kRowUnits, "tile split");
+  static_assert(kThreads >= kBKV, "bias row load");
+  __shared__ __attribute__((aligned(16))) float kbuf[2][kKRows * kKS];
+  __shared__ __attribute__((aligned(16))) float vbuf[2][kKRows * kVS];
   __shared__ __attribute__((aligned(16))) float bbuf[2][kBKV];
 
   const int tid = threadIdx.x;
@@ -96,15 +105,14 @@ __global__ __launch_bounds__(kThreads) void sdpa_kernel(SdpaArgs a) {
   const float* vbase = a.v + (int64_t)bh * (kPacked ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
   const float* brow = kBias ? a.bias + (int64_t)h * a.bias_head_stride : nullptr;
 
-  // Tile staging: 64 rows x 16 float4 for K and for V, 4 of each per thread.
-  floatx4 kr[4], vr[4];
+  floatx4 kr[kLoads], vr[kLoads];
   float br = 0.0f;
   auto load = [&](int key0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kLoads; ++j) {
       const int idx = tid + j * kThreads;
-      const int row = idx >> 4;
-      const int c = idx & 15;
+      const int row = idx / kRowUnits;
+      const int c = idx % kRowUnits;
       if (!kPacked) {
         const int key = key0 + row;
         const bool ok = key < a.Lk;
@@ -131,10 +139,10 @@ __global__ __launch_bounds__(kThreads) void sdpa_kernel(SdpaArgs a) {
   };
   auto store = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kLoads; ++j) {
       const int idx = tid + j * kThreads;
-      const int row = idx >> 4;
-      const int c = idx & 15;
+      const int row = idx / kRowUnits;
+      const int c = idx % kRowUnits;
       *reinterpret_cast<floatx4*>(&kbuf[buf][row * kKS + 4 * c]) = kr[j];
       *reinterpret_cast<floatx4*>(&vbuf[buf][row * kVS + 4 * c]) = vr[j];
     }
@@ -162,89 +170,97 @@ __global__ __launch_bounds__(kThreads) void sdpa_kernel(SdpaArgs a) {
     const float* kb_ = kbuf[buf];
     const float* vb_ = vbuf[buf];
 
-    // S^T[key][query] for keys key0 + 32*kb + (8*(r/4) + 4*g + r%4).
-    floatx16 s[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
-#pragma unroll
-    for (int hh = 0; hh < 8; ++hh) {
-      floatx4 kf[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        if (!kPacked) {
-          kf[kb] = *reinterpret_cast<const floatx4*>(&kb_[(kb * 32 + l32) * kKS + 8 * hh + 4 * g]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) kf[kb][e] = kb_[(8 * hh + 4 * g + e) * kKS + kb * 32 + l32];
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) s[kb] = mfma32x32x2(kf[kb][e], qf[hh][e], s[kb]);
-    }
-
-    // Scale (+ bias) in log2 units, mask keys past Lk, running max.
+    // One pass per group of kGB 32-key blocks: scores S^T[key][query] for keys
+    // key0 + 32*kb + (8*(r/4) + 4*g + r%4), running max, exponentials, PV.
+    constexpr int kGB = kSplit ? 1 : kNKB;
     const bool tail = key0 + kBKV > a.Lk;
-    float mx = -INFINITY;
+#pragma unroll(kSplit ? 1 : kNKB)
+    for (int kb0 = 0; kb0 < kNKB; kb0 += kGB) {
+      floatx16 s[kGB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int i = 0; i < kGB; ++i)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        floatx4 bb = {0, 0, 0, 0};
-        if (kBias) bb = *reinterpret_cast<const floatx4*>(&bbuf[buf][kb * 32 + 8 * r4 + 4 * g]);
+        for (int r = 0; r < 16; ++r) s[i][r] = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * r4 + e;
-          float x = kBias ? fmaf(s[kb][r], c1, bb[e]) : s[kb][r] * c1;
-          if (tail && key0 + kb * 32 + 8 * r4 + 4 * g + e >= a.Lk) x = -INFINITY;
-          s[kb][r] = x;
-          mx = fmaxf(mx, x);
-        }
-      }
-    mx = pair_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    float ls = 0.0f;
+      for (int hh = 0; hh < 8; ++hh) {
+        floatx4 kf[kGB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(s[kb][r] - m_new);
-        s[kb][r] = p;
-        ls += p;
-      }
-    l_run = fmaf(l_run, alpha, ls);
-    m_run = m_new;
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-
-    // O^T[d][query] += V^T P^T over the 64 keys of the tile.
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        floatx4 vf[2];
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
+        for (int i = 0; i < kGB; ++i) {
+          const int kb = kb0 + i;
           if (!kPacked) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              vf[db][e] = vb_[(kb * 32 + 8 * hh + 4 * g + e) * kVS + db * 32 + l32];
+            kf[i] = *reinterpret_cast<const floatx4*>(&kb_[(kb * 32 + l32) * kKS + 8 * hh + 4 * g]);
           } else {
-            vf[db] = *reinterpret_cast<const floatx4*>(
-                &vb_[(db * 32 + l32) * kVS + kb * 32 + 8 * hh + 4 * g]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) kf[i][e] = kb_[(8 * hh + 4 * g + e) * kKS + kb * 32 + l32];
           }
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
-          for (int db = 0; db < 2; ++db) o[db] = mfma32x32x2(vf[db][e], s[kb][4 * hh + e], o[db]);
+          for (int i = 0; i < kGB; ++i) s[i] = mfma32x32x2(kf[i][e], qf[hh][e], s[i]);
       }
+
+      // Scale (+ bias) in log2 units, mask keys past Lk, running max.
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < kGB; ++i)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int kb = kb0 + i;
+          floatx4 bb = {0, 0, 0, 0};
+          if (kBias) bb = *reinterpret_cast<const floatx4*>(&bbuf[buf][kb * 32 + 8 * r4 + 4 * g]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * r4 + e;
+            float x = kBias ? fmaf(s[i][r], c1, bb[e]) : s[i][r] * c1;
+            if (tail && key0 + kb * 32 + 8 * r4 + 4 * g + e >= a.Lk) x = -INFINITY;
+            s[i][r] = x;
+            mx = fmaxf(mx, x);
+          }
+        }
+      mx = pair_max(mx);
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      float ls = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kGB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pr = __builtin_amdgcn_exp2f(s[i][r] - m_new);
+          s[i][r] = pr;
+          ls += pr;
+        }
+      l_run = fmaf(l_run, alpha, ls);
+      m_run = m_new;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+
+      // O^T[d][query] += V^T P^T over these keys.
+#pragma unroll
+      for (int i = 0; i < kGB; ++i)
+#pragma unroll
+        for (int hh = 0; hh < 4; ++hh) {
+          const int kb = kb0 + i;
+          floatx4 vf[2];
+#pragma unroll
+          for (int db = 0; db < 2; ++db) {
+            if (!kPacked) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                vf[db][e] = vb_[(kb * 32 + 8 * hh + 4 * g + e) * kVS + db * 32 + l32];
+            } else {
+              vf[db] = *reinterpret_cast<const floatx4*>(
+                  &vb_[(db * 32 + l32) * kVS + kb * 32 + 8 * hh + 4 * g]);
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int db = 0; db < 2; ++db) o[db] = mfma32x32x2(vf[db][e], s[i][4 * hh + e], o[db]);
+        }
+    }
 
     if (t + 1 < ntiles) store(buf ^ 1);
     __syncthreads();
@@ -265,23 +281,39 @@ __global__ __launch_bounds__(kThreads) void sdpa_kernel(SdpaArgs a) {
     }
 }
 
+template <int kWaves, int kBKV, bool kSplit>
+int launch_shape(const SdpaArgs& a, const SdpaParams& p, hipStream_t stream) {
+  const int64_t tiles = (int64_t)p.B * p.H * ((p.Lq + kWaves * 32 - 1) / (kWaves * 32));
+  if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
+  dim3 grid((unsigned)tiles), block(kWaves * 64);
+  const bool bias = p.bias != nullptr;
+  if (p.kv_packed) {
+    if (bias) hipLaunchKernelGGL((sdpa_kernel<true, true, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((sdpa_kernel<true, false, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
+  } else {
+    if (bias) hipLaunchKernelGGL((sdpa_kernel<false, true, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((sdpa_kernel<false, false, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
+  }
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
 }  // namespace
 
+// Shapes measured on MI355X at B=1, H=16, L=16384 (fp32 TFLOP/s): 16 waves x
+// 64-key tiles 128 (no bias, 36 B/lane of spill that costs nothing there),
+// the same per-32-key split 128 with a key bias (the unsplit bias kernel
+// spills more and drops to 116), 8 x 64 about 118-125, 4 x 64 115-120.
+// Grids too small to give every CU one 512-query workgroup use 4 waves.
 int launch_sdpa(const SdpaParams& p, hipStream_t stream) {
   SdpaArgs a{p.q, p.k, p.v, p.bias, p.out, p.B, p.H, p.Lq, p.Lk, p.Lkp, p.bias_head_stride,
              p.out_blhd};
-  const int64_t tiles = (int64_t)p.B * p.H * ((p.Lq + kBQ - 1) / kBQ);
-  if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
-  dim3 grid((unsigned)tiles), block(kThreads);
-  const bool bias = p.bias != nullptr;
-  if (p.kv_packed) {
-    if (bias) hipLaunchKernelGGL((sdpa_kernel<true, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((sdpa_kernel<true, false>), grid, block, 0, stream, a);
-  } else {
-    if (bias) hipLaunchKernelGGL((sdpa_kernel<false, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((sdpa_kernel<false, false>), grid, block, 0, stream, a);
-  }
-  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const int64_t wide_tiles = (int64_t)p.B * p.H * ((p.Lq + 511) / 512);
+  if (wide_tiles < cus) return launch_shape<4, 64, false>(a, p, stream);
+  if (p.bias != nullptr) return launch_shape<16, 64, true>(a, p, stream);
+  return launch_shape<16, 64, false>(a, p, stream);
 }
 
 }  // namespace tsplat
