@@ -164,6 +164,43 @@ def run_sdpa(torch, dev, steps, warmup, host):
     return wall, kernel_ms
 
 
+def run_sdpa_variants(torch, dev, host, iters=5):
+    """key-bias self attention (per-head bias [16, 16384] ~ U(-2, 0),
+    and the reference-faithful shared [Lk] bias with log(2048) on one key),
+    and cross attention (16384 queries vs 2048 condition keys, k/v ~ N(0,1))."""
+    import numpy as np
+    from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
+
+    q_h, k_h, v_h = host
+    B, H, L, D = q_h.shape
+    q = torch.from_numpy(q_h).to(dev)
+    k = torch.from_numpy(k_h).to(dev)
+    v = torch.from_numpy(v_h).to(dev)
+    out = torch.empty((B, L, H, D), dtype=torch.float32, device=dev)
+    bias_h = np.random.default_rng(13).uniform(-2.0, 0.0, (H, L)).astype(np.float32)
+    bias = torch.from_numpy(bias_h).to(dev)
+    shared = torch.zeros(L, dtype=torch.float32, device=dev)
+    shared[4096] = math.log(2048.0)
+    Lc = 2048
+    kc = torch.from_numpy(np.random.default_rng(14).standard_normal((B, H, Lc, D), dtype=np.float32)).to(dev)
+    vc = torch.from_numpy(np.random.default_rng(15).standard_normal((B, H, Lc, D), dtype=np.float32)).to(dev)
+    res = {}
+    for name, fn, flop in (
+        ("keybias_per_head", lambda: native_sdpa_f32_ex(q, k, v, key_bias_per_head=bias, out=out, out_layout="blhd"),
+         4.0 * B * H * L * L * D),
+        ("keybias_shared_log2048", lambda: native_sdpa_f32_ex(q, k, v, key_bias=shared, out=out, out_layout="blhd"),
+         4.0 * B * H * L * L * D),
+        ("cross_16384x2048", lambda: native_sdpa_f32_ex(q, kc, vc, out=out, out_layout="blhd"),
+         4.0 * B * H * L * Lc * D),
+    ):
+        fn()
+        torch.cuda.synchronize()
+        ms = sorted(time_events(torch, fn, iters) for _ in range(3))[1]
+        tf = flop / (ms * 1e-3) / 1e12
+        res[name] = {"ms": ms, "tflops": tf, "frac_fp32_mfma_peak": tf / PEAK_FP32_MFMA}
+    return res
+
+
 def run_gemm(torch, dev, iters):
     """NF24 Linear 4096x1024 @ 1024x3072 (+ bias)."""
     import numpy as np
@@ -286,6 +323,33 @@ def run_flow(torch, dev, steps, with_cpu, validate):
     return out
 
 
+def run_gemm_skinny(torch, dev, iters=50):
+    """configs[0] skinny-M variants (HBM-bound): M in {1, 2, 8, 16} rows against
+    the K x N weights {1024 x 3072, 1024 x 6144, 4096 x 1024}; GB/s counts the
+    algorithmic bytes 3*K*N + 8*N + 4*M*(K+N) per call (HIP-event time of the
+    call, launch gaps included), against the 8 TB/s HBM peak."""
+    from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
+
+    g = torch.Generator(device=dev).manual_seed(3)
+    rows = []
+    for K, N in ((1024, 3072), (1024, 6144), (4096, 1024)):
+        w = torch.randn((N, K), generator=g, device=dev) * 0.02
+        b = torch.randn((N,), generator=g, device=dev) * 0.01
+        codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+        for M in (1, 2, 8, 16):
+            x = torch.randn((M, K), generator=g, device=dev)
+            out = torch.empty((M, N), device=dev)
+            fn = lambda: nf24_linear(x, codes[0], codes[1], scales[0], b, out=out)
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            us = sorted(time_events(torch, fn, iters) for _ in range(3))[1] * 1e3
+            byts = 3 * K * N + 8 * N + 4 * M * (K + N)
+            rows.append({"M": M, "K": K, "N": N, "us": us, "GBps": byts / us / 1e3,
+                         "frac_hbm_peak": byts / us / 1e3 / PEAK_HBM})
+    return rows
+
+
 def run_copy(torch, dev, iters):
     """Calibration kernel for the HBM counters: a plain 256 MiB device copy."""
     n = 64 << 20
@@ -304,7 +368,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=("sdpa", "gemm", "copy", "flow"), default=None,
+    ap.add_argument("--only", choices=("sdpa", "gemm", "copy", "flow", "skinny"), default=None,
                     help="run one workload alone (for profiler runs) and print its figures")
     ap.add_argument("--no-flow", action="store_true", help="skip configs[3]/[4] (flow block / step)")
     ap.add_argument("--validate-flow", action="store_true",
@@ -331,6 +395,9 @@ def main():
     if args.only == "copy":
         print(json.dumps(run_copy(torch, dev, max(3, args.steps))))
         return 0
+    if args.only == "skinny":
+        print(json.dumps(run_gemm_skinny(torch, dev)))
+        return 0
     if args.only == "flow":
         print(json.dumps(run_flow(torch, dev, 3, not args.no_cpu_baseline, args.validate_flow)))
         return 0
@@ -344,7 +411,9 @@ def main():
         print(json.dumps({"sdpa_ms": kernel_ms, "tflops": achieved}))
         return 0
 
+    variants = run_sdpa_variants(torch, dev, host)
     gemm = run_gemm(torch, dev, 20)
+    gemm["skinny_m"] = run_gemm_skinny(torch, dev)
     flow = None if args.no_flow else run_flow(torch, dev, 3, not args.no_cpu_baseline, args.validate_flow)
     cpu = None if args.no_cpu_baseline else cpu_baseline_sdpa(*host)
 
@@ -376,6 +445,7 @@ def main():
             "flop_per_launch": sdpa_flop,
         },
         "cpu_baseline": cpu,
+        "sdpa_config2": variants,
         "gemm_config0": gemm,
         "flow": flow,
     }

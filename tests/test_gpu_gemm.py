@@ -60,7 +60,9 @@ def _check(oracle, x, c01, q2, s, b, got, start=0):
 # including the N=5 tail, plus skinny and ragged shapes.
 SHAPES = [(25, 96, 64), (40, 96, 64), (10, 96, 64), (3, 96, 5), (1, 1024, 3072), (2, 1024, 256),
           (8, 4096, 64), (16, 64, 1024), (33, 130, 48), (129, 257, 200), (200, 64, 129),
-          (7, 3, 17), (300, 1024, 96)]
+          (7, 3, 17), (300, 1024, 96),
+          # few-row (HBM-bound) kernel: every row-count template, split and unsplit K
+          (4, 2048, 640), (16, 1024, 3072), (32, 512, 384), (5, 4096, 1024), (12, 1000, 130)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)

@@ -166,18 +166,13 @@ int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
     return kErrDims;
   const int64_t M = (int64_t)B * L;
   if (M > 0x7fffffff) return kErrDims;
-  // The [B*L, N] projection lives only for the duration of the call, in
-  // stream-ordered device memory.
-  float* qkv = nullptr;
-  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&qkv), (size_t)M * N * 4, stream);
-  if (e != hipSuccess || qkv == nullptr) {
-    (void)hipGetLastError();
-    return kErrWorkspace;
-  }
+  // The [B*L, N] projection goes through the stream's workspace (ordered by
+  // the stream, so consecutive calls reuse it).
+  float* qkv = static_cast<float*>(stream_workspace(stream, (size_t)M * N * 4, kSlotQkvProjection));
+  if (qkv == nullptr) return kErrWorkspace;
   int st = gemm_checked(x, code01, q2, scale, bias, qkv, (int)M, K, N, 0, N, K, N, stream);
   if (st == kOk) st = post_checked(qkv, freqs, qg, kg, q, pk, pv, B, L, H, D, Lp, fb, stream);
-  const int fst = note(hipFreeAsync(qkv, stream));
-  return st != kOk ? st : fst;
+  return st;
 }
 
 }  // namespace

@@ -279,7 +279,12 @@ int compute_units() {
 }  // namespace
 
 int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
-  if (p.M <= 32) return launch_cfg<CfgSkinny>(p, stream);
+  // Few rows: the weight stream is the cost; the MFMA skinny tile only wins
+  // for 9..32 rows over a short K (measured at K = 256).
+  if (p.M <= 32) {
+    if (p.M > 8 && p.K <= 256) return launch_cfg<CfgSkinny>(p, stream);
+    return launch_nf24_gemv(p, stream);
+  }
   const int cus = compute_units();
   int best = 0;
   double best_t = 0.0;

@@ -1,0 +1,224 @@
+// NF24 GEMM for few rows (M <= 32): the HBM-bound case (timestep / adaLN /
+// camera rows), where the 3 bytes per weight dominate and the arithmetic
+// intensity is ~0.66*M FLOP/B.
+//
+// Same semantics as nf24_gemm.hip (scripts/gemm_nf24_i16_avx512.c:26-197):
+// out[m, c] = bias[n] + sum_k x[m, k] * w[k, n] with the weight decoded in
+// registers exactly as decode16 does.  Layout of the work:
+//   * a lane owns two adjacent columns (one 32-bit code01 load and one 16-bit
+//     q2 load per k row: a wave reads 256 B + 128 B contiguous per row);
+//   * a workgroup (W waves) owns 128 columns and a K range, split into W
+//     consecutive parts, one per wave; x for that range is staged in LDS and
+//     read as broadcasts;
+//   * K is also split across workgroups so that every CU streams weights; the
+//     per-wave partial sums are combined in LDS in wave order; each split
+//     writes its partial to a per-stream workspace and a second kernel sums
+//     the partials in split order, so the result is deterministic.  (A
+//     last-workgroup reduction inside one kernel needs agent-scope fences,
+//     which write back L2 and measured 3x slower on gfx950.)
+// Per output the order is: sequential fma over each wave's rows, then the
+// fixed-order sums.
+
+#include "tsplat_common.h"
+#include "tsplat_launch.h"
+
+namespace tsplat {
+namespace {
+
+constexpr int kReduceThreads = 256;
+constexpr int kCols = 128;  // columns per workgroup
+
+struct GemvArgs {
+  const float* x;
+  const int16_t* code01;
+  const int8_t* q2;
+  const float* scale;
+  const float* bias;
+  float* out;
+  float* partial;   // [splits][M][count] when splits > 1
+  int M, K, N, n_start, n_count, stride_x, stride_out;
+  int k_per_split;  // rows of K per workgroup (multiple of 4)
+  int splits;
+};
+
+template <int MT, int W>
+__global__ __launch_bounds__(W * 64) void nf24_gemv_kernel(GemvArgs a) {
+  constexpr int kThreads = W * 64;
+  extern __shared__ float smem[];  // x tile [MT][k_per_split], then wave partials
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int cgroups = (a.n_count + kCols - 1) / kCols;
+  const int cg = blockIdx.x % cgroups;
+  const int split = blockIdx.x / cgroups;
+  const int k0 = split * a.k_per_split;
+  const int k1 = min(a.K, k0 + a.k_per_split);
+  const int kn = k1 - k0;
+
+  // Stage x[k0..k1)[m] k-major, so the MT values of one row are contiguous
+  // (read as 128-bit broadcasts); rows past M and K are zero.
+  float* xs = smem;
+  for (int i = tid; i < MT * a.k_per_split; i += kThreads) {
+    const int m = i / a.k_per_split, kk = i % a.k_per_split;
+    xs[kk * MT + m] = (m < a.M && kk < kn) ? a.x[(int64_t)m * a.stride_x + k0 + kk] : 0.0f;
+  }
+  __syncthreads();
+
+  const int lc = cg * kCols + 2 * lane;  // local column of this lane's first column
+  const bool ok0 = lc < a.n_count, ok1 = lc + 1 < a.n_count;
+  const int n = a.n_start + lc;
+  const float s0 = ok0 ? a.scale[n] : 0.0f;
+  const float s1 = ok1 ? a.scale[n + 1] : 0.0f;
+  const bool vec = ((a.N | a.n_start) & 1) == 0;
+
+  // This wave's 1/W of the split's rows.
+  const int q = (kn + W - 1) / W;
+  const int r0 = wave * q, r1 = min(kn, r0 + q);
+
+  float acc0[MT], acc1[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc0[m] = acc1[m] = 0.0f;
+
+  auto load_row = [&](int r, uint32_t& c, uint32_t& qq) {
+    const int64_t off = (int64_t)(k0 + r) * a.N + n;
+    c = 0;
+    qq = 0;
+    if (vec) {
+      if (ok0) {
+        c = *reinterpret_cast<const uint32_t*>(a.code01 + off);
+        qq = *reinterpret_cast<const uint16_t*>(a.q2 + off);
+      }
+    } else {
+      if (ok0) { c = (uint16_t)a.code01[off]; qq = (uint8_t)a.q2[off]; }
+      if (ok1) { c |= (uint32_t)(uint16_t)a.code01[off + 1] << 16; qq |= (uint32_t)(uint8_t)a.q2[off + 1] << 8; }
+    }
+  };
+  auto consume = [&](int r, uint32_t c, uint32_t qq) {
+    const float w0 = (float)((int32_t)(int16_t)(c & 0xffffu) * 256 + (int32_t)(int8_t)(qq & 0xffu)) * s0;
+    const float w1 = (float)((int32_t)(int16_t)(c >> 16) * 256 + (int32_t)(int8_t)((qq >> 8) & 0xffu)) * s1;
+    const float* xr = xs + r * MT;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const float xv = xr[m];
+      acc0[m] = fmaf(xv, w0, acc0[m]);
+      acc1[m] = fmaf(xv, w1, acc1[m]);
+    }
+  };
+  // Rows in groups of 8: all eight loads are issued before any is consumed.
+  constexpr int kU = 8;
+  int r = r0;
+  for (; r + kU <= r1; r += kU) {
+    uint32_t c[kU], qq[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) load_row(r + u, c[u], qq[u]);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) consume(r + u, c[u], qq[u]);
+  }
+  for (; r < r1; ++r) {
+    uint32_t c, qq;
+    load_row(r, c, qq);
+    consume(r, c, qq);
+  }
+
+  // Combine the W waves in wave order through LDS.
+  __syncthreads();
+  float* part = smem;  // [W][MT][kCols]
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    part[(wave * MT + m) * kCols + 2 * lane] = acc0[m];
+    part[(wave * MT + m) * kCols + 2 * lane + 1] = acc1[m];
+  }
+  __syncthreads();
+  for (int i = tid; i < MT * kCols; i += kThreads) {
+    const int m = i / kCols, c = i % kCols;
+    const int col = cg * kCols + c;
+    if (m >= a.M || col >= a.n_count) continue;
+    float v = part[m * kCols + c];
+#pragma unroll
+    for (int w = 1; w < W; ++w) v += part[(w * MT + m) * kCols + c];
+    if (a.splits > 1) {
+      a.partial[((int64_t)split * a.M + m) * a.n_count + col] = v;
+    } else {
+      a.out[(int64_t)m * a.stride_out + col] = a.bias[a.n_start + col] + v;
+    }
+  }
+}
+
+// out[m, c] = bias + sum over splits (in split order) of the partials.
+__global__ __launch_bounds__(kReduceThreads) void nf24_gemv_reduce_kernel(
+    const float* partial, const float* bias, float* out, int M, int count, int n_start,
+    int stride_out, int splits) {
+  const int64_t i = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x;
+  if (i >= (int64_t)M * count) return;
+  const int m = (int)(i / count), c = (int)(i % count);
+  float v = partial[i];
+  for (int s = 1; s < splits; ++s) v += partial[(int64_t)s * M * count + i];
+  out[(int64_t)m * stride_out + c] = bias[n_start + c] + v;
+}
+
+template <int MT, int W>
+int launch_mt(GemvArgs a, int cgroups, int splits, hipStream_t stream) {
+  const size_t x_bytes = (size_t)MT * a.k_per_split * 4;
+  const size_t p_bytes = (size_t)W * MT * kCols * 4;
+  const size_t lds = x_bytes > p_bytes ? x_bytes : p_bytes;
+  if (lds > 64 * 1024) return kErrDims;
+  hipLaunchKernelGGL((nf24_gemv_kernel<MT, W>), dim3(cgroups * splits), dim3(W * 64), lds, stream, a);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // namespace
+
+// Workgroups of W waves (16 for M <= 4, 8 for M <= 8, else 4: the LDS of the
+// in-workgroup reduction is W * M * 128 floats) own 128 columns and split
+// their K range W ways.  K is split across workgroups only when the column
+// groups alone leave most CUs idle (fewer than 64 groups), so that ~256
+// workgroups stream the weights, at most until each wave keeps 16 rows and
+// the partial sums (splits * M * count * 8 bytes) stay under half the weight
+// bytes; a split costs a second, small kernel.
+int launch_nf24_gemv(const GemmParams& p, hipStream_t stream) {
+  if (p.M < 1 || p.M > 32) return kErrDims;
+  const int mt = p.M <= 1 ? 1 : p.M <= 2 ? 2 : p.M <= 4 ? 4 : p.M <= 8 ? 8 : p.M <= 16 ? 16 : 32;
+  const int w = mt <= 4 ? 16 : mt <= 8 ? 8 : 4;
+  const int cgroups = (p.n_count + kCols - 1) / kCols;
+  int splits = 1;
+  if (cgroups < 64) {
+    splits = (256 + cgroups - 1) / cgroups;
+    const int by_rows = p.K / (16 * w) > 1 ? p.K / (16 * w) : 1;
+    const double by_traffic = 0.1875 * (double)p.K / (double)p.M;
+    if (splits > by_rows) splits = by_rows;
+    if (splits > by_traffic) splits = by_traffic < 1.0 ? 1 : (int)by_traffic;
+    if (splits < 1) splits = 1;
+  }
+  int kps = (((p.K + splits - 1) / splits) + 3) & ~3;
+  while ((size_t)mt * kps * 4 > 64 * 1024) {  // keep the x tile within 64 KB of LDS
+    ++splits;
+    kps = (((p.K + splits - 1) / splits) + 3) & ~3;
+  }
+  splits = (p.K + kps - 1) / kps;
+
+  GemvArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out, nullptr, p.M, p.K, p.N,
+             p.n_start, p.n_count, p.stride_x, p.stride_out, kps, splits};
+  if (splits > 1) {
+    a.partial = static_cast<float*>(
+        stream_workspace(stream, (size_t)splits * p.M * p.n_count * 4, kSlotGemvPartial));
+    if (a.partial == nullptr) return kErrWorkspace;
+  }
+  int st;
+  switch (mt) {
+    case 1: st = launch_mt<1, 16>(a, cgroups, splits, stream); break;
+    case 2: st = launch_mt<2, 16>(a, cgroups, splits, stream); break;
+    case 4: st = launch_mt<4, 16>(a, cgroups, splits, stream); break;
+    case 8: st = launch_mt<8, 8>(a, cgroups, splits, stream); break;
+    case 16: st = launch_mt<16, 4>(a, cgroups, splits, stream); break;
+    default: st = launch_mt<32, 4>(a, cgroups, splits, stream); break;
+  }
+  if (st != kOk || splits == 1) return st;
+  const int64_t total = (int64_t)p.M * p.n_count;
+  hipLaunchKernelGGL(nf24_gemv_reduce_kernel,
+                     dim3((unsigned)((total + kReduceThreads - 1) / kReduceThreads)),
+                     dim3(kReduceThreads), 0, stream, a.partial, p.bias, p.out, p.M, p.n_count,
+                     p.n_start, p.stride_out, splits);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // namespace tsplat

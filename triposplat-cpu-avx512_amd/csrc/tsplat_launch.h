@@ -22,6 +22,8 @@ struct GemmParams {
   int stride_x, stride_out;
 };
 int launch_nf24_gemm(const GemmParams& p, hipStream_t stream);
+// Few-row form (1 <= M <= 32), HBM-bound; same result contract.
+int launch_nf24_gemv(const GemmParams& p, hipStream_t stream);
 
 // softmax(q k^T / 8 + bias[key]) v over one (b, h) per query row.
 struct SdpaParams {
@@ -57,5 +59,11 @@ int launch_qkv_postprocess(const QkvPostParams& p, hipStream_t stream);
 int launch_nf24_pack(const float* w, int out_f, int in_f, const float* alphabet, int alphabet_len,
                      float* base_tmp, int16_t* code01_t, int8_t* q2_t, float* scale,
                      hipStream_t stream);
+
+// Grow-only device scratch owned by the library, one buffer per (device,
+// stream, slot); null on allocation failure.  Valid until the next call with
+// the same key that asks for more bytes.
+enum WorkspaceSlot : int { kSlotGemvPartial = 0, kSlotQkvProjection = 1 };
+void* stream_workspace(hipStream_t stream, size_t bytes, int slot);
 
 }  // namespace tsplat
