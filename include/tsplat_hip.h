@@ -119,7 +119,7 @@ void triposplat_sdpa_q8t512_workspace_release(void);
 /* Asynchronous SDPA on `stream` (extension of the two entries above):
  * kv_packed selects k/v [B,H,64,Lkp] instead of [B,H,Lk,64]; out_blhd
  * selects [B,Lq,H,64] output; bias_head_stride = 0 shares one [Lk] bias
- * row, = Lk reads a [H,Lk] per-head bias. */
+ * row, = Lk reads a [H,Lk] per-head bias (the key-bias benchmark variant). */
 int tsplat_sdpa_async(const float* q, const float* k, const float* v,
                       const float* key_bias_or_null, float* out, int B, int H, int Lq, int Lk,
                       int D, int has_key_bias, int key_bias_len, int64_t bias_head_stride,

@@ -1,4 +1,4 @@
-"""CPU fp32 restatement of the synthetic flow model (BASELINE configs 4/5).
+"""CPU fp32 restatement of the synthetic flow model (benchmark configs 4 and 5).
 
 TEST INFRASTRUCTURE ONLY (tests/ and bench.py's cpu_baseline leg).  The graph
 is the one frozen in triposplat-cpu-avx512_amd/tsplat/flow.py; here every

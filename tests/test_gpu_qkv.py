@@ -53,22 +53,31 @@ def test_qkv_postprocess(oracle, cuda, B, L, H, fb):
         assert not got[1].cpu().numpy()[..., L:].any()
 
 
-def test_qkv_direct(oracle, cuda):
+@pytest.mark.parametrize("B,L,H,fb,Lp", [(2, 45, 2, 2, None), (1, 17, 4, 1, None), (3, 20, 2, 1, 64),
+                                         (2, 61, 3, 1, None)])
+def test_qkv_direct(oracle, cuda, B, L, H, fb, Lp):
+    """The fused projection (RoPE, RMSNorm and the packed stores in the GEMM
+    epilogue) against the oracle's projection + postprocess; covers rows of
+    two sequences in one tile, L % 4 != 0 (scalar packed stores), a padded
+    length beyond roundup16(L) (tail-zero kernel) and a tiny M."""
     import torch
     from tsplat.qkv import gemm_nf24_qkv_direct
 
-    B, L, H = 2, 45, 2
+    print(f"qkv_direct B={B} L={L} H={H} fb={fb} Lp={Lp}", flush=True)
     C = H * 64
-    r = np.random.default_rng(8)
+    r = np.random.default_rng(8 + L)
     x = r.standard_normal((B * L, C), dtype=np.float32)
     w = (r.standard_normal((3 * C, C)) * 0.03).astype(np.float32)
     b = (r.standard_normal(3 * C) * 0.01).astype(np.float32)
     c01, q2, s = oracle.quantize_nf24_i16(w)
-    fr = _freqs(B, L, H, 5)
+    fr = _freqs(fb, L, H, 5)
     qg, kg = _gammas(H, 6)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
-    got = gemm_nf24_qkv_direct(t(x), t(c01), t(q2), t(s), t(b), t(fr), t(qg), t(kg), B, L, H)
+    got = gemm_nf24_qkv_direct(t(x), t(c01), t(q2), t(s), t(b), t(fr), t(qg), t(kg), B, L, H,
+                               L_padded=Lp)
     ref = oracle.gemm_nf24_qkv_direct(x, c01, q2, s, b, fr, qg, kg, B, L, H)
+    if Lp is not None:
+        assert not got[1].cpu().numpy()[..., L:].any() and not got[2].cpu().numpy()[..., L:].any()
     proj = oracle.nf24_gemm(x, c01, q2, s, b)
     bound = gemm_order_bound(x, oracle.decode_nf24(c01, q2, s), b)  # [B*L, 3C]
     for which, (g, r_) in enumerate(zip(got, ref)):
@@ -86,6 +95,37 @@ def test_qkv_direct(oracle, cuda):
         else:
             d = np.abs(g[..., :L] - r_[..., :L]).transpose(0, 1, 3, 2)   # -> [B, H, L, 64]
         assert np.all(d <= tol), (which, float(d.max()))
+
+
+@pytest.mark.parametrize("B,L,H,fb", [(1, 16384, 16, 1), (1, 4096, 16, 1), (2, 300, 4, 2), (3, 257, 2, 1),
+                                     (1, 5000, 16, 1), (1, 8194, 16, 1), (1, 3000, 16, 1)])
+def test_qkv_fused_matches_unfused(oracle, cuda, B, L, H, fb):
+    """Fused epilogue == NF24 GEMM then the postprocess kernel, at shapes that
+    route to each tile configuration (256x256: L=16384, 5000, 8194; 256x192:
+    L=4096, 3000; 128x128: the rest), with partial row tiles and odd L.
+    Both paths run the same GEMM main loop, so v is bit-identical and q, k
+    differ only in the order of the 64-term sum of squares (|dy| <= 1e-5)."""
+    import torch
+    from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
+    from tsplat.qkv import gemm_nf24_qkv_direct, qkv_rope_rmsnorm_pack
+
+    print(f"qkv fused vs unfused B={B} L={L} H={H}", flush=True)
+    C = H * 64
+    g = torch.Generator(device=cuda).manual_seed(L)
+    x = torch.randn((B * L, 1024), generator=g, device=cuda)
+    w = torch.randn((3 * C, 1024), generator=g, device=cuda) * 0.02
+    bias = torch.randn((3 * C,), generator=g, device=cuda) * 0.01
+    codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+    fr = torch.from_numpy(_freqs(fb, L, H, 7)).to(cuda)
+    qg, kg = (torch.from_numpy(a).to(cuda) for a in _gammas(H, 9))
+    fused = gemm_nf24_qkv_direct(x, codes[0], codes[1], scales[0], bias, fr, qg, kg, B, L, H)
+    proj = nf24_linear(x, codes[0], codes[1], scales[0], bias)
+    unfused = qkv_rope_rmsnorm_pack(proj, fr, qg, kg, B, L, H)
+    torch.cuda.synchronize(cuda)
+    assert torch.equal(fused[2], unfused[2])
+    for a_, b_ in zip(fused[:2], unfused[:2]):
+        assert bool(torch.isfinite(a_).all())
+        assert float((a_ - b_).abs().max()) <= 1e-5
 
 
 @pytest.mark.parametrize("out_f,in_f", [(64, 96), (17, 64), (3072, 1024), (5, 1024), (100, 33)])

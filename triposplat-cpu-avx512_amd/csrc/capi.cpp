@@ -166,12 +166,24 @@ int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
     return kErrDims;
   const int64_t M = (int64_t)B * L;
   if (M > 0x7fffffff) return kErrDims;
-  // The [B*L, N] projection goes through the stream's workspace (ordered by
-  // the stream, so consecutive calls reuse it).
-  float* qkv = static_cast<float*>(stream_workspace(stream, (size_t)M * N * 4, kSlotQkvProjection));
-  if (qkv == nullptr) return kErrWorkspace;
-  int st = gemm_checked(x, code01, q2, scale, bias, qkv, (int)M, K, N, 0, N, K, N, stream);
-  if (st == kOk) st = post_checked(qkv, freqs, qg, kg, q, pk, pv, B, L, H, D, Lp, fb, stream);
+  if (!aligned16(pk) || !aligned16(pv)) return kErrAlign;
+  const int64_t C = (int64_t)H * kHeadDim;
+  TSPLAT_CHECK(check_dev(x, M * K * 4));
+  TSPLAT_CHECK(check_dev(code01, (int64_t)K * N * 2));
+  TSPLAT_CHECK(check_dev(q2, (int64_t)K * N));
+  TSPLAT_CHECK(check_dev(scale, (int64_t)N * 4));
+  TSPLAT_CHECK(check_dev(bias, (int64_t)N * 4));
+  TSPLAT_CHECK(check_dev(freqs, (int64_t)fb * L * C * 4));
+  TSPLAT_CHECK(check_dev(qg, C * 4));
+  TSPLAT_CHECK(check_dev(kg, C * 4));
+  TSPLAT_CHECK(check_dev(q, M * C * 4));
+  TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * Lp * 4));
+  TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lp * 4));
+  // RoPE, RMSNorm and the q / packed k,v stores run in the GEMM's epilogue.
+  QkvFusedParams p{{x, code01, q2, scale, bias, nullptr, (int)M, K, N, 0, N, K, N},
+                   freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb};
+  const int st = launch_nf24_gemm_qkv(p, stream);
+  if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
   return st;
 }
 

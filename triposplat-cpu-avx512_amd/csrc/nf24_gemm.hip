@@ -44,6 +44,18 @@ struct GemmCfg {
   static_assert(BK % 8 == 0 && BN % 2 == 0, "BK must be a multiple of 8, BN even");
 };
 
+// Fused QKV epilogue operands (kEpiQkv): rows are tokens b*L + l, columns
+// [q | k | v] with H heads of 64 each.
+struct QkvArgs {
+  const float* freqs;  // [fb, L, H, 64] interleaved (cos, sin)
+  const float* qg;     // [H, 64]
+  const float* kg;     // [H, 64]
+  float* q;            // [B, H, L, 64]
+  float* pk;           // [B, H, 64, Lpad]
+  float* pv;           // [B, H, 64, Lpad]
+  int L, H, Lpad, fb;
+};
+
 struct GemmArgs {
   const float* x;
   const int16_t* code01;
@@ -52,11 +64,115 @@ struct GemmArgs {
   const float* bias;
   float* out;
   int M, K, N, n_start, n_count, stride_x, stride_out;
+  QkvArgs e;
 };
+
+enum Epilogue : int { kEpiStore = 0, kEpiQkv = 1 };
+
+// Sum over the 32 lanes of a half-wave (lanes that hold one output row).
+__device__ __forceinline__ float sum32(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 8);
+  v += __shfl_xor(v, 16);
+  return v;
+}
+
+// QKV epilogue of one wave: its 64 columns are one head of q, k or v
+// (colw = first column, a multiple of 64); lane l32 holds dims l32 and
+// 32 + l32 of rows 8*(r/4) + 4*g + r%4 of each 32-row block.  q and k get
+// RoPE (the partner of dim 2i / 2i+1 is the neighbouring lane) then
+// y * 8 / max(||y||, 1e-12) * gamma, with ||y||^2 summed over the half-wave;
+// q is stored [B, H, L, 64], k and v key-contiguous [B, H, 64, Lpad] (four
+// consecutive tokens per 128-bit store when L % 4 == 0).  Same fmaf forms as
+// qkv_postprocess.hip; only the order of the 64-term sum of squares differs.
+template <class C>
+__device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, floatx16 (&acc)[C::kMB][C::kNB],
+                                             int row_base, int colw, int g, int l32) {
+  static_assert(C::kTN == 64 && C::kNB == 2, "the QKV epilogue needs one head per wave");
+  if (colw >= a.n_count) return;
+  const QkvArgs& e = a.e;
+  const int width = e.H * 64;
+  const int sec = colw / width;  // 0 q, 1 k, 2 v
+  const int h = (colw - sec * width) >> 6;
+  const bool odd = (l32 & 1) != 0;
+  float g0 = 1.0f, g1 = 1.0f;
+  if (sec < 2) {
+    const float* gp = (sec == 0 ? e.qg : e.kg) + h * 64;
+    g0 = gp[l32];
+    g1 = gp[32 + l32];
+  }
+#pragma unroll
+  for (int mb = 0; mb < C::kMB; ++mb) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row0 = row_base + mb * 32 + 8 * j + 4 * g;
+      floatx4 y0, y1;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        float v0 = acc[mb][0][4 * j + t];
+        float v1 = acc[mb][1][4 * j + t];
+        if (sec < 2) {  // uniform over the wave
+          const int row = row0 + t;
+          const bool valid = row < a.M;  // uniform over the half-wave
+          const int b = valid ? row / e.L : 0;
+          const int l = valid ? row - b * e.L : 0;
+          const float* fr =
+              e.freqs + (((int64_t)(e.fb == 1 ? 0 : b) * e.L + l) * e.H + h) * 64;
+          const float f0 = valid ? fr[l32] : 0.0f;
+          const float f1 = valid ? fr[32 + l32] : 0.0f;
+          const float p0 = __shfl_xor(v0, 1), p1 = __shfl_xor(v1, 1);
+          const float fp0 = __shfl_xor(f0, 1), fp1 = __shfl_xor(f1, 1);
+          const float r0 = odd ? fmaf(p0, f0, v0 * fp0) : fmaf(v0, f0, -(p0 * fp0));
+          const float r1 = odd ? fmaf(p1, f1, v1 * fp1) : fmaf(v1, f1, -(p1 * fp1));
+          const float ss = sum32(r0 * r0 + r1 * r1);
+          const float fac = 8.0f / fmaxf(sqrtf(ss), 1.0e-12f);
+          v0 = (r0 * fac) * g0;
+          v1 = (r1 * fac) * g1;
+        }
+        y0[t] = v0;
+        y1[t] = v1;
+      }
+      if (sec == 0) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int row = row0 + t;
+          if (row >= a.M) continue;
+          const int b = row / e.L, l = row - b * e.L;
+          float* dst = e.q + (((int64_t)b * e.H + h) * e.L + l) * 64;
+          dst[l32] = y0[t];
+          dst[32 + l32] = y1[t];
+        }
+      } else {
+        float* base = sec == 1 ? e.pk : e.pv;
+        const int64_t dim_stride = (int64_t)32 * e.Lpad;
+        if ((e.L & 3) == 0) {  // the four rows are four tokens of one sequence
+          if (row0 < a.M) {
+            const int b = row0 / e.L, l = row0 - b * e.L;
+            const int64_t off = (((int64_t)b * e.H + h) * 64 + l32) * e.Lpad + l;
+            *reinterpret_cast<floatx4*>(base + off) = y0;
+            *reinterpret_cast<floatx4*>(base + off + dim_stride) = y1;
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int row = row0 + t;
+            if (row >= a.M) continue;
+            const int b = row / e.L, l = row - b * e.L;
+            const int64_t off = (((int64_t)b * e.H + h) * 64 + l32) * e.Lpad + l;
+            base[off] = y0[t];
+            base[off + dim_stride] = y1[t];
+          }
+        }
+      }
+    }
+  }
+}
 
 // kVec: x rows 16-byte aligned with K % 4 == 0, and N, n_start, n_count even
 // (so a column pair is loaded with one 32-bit / 16-bit access).
-template <class C, bool kVec>
+template <class C, bool kVec, int kEpi>
 __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::kMinWaves)))
 void nf24_gemm_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) float xs[2][C::BM * C::kS];
@@ -211,6 +327,10 @@ void nf24_gemm_kernel(GemmArgs a) {
     __syncthreads();
   }
 
+  if constexpr (kEpi == kEpiQkv) {
+    qkv_epilogue<C>(a, acc, m0 + wm * C::kTM, c0 + wn * C::kTN, g, l32);
+    return;
+  }
 #pragma unroll
   for (int mb = 0; mb < C::kMB; ++mb)
 #pragma unroll
@@ -225,10 +345,10 @@ void nf24_gemm_kernel(GemmArgs a) {
     }
 }
 
-template <class C>
-int launch_cfg(const GemmParams& p, hipStream_t stream) {
+template <class C, int kEpi = kEpiStore>
+int launch_cfg(const GemmParams& p, hipStream_t stream, const QkvArgs& e = QkvArgs{}) {
   GemmArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out,
-             p.M, p.K, p.N, p.n_start, p.n_count, p.stride_x, p.stride_out};
+             p.M, p.K, p.N, p.n_start, p.n_count, p.stride_x, p.stride_out, e};
   const int64_t tiles = (int64_t)((p.M + C::BM - 1) / C::BM) * ((p.n_count + C::BN - 1) / C::BN);
   if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
   const bool vec = (reinterpret_cast<uintptr_t>(p.x) % 16 == 0) && (p.stride_x % 4 == 0) &&
@@ -237,10 +357,23 @@ int launch_cfg(const GemmParams& p, hipStream_t stream) {
                    (reinterpret_cast<uintptr_t>(p.q2) % 2 == 0);
   dim3 grid((unsigned)tiles), block(C::kThreads);
   if (vec)
-    hipLaunchKernelGGL((nf24_gemm_kernel<C, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((nf24_gemm_kernel<C, true, kEpi>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((nf24_gemm_kernel<C, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((nf24_gemm_kernel<C, false, kEpi>), grid, block, 0, stream, a);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// Packed k/v tokens L..Lpad-1 of every (b, h, dim) row are zero.
+constexpr int kTailThreads = 256;
+__global__ __launch_bounds__(kTailThreads) void packed_tail_zero_kernel(float* pk, float* pv,
+                                                                        int64_t rows, int L,
+                                                                        int Lpad) {
+  const int tail = Lpad - L;
+  const int64_t i = (int64_t)blockIdx.x * kTailThreads + threadIdx.x;
+  if (i >= rows * tail) return;
+  const int64_t off = (i / tail) * Lpad + L + i % tail;
+  pk[off] = 0.0f;
+  pv[off] = 0.0f;
 }
 
 // Tile configurations and the rates they sustain on MI355X when the grid is
@@ -276,21 +409,14 @@ int compute_units() {
   return cached[dev];
 }
 
-}  // namespace
-
-int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
-  // Few rows: the weight stream is the cost; the MFMA skinny tile only wins
-  // for 9..32 rows over a short K (measured at K = 256).
-  if (p.M <= 32) {
-    if (p.M > 8 && p.K <= 256) return launch_cfg<CfgSkinny>(p, stream);
-    return launch_nf24_gemv(p, stream);
-  }
+// Index into kChoices of the configuration with the smallest modelled time.
+int pick_config(int M, int n_count) {
   const int cus = compute_units();
   int best = 0;
   double best_t = 0.0;
   for (int i = 0; i < 3; ++i) {
     const Choice& c = kChoices[i];
-    const int64_t tiles = (int64_t)((p.M + c.bm - 1) / c.bm) * ((p.n_count + c.bn - 1) / c.bn);
+    const int64_t tiles = (int64_t)((M + c.bm - 1) / c.bm) * ((n_count + c.bn - 1) / c.bn);
     const int64_t slots = (int64_t)cus * c.wgs_per_cu;
     const int64_t full = tiles / slots;
     const int64_t rest = tiles - full * slots;
@@ -305,9 +431,43 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
       best_t = t;
     }
   }
+  return best;
+}
+
+}  // namespace
+
+int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
+  // Few rows: the weight stream is the cost; the MFMA skinny tile only wins
+  // for 9..32 rows over a short K (measured at K = 256).
+  if (p.M <= 32) {
+    if (p.M > 8 && p.K <= 256) return launch_cfg<CfgSkinny>(p, stream);
+    return launch_nf24_gemv(p, stream);
+  }
+  const int best = pick_config(p.M, p.n_count);
   if (best == 0) return launch_cfg<CfgLarge>(p, stream);
   if (best == 1) return launch_cfg<CfgWide>(p, stream);
   return launch_cfg<CfgSmall>(p, stream);
+}
+
+int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream) {
+  const GemmParams& gp = p.gemm;
+  if (gp.n_start != 0 || gp.n_count != gp.N || gp.N != 3 * p.H * 64 ||
+      (int64_t)p.B * p.L != gp.M || p.L_padded < p.L)
+    return kErrDims;
+  if (p.L_padded > p.L) {
+    const int64_t rows = (int64_t)p.B * p.H * 64;
+    const int64_t n = rows * (p.L_padded - p.L);
+    hipLaunchKernelGGL(packed_tail_zero_kernel,
+                       dim3((unsigned)((n + kTailThreads - 1) / kTailThreads)), dim3(kTailThreads),
+                       0, stream, p.packed_k, p.packed_v, rows, p.L, p.L_padded);
+    if (hipGetLastError() != hipSuccess) return kErrLaunch;
+  }
+  const QkvArgs e{p.freqs, p.q_gamma, p.k_gamma, p.q, p.packed_k, p.packed_v,
+                  p.L, p.H, p.L_padded, p.freq_batches};
+  const int best = pick_config(gp.M, gp.n_count);
+  if (best == 0) return launch_cfg<CfgLarge, kEpiQkv>(gp, stream, e);
+  if (best == 1) return launch_cfg<CfgWide, kEpiQkv>(gp, stream, e);
+  return launch_cfg<CfgSmall, kEpiQkv>(gp, stream, e);
 }
 
 }  // namespace tsplat

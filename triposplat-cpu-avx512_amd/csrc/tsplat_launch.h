@@ -54,6 +54,21 @@ struct QkvPostParams {
 };
 int launch_qkv_postprocess(const QkvPostParams& p, hipStream_t stream);
 
+// The NF24 projection x [B*L, K] -> [B*L, 3*H*64] with the postprocess
+// above applied in the GEMM's epilogue: no [B*L, 3*H*64] intermediate.
+// gemm.out is unused; gemm.M = B*L, gemm.N = gemm.n_count = 3*H*64.
+struct QkvFusedParams {
+  GemmParams gemm;
+  const float* freqs;
+  const float* q_gamma;
+  const float* k_gamma;
+  float* q;
+  float* packed_k;
+  float* packed_v;
+  int B, L, H, L_padded, freq_batches;
+};
+int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream);
+
 // NF24 packer: w [out_f, in_f] fp32 -> code01_t [in_f, out_f], q2_t, scale
 // [out_f]; base_tmp [out_f] receives max|w_row| / 127.
 int launch_nf24_pack(const float* w, int out_f, int in_f, const float* alphabet, int alphabet_len,
@@ -63,7 +78,7 @@ int launch_nf24_pack(const float* w, int out_f, int in_f, const float* alphabet,
 // Grow-only device scratch owned by the library, one buffer per (device,
 // stream, slot); null on allocation failure.  Valid until the next call with
 // the same key that asks for more bytes.
-enum WorkspaceSlot : int { kSlotGemvPartial = 0, kSlotQkvProjection = 1 };
+enum WorkspaceSlot : int { kSlotGemvPartial = 0 };
 void* stream_workspace(hipStream_t stream, size_t bytes, int slot);
 
 }  // namespace tsplat

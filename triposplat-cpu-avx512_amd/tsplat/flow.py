@@ -1,4 +1,4 @@
-"""Synthetic flow transformer (BASELINE configs 4 and 5) on the device.
+"""Synthetic flow transformer (benchmark configs 4 and 5) on the device.
 
 The upstream TripoSplat model is not available offline, so this module
 freezes a graph with the block structure of the reference's unified block
@@ -12,7 +12,7 @@ by the gfx950 GEMM; self attention uses the fused NF24 QKV projection +
 RoPE/RMSNorm/pack and the packed exact SDPA; elementwise work (LayerNorm,
 modulation, GELU, residuals, cross q/k RMSNorm) is torch on the device.
 
-Frozen choices (not pinned by the reference; recorded here and in DESIGN):
+Frozen choices (not pinned by the reference; recorded here):
   * LayerNorm eps 1e-6; norm1/norm3 without affine, the cross-attention
     norm with affine weight/bias; the final LayerNorm eps 1e-5
     (attention_patch.py:59);
