@@ -173,6 +173,106 @@ int tsplat_nf24_pack_async(const float* weight, int out_features, int in_feature
                            const float* alphabet, int alphabet_len, float* base_workspace,
                            int16_t* code01_t, int8_t* q2_t, float* scale, void* stream);
 
+/* ---------------- NF24 GEMM with an elementwise epilogue --------------- */
+
+/* The GEMM of tsplat_nf24_gemm_async with the block's next elementwise step
+ * applied to the result before it is stored (no counterpart symbol in the
+ * reference, which runs the two steps as separate calls; the elementwise
+ * arithmetic is that of the cited reference kernels, bit for bit):
+ *   epilogue 0: out = acc
+ *   epilogue 2: out = gelu_tanh(acc)            (native_gelu_avx512.c:44-68)
+ *   epilogue 3: out += acc * gate[(m / rows_per_batch) * gate_stride + n]
+ *                                   (native_block_elementwise_avx512.c:24-35)
+ *   epilogue 4: out += acc          (native_block_elementwise_avx512.c:37-46)
+ * acc includes the bias.  gate_stride >= N. */
+int tsplat_nf24_gemm_epilogue_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,
+                                    const float* scale, const float* bias, float* out, int M,
+                                    int K, int N, int output_start, int output_count,
+                                    int stride_x, int stride_out, int epilogue, const float* gate,
+                                    int64_t gate_stride, int rows_per_batch, void* stream);
+
+/* ---------------- flow-block elementwise -------------------------------- */
+/* Bit-identical per element to the reference kernels (same operation order,
+ * same fused multiply-adds, the reductions in the AVX-512 lane order). */
+
+/* scripts/native_norm_rope_avx512.c:13-49.  rows x cols, eps inside the
+ * sqrt; -3 if has_affine and weight/bias is null. */
+int triposplat_layernorm_f32_avx512(const float* input, const float* weight, const float* bias,
+                                    float* output, int64_t rows, int cols, float eps,
+                                    int has_affine, int threads);
+/* native_norm_rope_avx512.c:51-83.  [outer, heads, dim] * sqrt(dim) /
+ * max(||x||, eps) * gamma[heads, dim]. */
+int triposplat_multihead_rmsnorm_f32_avx512(const float* input, const float* gamma, float* output,
+                                            int64_t outer, int heads, int dim, float eps,
+                                            int threads);
+/* native_norm_rope_avx512.c:85-119.  Interleaved complex multiply; dim even;
+ * pointers 8-byte aligned (else -4). */
+int triposplat_rope_complex_f32_avx512(const float* input, const float* freqs_interleaved,
+                                       float* output, int64_t vectors, int dim, int threads);
+/* scripts/native_block_elementwise_avx512.c:9-22: h[b] = h[b] * (1 + scale[b]) + shift[b]. */
+int triposplat_modulate_inplace_f32_avx512(float* h, const float* scale, const float* shift,
+                                           int batch, int rows, int cols, int threads);
+/* native_block_elementwise_avx512.c:24-35: delta *= gate[b]; base += delta. */
+int triposplat_gated_residual_inplace_f32_avx512(float* base, float* delta, const float* gate,
+                                                 int batch, int rows, int cols, int threads);
+/* native_block_elementwise_avx512.c:37-46: base += delta. */
+int triposplat_add_inplace_f32_avx512(float* base, const float* delta, int64_t count,
+                                      int threads);
+/* scripts/native_gelu_avx512.c:44-68 (tanh form). */
+int triposplat_gelu_tanh_f32_avx512(const float* input, float* output, int64_t count,
+                                    int threads);
+/* scripts/native_silu_avx512_extra.c: x / (1 + exp(-x)). */
+int triposplat_silu_f32_avx512(const float* input, float* output, int64_t count, int threads);
+
+/* Asynchronous forms.  tsplat_layernorm_modulate_async fuses the modulation
+ * y * (1 + scale[b]) + shift[b] (b = row / rows_per_batch, scale/shift rows
+ * mod_batch_stride floats apart; both null for a plain LayerNorm).
+ * tsplat_head_rmsnorm_async normalises vectors (b, l, h) read at input +
+ * (b*L + l) * in_token_stride + h*dim into [B, L, H, dim] or, with out_bhld,
+ * [B, H, L, dim]; normalize = 0 only moves them. */
+int tsplat_layernorm_modulate_async(const float* input, const float* weight, const float* bias,
+                                    float* output, int64_t rows, int cols, float eps,
+                                    int has_affine, const float* scale, const float* shift,
+                                    int64_t mod_batch_stride, int64_t rows_per_batch,
+                                    void* stream);
+int tsplat_head_rmsnorm_async(const float* input, int64_t in_token_stride, const float* gamma,
+                              float* output, int B, int L, int H, int dim, float eps,
+                              int out_bhld, int normalize, void* stream);
+int tsplat_rope_complex_async(const float* input, const float* freqs_interleaved, float* output,
+                              int64_t vectors, int dim, void* stream);
+int tsplat_modulate_async(float* h, const float* scale, const float* shift, int batch, int rows,
+                          int cols, void* stream);
+int tsplat_gated_residual_async(float* base, float* delta, const float* gate, int batch, int rows,
+                                int cols, void* stream);
+int tsplat_add_async(float* base, const float* delta, int64_t count, void* stream);
+int tsplat_gelu_tanh_async(const float* input, float* output, int64_t count, void* stream);
+int tsplat_silu_async(const float* input, float* output, int64_t count, void* stream);
+
+/* ---------------- sampler ------------------------------------------------ */
+
+/* scripts/native_sampler_avx512.c:19-54: positive = g*positive - (g-1)*negative
+ * per batch (guidance [batch], a device array). */
+int triposplat_cfg_combine_inplace_f32_avx512(float* positive, const float* negative,
+                                              const float* guidance, int batch,
+                                              int64_t elements_per_batch, int threads);
+/* native_sampler_avx512.c:56-89: sample -= dt[b] * prediction. */
+int triposplat_euler_update_inplace_f32_avx512(float* sample, const float* prediction,
+                                               const float* dt, int batch,
+                                               int64_t elements_per_batch, int threads);
+/* native_sampler_avx512.c:91-134: second-order Adams-Bashforth update. */
+int triposplat_ab2_update_inplace_f32_avx512(float* sample, const float* prediction,
+                                             const float* previous_prediction, const float* dt,
+                                             const float* previous_dt, int batch,
+                                             int64_t elements_per_batch, int threads);
+int tsplat_cfg_combine_async(float* positive, const float* negative, const float* guidance,
+                             int batch, int64_t elements_per_batch, void* stream);
+int tsplat_euler_update_async(float* sample, const float* prediction, const float* dt, int batch,
+                              int64_t elements_per_batch, void* stream);
+int tsplat_ab2_update_async(float* sample, const float* prediction,
+                            const float* previous_prediction, const float* dt,
+                            const float* previous_dt, int batch, int64_t elements_per_batch,
+                            void* stream);
+
 /* ---------------- library ------------------------------------------------ */
 int tsplat_abi_version(void);         /* bumped on any ABI change */
 int tsplat_last_hip_error(void);      /* last hipError_t seen by this library */

@@ -3,11 +3,12 @@
 TEST INFRASTRUCTURE ONLY (tests/ and bench.py's cpu_baseline leg).  The graph
 is the one frozen in triposplat-cpu-avx512_amd/tsplat/flow.py; here every
 NF24 Linear, the fused QKV projection and both SDPAs run through the CPU
-kernels -- the oracle restatement (`backend="oracle"`, elementwise work in
-NumPy float32) or the reference's own AVX-512 build in oracle/_ref
-(`backend="reference"`: its NF24 GEMM, QKV-direct and SDPA kernels and its
-LayerNorm / modulate / gated-residual / GELU / SiLU / RMSNorm / CFG / Euler
-kernels, i.e. the repository's CPU pipeline).  Parameters come from
+kernels -- the oracle restatement (`backend="oracle"`) or the reference's own
+AVX-512 build in oracle/_ref (`backend="reference"`: its NF24 GEMM,
+QKV-direct and SDPA kernels and its LayerNorm / modulate / gated-residual /
+GELU / SiLU / RMSNorm / CFG / Euler kernels, i.e. the repository's CPU
+pipeline).  The elementwise restatements are bit-identical to the reference
+kernels, so the two backends differ only where the GEMM / SDPA do.  Parameters come from
 FlowModel.host(), so both sides use bit-identical packed weights.
 
 Model-level parity is "unpinned at the upstream boundary": the upstream
@@ -57,30 +58,13 @@ class CpuFlow:
         return O.sdpa_q8t512(q, k, v)
 
     # ---------------------------------------------------------- elementwise
-    @staticmethod
-    def layer_norm(x, eps, w=None, b=None):
-        x = x.astype(np.float32)
-        mean = x.mean(axis=-1, keepdims=True, dtype=np.float32)
-        d = x - mean
-        var = (d * d).mean(axis=-1, keepdims=True, dtype=np.float32)
-        y = d / np.sqrt(var + np.float32(eps))
-        if w is not None:
-            y = y * w + b
-        return y.astype(np.float32)
-
-    @staticmethod
-    def gelu_tanh(x):
-        c = np.float32(math.sqrt(2.0 / math.pi))
-        return (np.float32(0.5) * x * (np.float32(1.0) + np.tanh(c * (x + np.float32(0.044715) * x * x * x)))).astype(np.float32)
-
-    @staticmethod
-    def silu(x):
-        return (x / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
-
-    @staticmethod
-    def head_rmsnorm(y, gamma):
-        n = np.maximum(np.sqrt((y.astype(np.float64) ** 2).sum(-1, keepdims=True)), 1e-12).astype(np.float32)
-        return (y * (np.float32(8.0) / n) * gamma).astype(np.float32)
+    # LayerNorm / modulate / gated residual / add / GELU / SiLU / RMSNorm and
+    # the sampler updates: the oracle's C restatements (backend "oracle") or
+    # the reference's AVX-512 build (backend "reference") -- bit-identical.
+    def _ew(self, op, *args):
+        st = O.ew(op, *args, backend=self.backend, threads=self.threads)
+        if st != 0:
+            raise RuntimeError(f"{op} status {st}")
 
     def freqs(self, L):
         H = self.cfg.heads
@@ -99,38 +83,49 @@ class CpuFlow:
         return t_emb, t_mod
 
     # ---------------------------------------------------------- graph
-    # Elementwise dispatch: NumPy fp32 for the oracle backend, the reference's
-    # own AVX-512 kernels for the reference backend.
     def _ln(self, x, eps, w=None, b=None):
-        if self.backend == "reference":
-            return O.ref_layernorm(x, eps, w, b, self.threads)
-        return self.layer_norm(x, eps, w, b)
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        cols = x.shape[-1]
+        self._ew("layernorm", x, None if w is None else np.ascontiguousarray(w, np.float32),
+                 None if b is None else np.ascontiguousarray(b, np.float32), out, x.size // cols, cols,
+                 np.float32(eps), int(w is not None))
+        return out
 
     def _modulate(self, h, scale, shift):
-        if self.backend == "reference":
-            return O.ref_modulate_inplace(h, scale, shift, self.threads)
-        return (h * (np.float32(1) + scale[:, None, :]) + shift[:, None, :]).astype(np.float32)
+        B, L, C = h.shape
+        self._ew("modulate_inplace", h, np.ascontiguousarray(scale), np.ascontiguousarray(shift), B, L, C)
+        return h
 
     def _gated(self, x, h, gate):
-        if self.backend == "reference":
-            return O.ref_gated_residual_inplace(x, np.ascontiguousarray(h), gate, self.threads)
-        return (x + gate[:, None, :] * h).astype(np.float32)
+        B, L, C = x.shape
+        self._ew("gated_residual_inplace", x, np.ascontiguousarray(h, np.float32),
+                 np.ascontiguousarray(gate), B, L, C)
+        return x
 
     def _add(self, x, d):
-        if self.backend == "reference":
-            return O.ref_add_inplace(x, d, self.threads)
-        return (x + d).astype(np.float32)
+        self._ew("add_inplace", x, np.ascontiguousarray(d, np.float32), x.size)
+        return x
 
     def _gelu(self, x):
-        return O.ref_gelu_tanh(x, self.threads) if self.backend == "reference" else self.gelu_tanh(x)
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        self._ew("gelu_tanh", x, out, x.size)
+        return out
 
     def _silu(self, x):
-        return O.ref_silu(x, self.threads) if self.backend == "reference" else self.silu(x)
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        self._ew("silu", x, out, x.size)
+        return out
 
     def _rmsnorm(self, y, gamma):
-        if self.backend == "reference":
-            return O.ref_multihead_rmsnorm(y, gamma, 1e-12, self.threads)
-        return self.head_rmsnorm(y, gamma)
+        y = np.ascontiguousarray(y, np.float32)
+        out = np.empty_like(y)
+        H, D = gamma.shape
+        self._ew("multihead_rmsnorm", y, np.ascontiguousarray(gamma), out, y.size // (H * D), H, D,
+                 np.float32(1e-12))
+        return out
 
     def block(self, bp, x, cond, t_mod):
         cfg = self.cfg
@@ -180,11 +175,12 @@ class CpuFlow:
         t = np.full(2, ts[step] * 1000.0, np.float32)
         dt = np.float32(ts[step] - ts[step + 1])
         v = self.velocity(np.stack((z, z)), np.stack((cond, np.zeros_like(cond))), t)
-        if self.backend == "reference":
-            return O.ref_cfg_euler(z, v[0], v[1], self.cfg.guidance, float(dt), self.threads)
-        g = np.float32(self.cfg.guidance)
-        v_cfg = (g * v[0] - (g - np.float32(1)) * v[1]).astype(np.float32)
-        return (z - dt * v_cfg).astype(np.float32), v_cfg
+        v_cfg = np.ascontiguousarray(v[0])
+        self._ew("cfg_combine_inplace", v_cfg, np.ascontiguousarray(v[1]),
+                 np.array([self.cfg.guidance], np.float32), 1, v_cfg.size)
+        z_next = np.array(z, np.float32, copy=True)
+        self._ew("euler_update_inplace", z_next, v_cfg, np.array([dt], np.float32), 1, z_next.size)
+        return z_next, v_cfg
 
 
 def combined_rmse(a, b):

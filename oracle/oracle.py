@@ -482,3 +482,70 @@ def ref_cfg_euler(z, v_pos, v_neg, guidance, dt, threads=0):
     if st != 0:
         raise RuntimeError(f"reference euler status {st}")
     return out, pos
+
+
+# --------------------------------------------------------------------------
+# Flow-block and sampler elementwise ops: the oracle restatements
+# (tsplat_oracle.c, backend="oracle") and the reference build
+# (oracle/_ref, backend="reference") behind one calling convention -- the
+# reference's C argument list without the trailing `threads`.
+_EW_OPS = {
+    "layernorm": ("libref_norm_rope.so", "triposplat_layernorm_f32_avx512",
+                  [_vp] * 4 + [ctypes.c_int64, _i, ctypes.c_float, _i]),
+    "multihead_rmsnorm": ("libref_norm_rope.so", "triposplat_multihead_rmsnorm_f32_avx512",
+                          [_vp] * 3 + [ctypes.c_int64, _i, _i, ctypes.c_float]),
+    "rope_complex": ("libref_norm_rope.so", "triposplat_rope_complex_f32_avx512",
+                     [_vp] * 3 + [ctypes.c_int64, _i]),
+    "modulate_inplace": ("libref_block_elementwise.so", "triposplat_modulate_inplace_f32_avx512",
+                         [_vp] * 3 + [_i] * 3),
+    "gated_residual_inplace": ("libref_block_elementwise.so",
+                               "triposplat_gated_residual_inplace_f32_avx512", [_vp] * 3 + [_i] * 3),
+    "add_inplace": ("libref_block_elementwise.so", "triposplat_add_inplace_f32_avx512",
+                    [_vp] * 2 + [ctypes.c_int64]),
+    "gelu_tanh": ("libref_activations.so", "triposplat_gelu_tanh_f32_avx512", [_vp] * 2 + [ctypes.c_int64]),
+    "silu": ("libref_activations.so", "triposplat_silu_f32_avx512", [_vp] * 2 + [ctypes.c_int64]),
+    "cfg_combine_inplace": ("libref_sampler.so", "triposplat_cfg_combine_inplace_f32_avx512",
+                            [_vp] * 3 + [_i, ctypes.c_int64]),
+    "euler_update_inplace": ("libref_sampler.so", "triposplat_euler_update_inplace_f32_avx512",
+                             [_vp] * 3 + [_i, ctypes.c_int64]),
+    "ab2_update_inplace": ("libref_sampler.so", "triposplat_ab2_update_inplace_f32_avx512",
+                           [_vp] * 5 + [_i, ctypes.c_int64]),
+}
+EW_OPS = tuple(_EW_OPS)
+_EW_FNS = {}
+
+
+def _ew_fn(op, backend):
+    key = (op, backend)
+    if key not in _EW_FNS:
+        lib_name, sym, argtypes = _EW_OPS[op]
+        if backend == "oracle":
+            fn = getattr(lib(), "oracle_" + op)
+            fn.argtypes = argtypes
+        elif backend == "reference":
+            fn = getattr(ref_lib(lib_name), sym)
+            fn.argtypes = argtypes + [_i]
+        else:
+            raise ValueError(backend)
+        fn.restype = _i
+        _EW_FNS[key] = fn
+    return _EW_FNS[key]
+
+
+def ew(op, *args, backend="oracle", threads=0):
+    """Run one block/sampler op in place on NumPy arrays and return its status.
+
+    ``args`` follow the reference's C signature without ``threads``: arrays
+    (contiguous fp32, None for a null pointer) then the integer / float
+    arguments.  Outputs are written into the arrays passed.
+    """
+    conv = []
+    for a in args:
+        if isinstance(a, np.ndarray):
+            if a.dtype != np.float32 or not a.flags.c_contiguous:
+                raise ValueError("ew arrays must be contiguous float32")
+            conv.append(_ptr(a))
+        else:
+            conv.append(a)
+    fn = _ew_fn(op, backend)
+    return int(fn(*conv, threads) if backend == "reference" else fn(*conv))

@@ -19,6 +19,17 @@
  *   scripts/native_sdpa_avx512_exact_q8t512_packed.c  packed-K/V, BLHD out
  *   scripts/native_qkv_postprocess_v2_avx512.c RoPE -> RMSNorm -> pack
  *   scripts/gemm_nf24_qkv_direct_avx512.c     fused QKV GEMM + postprocess
+ *   scripts/native_norm_rope_avx512.c         LayerNorm, multi-head RMSNorm, RoPE
+ *   scripts/native_block_elementwise_avx512.c modulate, gated residual, add
+ *   scripts/native_gelu_avx512.c, native_silu_avx512_extra.c  activations
+ *   scripts/native_sampler_avx512.c           CFG combine, Euler, AB2
+ *
+ * The reference builds its elementwise kernels with gcc -O3 -mfma and the
+ * default -ffp-contract=fast, under which GCC fuses a multiply whose only
+ * use is an add (native_block_elementwise_avx512.c's modulate, the
+ * x + 0.044715 x^3 of the GELU); those fusions are written out below and
+ * were confirmed against the _ref build.  The sampler is built with
+ * -ffp-contract=off and has none.
  *
  * Pinning (how each function is checked, beyond retyping):
  *   - bit-exact against the reference C compiled from its own sources into
@@ -365,6 +376,194 @@ int oracle_gemm_nf24_qkv_direct(const float* x, const int16_t* code01_t, const i
                                       L, H, D, L_padded, frequency_batches);
   free(qkv);
   return st;
+}
+
+/* ------------------------------------------------------------------ */
+/* Flow-block elementwise kernels.  A row is processed as the reference's
+ * 16-lane vectors: lane j accumulates columns j, j+16, ... sequentially and
+ * the lanes are combined by reduce_add16; masked lanes read 0. */
+
+/* scripts/native_norm_rope_avx512.c:13-49.  The variance pass subtracts the
+ * mean from every lane of every 16-column chunk, so masked lanes of a
+ * partial last chunk contribute mean^2 (as the reference does). */
+int oracle_layernorm(const float* input, const float* weight, const float* bias, float* output,
+                     int64_t rows, int cols, float eps, int has_affine) {
+  if (input == 0 || output == 0) return -1;
+  if (rows <= 0 || cols <= 0 || eps < 0.0f) return -2;
+  if (has_affine && (weight == 0 || bias == 0)) return -3;
+  for (int64_t row = 0; row < rows; ++row) {
+    const float* src = input + row * (int64_t)cols;
+    float* dst = output + row * (int64_t)cols;
+    float acc[OR_LANES] = {0};
+    for (int col = 0; col < cols; col += OR_LANES)
+      for (int j = 0; j < OR_LANES; ++j) acc[j] += (col + j < cols) ? src[col + j] : 0.0f;
+    const float mean = reduce_add16(acc) / (float)cols;
+    float var[OR_LANES] = {0};
+    for (int col = 0; col < cols; col += OR_LANES)
+      for (int j = 0; j < OR_LANES; ++j) {
+        const float d = ((col + j < cols) ? src[col + j] : 0.0f) - mean;
+        var[j] = fmaf(d, d, var[j]);
+      }
+    const float inv_std = 1.0f / sqrtf(reduce_add16(var) / (float)cols + eps);
+    for (int c = 0; c < cols; ++c) {
+      float y = (src[c] - mean) * inv_std;
+      if (has_affine) y = fmaf(y, weight[c], bias[c]);
+      dst[c] = y;
+    }
+  }
+  return 0;
+}
+
+/* native_norm_rope_avx512.c:51-83: x * (sqrt(dim) / max(||x||, eps)) * gamma[h]. */
+int oracle_multihead_rmsnorm(const float* input, const float* gamma, float* output, int64_t outer,
+                             int heads, int dim, float eps) {
+  if (input == 0 || gamma == 0 || output == 0) return -1;
+  if (outer <= 0 || heads <= 0 || dim <= 0 || eps < 0.0f) return -2;
+  for (int64_t vec = 0; vec < outer * heads; ++vec) {
+    const float* src = input + vec * dim;
+    const float* g = gamma + (int64_t)(vec % heads) * dim;
+    float* dst = output + vec * dim;
+    float acc[OR_LANES] = {0};
+    for (int d = 0; d < dim; d += OR_LANES)
+      for (int j = 0; j < OR_LANES; ++j) {
+        const float x = (d + j < dim) ? src[d + j] : 0.0f;
+        acc[j] = fmaf(x, x, acc[j]);
+      }
+    const float norm = sqrtf(reduce_add16(acc));
+    const float factor = sqrtf((float)dim) / fmaxf(norm, eps);
+    for (int d = 0; d < dim; ++d) dst[d] = (src[d] * factor) * g[d];
+  }
+  return 0;
+}
+
+/* native_norm_rope_avx512.c:85-119: fmaddsub(x_re, f, x_im * swap(f)). */
+int oracle_rope_complex(const float* input, const float* freqs, float* output, int64_t vectors,
+                        int dim) {
+  if (input == 0 || freqs == 0 || output == 0) return -1;
+  if (vectors <= 0 || dim <= 0 || (dim & 1) != 0) return -2;
+  for (int64_t i = 0; i < vectors * dim; i += 2) {
+    const float re = input[i], im = input[i + 1], c = freqs[i], s = freqs[i + 1];
+    output[i] = fmaf(re, c, -(im * s));
+    output[i + 1] = fmaf(re, s, im * c);
+  }
+  return 0;
+}
+
+/* native_block_elementwise_avx512.c:9-22: h * (1 + scale) + shift, one fma. */
+int oracle_modulate_inplace(float* h, const float* scale, const float* shift, int batch, int rows,
+                            int cols) {
+  if (!h || !scale || !shift) return -1;
+  if (batch <= 0 || rows <= 0 || cols <= 0) return -2;
+  for (int64_t r = 0; r < (int64_t)batch * rows; ++r) {
+    const int64_t b = r / rows;
+    float* dst = h + r * cols;
+    for (int c = 0; c < cols; ++c)
+#ifndef ORACLE_EW_UNFUSED
+      dst[c] = fmaf(dst[c], 1.0f + scale[b * cols + c], shift[b * cols + c]);
+#else /* planted mistake for the tests: the contracted fma written unfused */
+      dst[c] = dst[c] * (1.0f + scale[b * cols + c]) + shift[b * cols + c];
+#endif
+  }
+  return 0;
+}
+
+/* native_block_elementwise_avx512.c:24-35: delta *= gate; base += delta. */
+int oracle_gated_residual_inplace(float* base, float* delta, const float* gate, int batch,
+                                  int rows, int cols) {
+  if (!base || !delta || !gate) return -1;
+  if (batch <= 0 || rows <= 0 || cols <= 0) return -2;
+  for (int64_t r = 0; r < (int64_t)batch * rows; ++r) {
+    const float* g = gate + (r / rows) * cols;
+    for (int c = 0; c < cols; ++c) {
+      const float hv = delta[r * cols + c] * g[c];
+      delta[r * cols + c] = hv;
+      base[r * cols + c] = base[r * cols + c] + hv;
+    }
+  }
+  return 0;
+}
+
+/* native_block_elementwise_avx512.c:37-46. */
+int oracle_add_inplace(float* base, const float* delta, int64_t count) {
+  if (!base || !delta) return -1;
+  if (count <= 0) return -2;
+  for (int64_t i = 0; i < count; ++i) base[i] = base[i] + delta[i];
+  return 0;
+}
+
+/* native_gelu_avx512.c:33-68: 0.5x (1 + tanh(0.79788456 (x + 0.044715 x^3)))
+ * with tanh(u) = sign(u) (1 - 2 / (exp512(2|u|) + 1)), 0 at u = 0; the
+ * x + 0.044715 x^3 is one fma in the reference build. */
+static inline float gelu_tanh_lane(float x) {
+  const float x2 = x * x;
+#ifndef ORACLE_EW_UNFUSED
+  const float s = fmaf(0.044715f, x2 * x, x);
+#else /* planted mistake for the tests */
+  const float s = x + 0.044715f * (x2 * x);
+#endif
+  const float inner = 0.7978845608028654f * s;
+  const float e = exp512_lane(2.0f * fabsf(inner));
+  float t = 1.0f - 2.0f / (e + 1.0f);
+  t = copysignf(t, inner);
+  if (inner == 0.0f) t = 0.0f;
+  return (0.5f * x) * (1.0f + t);
+}
+
+int oracle_gelu_tanh(const float* input, float* output, int64_t count) {
+  if (input == 0 || output == 0) return -1;
+  if (count <= 0) return -2;
+  for (int64_t i = 0; i < count; ++i) output[i] = gelu_tanh_lane(input[i]);
+  return 0;
+}
+
+/* native_silu_avx512_extra.c:28-45: x / (1 + exp512(0 - x)). */
+int oracle_silu(const float* input, float* output, int64_t count) {
+  if (input == 0 || output == 0) return -1;
+  if (count <= 0) return -2;
+  for (int64_t i = 0; i < count; ++i) output[i] = input[i] / (1.0f + exp512_lane(0.0f - input[i]));
+  return 0;
+}
+
+/* native_sampler_avx512.c:19-54: positive = g * positive - (g - 1) * negative. */
+int oracle_cfg_combine_inplace(float* positive, const float* negative, const float* guidance,
+                               int batch, int64_t per_batch) {
+  if (!positive || !negative || !guidance) return -1;
+  if (batch <= 0 || per_batch <= 0) return -2;
+  for (int b = 0; b < batch; ++b) {
+    const float g = guidance[b], gm1 = g - 1.0f;
+    for (int64_t i = (int64_t)b * per_batch; i < (int64_t)(b + 1) * per_batch; ++i)
+      positive[i] = g * positive[i] - gm1 * negative[i];
+  }
+  return 0;
+}
+
+/* native_sampler_avx512.c:56-89: sample -= dt * prediction. */
+int oracle_euler_update_inplace(float* sample, const float* prediction, const float* dt, int batch,
+                                int64_t per_batch) {
+  if (!sample || !prediction || !dt) return -1;
+  if (batch <= 0 || per_batch <= 0) return -2;
+  for (int b = 0; b < batch; ++b)
+    for (int64_t i = (int64_t)b * per_batch; i < (int64_t)(b + 1) * per_batch; ++i)
+      sample[i] = sample[i] - dt[b] * prediction[i];
+  return 0;
+}
+
+/* native_sampler_avx512.c:91-134: with r = 0.5 * dt / max(prev_dt, 1e-12),
+ * sample -= dt * ((1 + r) * prediction - r * previous_prediction). */
+int oracle_ab2_update_inplace(float* sample, const float* prediction, const float* previous,
+                              const float* dt, const float* previous_dt, int batch,
+                              int64_t per_batch) {
+  if (!sample || !prediction || !previous || !dt || !previous_dt) return -1;
+  if (batch <= 0 || per_batch <= 0) return -2;
+  for (int b = 0; b < batch; ++b) {
+    const float r = 0.5f * (dt[b] / fmaxf(previous_dt[b], 1.0e-12f));
+    const float cs = 1.0f + r;
+    for (int64_t i = (int64_t)b * per_batch; i < (int64_t)(b + 1) * per_batch; ++i) {
+      const float eff = cs * prediction[i] - r * previous[i];
+      sample[i] = sample[i] - dt[b] * eff;
+    }
+  }
+  return 0;
 }
 
 int oracle_threads(void) {

@@ -4,9 +4,10 @@
 Runs only where the reference sources are mounted: `make -C oracle` compiles
 them (scripts/gemm_nf24_i16_avx512.c + _tail.c,
 native_sdpa_avx512_exact_q8t512.c, native_sdpa_avx512_exact_q8t512_packed.c,
-native_qkv_postprocess_v2_avx512.c, gemm_nf24_qkv_direct_avx512.c) into
-oracle/_ref/, and this script calls those builds through ctypes on small
-seeded inputs.  Each .npz holds the inputs and the reference's outputs; the
+native_qkv_postprocess_v2_avx512.c, gemm_nf24_qkv_direct_avx512.c, and the
+block / sampler elementwise kernels) into oracle/_ref/, and this script calls
+those builds through ctypes on small seeded inputs.  `make_golden.py NAME...`
+rewrites only the named fixtures.  Each .npz holds the inputs and the reference's outputs; the
 tests check the oracle against them bit for bit.  The weight codes come from
 the oracle's NumPy packer (a fixture input, not a reference output).
 """
@@ -95,9 +96,30 @@ def main():
     out["qkv_direct_1x17x2_k128"] = dict(x=x, code01_t=c01, q2_t=q2, scale=s, bias=b, freqs=fr,
                                          q_gamma=qg, k_gamma=kg, q=qo, packed_k=pko, packed_v=pvo)
 
+    ew = ew_fixture()
+    out["ew_ops"] = ew
+    only = set(sys.argv[1:])
     for name, arrays in out.items():
+        if only and name not in only:
+            continue
         np.savez(HERE / f"{name}.npz", **arrays)
-        print(name, {k: tuple(v.shape) for k, v in arrays.items()})
+        print(name, len(arrays), "arrays")
+
+
+def ew_fixture():
+    """Flow-block / sampler ops (tests/_ew_cases.py) through the reference
+    build: keys '<case>/in/<array>' and '<case>/out/<array>'."""
+    sys.path.insert(0, str(HERE.parent))
+    import _ew_cases as EC
+
+    arrays = {}
+    for name, case in EC.cases().items():
+        for k, v in case[1].items():
+            arrays[f"{name}/in/{k}"] = v
+        got = EC.run(O, case, backend="reference")
+        for k in case[3]:
+            arrays[f"{name}/out/{k}"] = got[k]
+    return arrays
 
 
 if __name__ == "__main__":

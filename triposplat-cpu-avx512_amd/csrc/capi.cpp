@@ -11,18 +11,13 @@
 
 #include "tsplat_common.h"
 #include "tsplat_launch.h"
+#include "capi_internal.h"
 #include "../../include/tsplat_hip.h"
 
-using namespace tsplat;
-
+namespace tsplat {
 namespace {
-
-constexpr int kHeadDim = 64;
-constexpr int kAbiVersion = 1;
-
 std::atomic<int> g_last_hip_error{0};
-std::atomic<uint64_t> g_sdpa_calls{0};
-std::atomic<uint64_t> g_sdpa_ns{0};
+}  // namespace
 
 int note(hipError_t e) {
   if (e != hipSuccess) g_last_hip_error.store((int)e);
@@ -57,15 +52,21 @@ int check_dev(const void* p, int64_t bytes) {
   return kOk;
 }
 
-#define TSPLAT_CHECK(expr)        \
-  do {                            \
-    const int st_ = (expr);       \
-    if (st_ != kOk) return st_;   \
-  } while (0)
-
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int sync_null_stream() { return note(hipStreamSynchronize(nullptr)); }
+
+}  // namespace tsplat
+
+using namespace tsplat;
+
+namespace {
+
+constexpr int kHeadDim = 64;
+constexpr int kAbiVersion = 1;
+
+std::atomic<uint64_t> g_sdpa_calls{0};
+std::atomic<uint64_t> g_sdpa_ns{0};
 
 // ---------------------------------------------------------------- GEMM
 int gemm_checked(const float* x, const int16_t* code01, const int8_t* q2, const float* scale,

@@ -20,6 +20,7 @@
 // of the current step run (double-buffered LDS, one barrier per step).
 
 #include "tsplat_common.h"
+#include "tsplat_ew.h"
 #include "tsplat_launch.h"
 
 namespace tsplat {
@@ -65,9 +66,14 @@ struct GemmArgs {
   float* out;
   int M, K, N, n_start, n_count, stride_x, stride_out;
   QkvArgs e;
+  // kEpilogueGated: gate row of batch m / rows_per_batch
+  const float* gate;
+  int64_t gate_stride;
+  int rows_per_batch;
 };
 
-enum Epilogue : int { kEpiStore = 0, kEpiQkv = 1 };
+// kEpilogue* of tsplat_launch.h, plus the fused QKV epilogue.
+enum Epilogue : int { kEpiStore = kEpilogueStore, kEpiQkv = 1 };
 
 // Sum over the 32 lanes of a half-wave (lanes that hold one output row).
 __device__ __forceinline__ float sum32(float v) {
@@ -340,15 +346,31 @@ void nf24_gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm * C::kTM + mb * 32 + 8 * (r / 4) + 4 * g + (r % 4);
-        if (row < a.M) a.out[(int64_t)row * a.stride_out + col] = acc[mb][nb][r];
+        if (row >= a.M) continue;
+        float* dst = a.out + (int64_t)row * a.stride_out + col;
+        const float v = acc[mb][nb][r];
+        if constexpr (kEpi == kEpilogueGelu) {
+          *dst = gelu_tanh_ref(v);
+        } else if constexpr (kEpi == kEpilogueGated) {
+          // h = acc * gate, x = x + h: two roundings, as the reference's
+          // native_block_elementwise_avx512.c:24-35
+          const float* gate = a.gate + (int64_t)(row / a.rows_per_batch) * a.gate_stride;
+          *dst = gated_residual_ref(*dst, v, gate[a.n_start + col]);
+        } else if constexpr (kEpi == kEpilogueAdd) {
+          *dst = *dst + v;
+        } else {
+          *dst = v;
+        }
       }
     }
 }
 
 template <class C, int kEpi = kEpiStore>
-int launch_cfg(const GemmParams& p, hipStream_t stream, const QkvArgs& e = QkvArgs{}) {
+int launch_cfg(const GemmParams& p, hipStream_t stream, const QkvArgs& e = QkvArgs{},
+               const GemmEpilogueParams& ep = GemmEpilogueParams{kEpilogueStore, nullptr, 0, 1}) {
   GemmArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out,
-             p.M, p.K, p.N, p.n_start, p.n_count, p.stride_x, p.stride_out, e};
+             p.M, p.K, p.N, p.n_start, p.n_count, p.stride_x, p.stride_out, e,
+             ep.gate, ep.gate_stride, ep.rows_per_batch};
   const int64_t tiles = (int64_t)((p.M + C::BM - 1) / C::BM) * ((p.n_count + C::BN - 1) / C::BN);
   if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
   const bool vec = (reinterpret_cast<uintptr_t>(p.x) % 16 == 0) && (p.stride_x % 4 == 0) &&
@@ -447,6 +469,30 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
   if (best == 0) return launch_cfg<CfgLarge>(p, stream);
   if (best == 1) return launch_cfg<CfgWide>(p, stream);
   return launch_cfg<CfgSmall>(p, stream);
+}
+
+namespace {
+template <int kEpi>
+int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_t stream) {
+  // Few rows go to the 128x128 tile: the epilogue lives in the MFMA kernels.
+  const int best = p.M <= 32 ? 2 : pick_config(p.M, p.n_count);
+  if (best == 0) return launch_cfg<CfgLarge, kEpi>(p, stream, QkvArgs{}, e);
+  if (best == 1) return launch_cfg<CfgWide, kEpi>(p, stream, QkvArgs{}, e);
+  return launch_cfg<CfgSmall, kEpi>(p, stream, QkvArgs{}, e);
+}
+}  // namespace
+
+int launch_nf24_gemm_epilogue(const GemmParams& p, const GemmEpilogueParams& e,
+                              hipStream_t stream) {
+  switch (e.kind) {
+    case kEpilogueStore: return launch_nf24_gemm(p, stream);
+    case kEpilogueGelu: return launch_epi_kind<kEpilogueGelu>(p, e, stream);
+    case kEpilogueGated:
+      if (e.gate == nullptr || e.rows_per_batch <= 0) return kErrDims;
+      return launch_epi_kind<kEpilogueGated>(p, e, stream);
+    case kEpilogueAdd: return launch_epi_kind<kEpilogueAdd>(p, e, stream);
+    default: return kErrDims;
+  }
 }
 
 int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream) {

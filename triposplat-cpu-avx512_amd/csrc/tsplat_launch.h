@@ -69,6 +69,74 @@ struct QkvFusedParams {
 };
 int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream);
 
+// NF24 GEMM with an elementwise epilogue on out[m, c] (same GEMM as
+// launch_nf24_gemm; bias included before the epilogue):
+//   kEpilogueGelu:   out = gelu_tanh(acc)
+//   kEpilogueGated:  out = out + acc * gate[(m / rows_per_batch) * gate_stride + n_start + c]
+//   kEpilogueAdd:    out = out + acc
+// (out is read and written in place for the last two.)
+enum GemmEpilogue : int { kEpilogueStore = 0, kEpilogueGelu = 2, kEpilogueGated = 3, kEpilogueAdd = 4 };
+struct GemmEpilogueParams {
+  int kind;
+  const float* gate;
+  int64_t gate_stride;
+  int rows_per_batch;
+};
+int launch_nf24_gemm_epilogue(const GemmParams& p, const GemmEpilogueParams& e,
+                              hipStream_t stream);
+
+// LayerNorm over rows of `cols` (eps inside the sqrt), optional affine
+// (weight, bias [cols]) and modulation y * (1 + scale[b]) + shift[b] with
+// b = row / rows_per_batch and scale/shift rows mod_batch_stride apart.
+struct LayerNormParams {
+  const float* input;
+  const float* weight;
+  const float* bias;
+  float* output;
+  int64_t rows;
+  int cols;
+  float eps;
+  int affine;
+  int modulate;
+  const float* scale;
+  const float* shift;
+  int64_t mod_batch_stride;
+  int64_t rows_per_batch;
+};
+int launch_layernorm(const LayerNormParams& p, hipStream_t stream);
+
+// Per-head RMSNorm x * sqrt(dim) / max(||x||, eps) * gamma[h] of vectors
+// (b, l, h) read at input + (b*L + l) * in_token_stride + h*dim; output
+// [B, L, H, dim] or [B, H, L, dim] (out_bhld); normalize = 0 copies.
+struct HeadNormParams {
+  const float* input;
+  const float* gamma;
+  float* output;
+  int B, L, H, dim;
+  int64_t in_token_stride;
+  float eps;
+  int out_bhld;
+  int normalize;
+};
+int launch_head_rmsnorm(const HeadNormParams& p, hipStream_t stream);
+
+int launch_rope_complex(const float* in, const float* freqs, float* out, int64_t pairs,
+                        hipStream_t stream);
+int launch_modulate(float* h, const float* scale, const float* shift, int batch, int rows, int cols,
+                    hipStream_t stream);
+int launch_gated_residual(float* base, float* delta, const float* gate, int batch, int rows,
+                          int cols, hipStream_t stream);
+int launch_add(float* base, const float* delta, int64_t count, hipStream_t stream);
+int launch_gelu_tanh(const float* in, float* out, int64_t count, hipStream_t stream);
+int launch_silu(const float* in, float* out, int64_t count, hipStream_t stream);
+int launch_cfg_combine(float* positive, const float* negative, const float* guidance, int batch,
+                       int64_t per_batch, hipStream_t stream);
+int launch_euler_update(float* sample, const float* prediction, const float* dt, int batch,
+                        int64_t per_batch, hipStream_t stream);
+int launch_ab2_update(float* sample, const float* prediction, const float* previous_prediction,
+                      const float* dt, const float* previous_dt, int batch, int64_t per_batch,
+                      hipStream_t stream);
+
 // NF24 packer: w [out_f, in_f] fp32 -> code01_t [in_f, out_f], q2_t, scale
 // [out_f]; base_tmp [out_f] receives max|w_row| / 127.
 int launch_nf24_pack(const float* w, int out_f, int in_f, const float* alphabet, int alphabet_len,

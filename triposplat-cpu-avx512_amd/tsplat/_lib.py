@@ -44,6 +44,30 @@ SIGNATURES = {
     "tsplat_qkv_postprocess_async": ([_vp] * 7 + [_i] * 6 + [_vp], _i),
     "tsplat_gemm_nf24_qkv_direct_async": ([_vp] * 11 + [_i] * 8 + [_vp], _i),
     "tsplat_nf24_pack_async": ([_vp, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp], _i),
+    "tsplat_nf24_gemm_epilogue_async": ([_vp] * 6 + [_i] * 8 + [_vp, _i64, _i, _vp], _i),
+    "triposplat_layernorm_f32_avx512": ([_vp] * 4 + [_i64, _i, ctypes.c_float, _i, _i], _i),
+    "triposplat_multihead_rmsnorm_f32_avx512": ([_vp] * 3 + [_i64, _i, _i, ctypes.c_float, _i], _i),
+    "triposplat_rope_complex_f32_avx512": ([_vp] * 3 + [_i64, _i, _i], _i),
+    "triposplat_modulate_inplace_f32_avx512": ([_vp] * 3 + [_i] * 4, _i),
+    "triposplat_gated_residual_inplace_f32_avx512": ([_vp] * 3 + [_i] * 4, _i),
+    "triposplat_add_inplace_f32_avx512": ([_vp] * 2 + [_i64, _i], _i),
+    "triposplat_gelu_tanh_f32_avx512": ([_vp] * 2 + [_i64, _i], _i),
+    "triposplat_silu_f32_avx512": ([_vp] * 2 + [_i64, _i], _i),
+    "triposplat_cfg_combine_inplace_f32_avx512": ([_vp] * 3 + [_i, _i64, _i], _i),
+    "triposplat_euler_update_inplace_f32_avx512": ([_vp] * 3 + [_i, _i64, _i], _i),
+    "triposplat_ab2_update_inplace_f32_avx512": ([_vp] * 5 + [_i, _i64, _i], _i),
+    "tsplat_layernorm_modulate_async": ([_vp] * 4 + [_i64, _i, ctypes.c_float, _i, _vp, _vp, _i64,
+                                         _i64, _vp], _i),
+    "tsplat_head_rmsnorm_async": ([_vp, _i64, _vp, _vp] + [_i] * 4 + [ctypes.c_float, _i, _i, _vp], _i),
+    "tsplat_rope_complex_async": ([_vp] * 3 + [_i64, _i, _vp], _i),
+    "tsplat_modulate_async": ([_vp] * 3 + [_i] * 3 + [_vp], _i),
+    "tsplat_gated_residual_async": ([_vp] * 3 + [_i] * 3 + [_vp], _i),
+    "tsplat_add_async": ([_vp] * 2 + [_i64, _vp], _i),
+    "tsplat_gelu_tanh_async": ([_vp] * 2 + [_i64, _vp], _i),
+    "tsplat_silu_async": ([_vp] * 2 + [_i64, _vp], _i),
+    "tsplat_cfg_combine_async": ([_vp] * 3 + [_i, _i64, _vp], _i),
+    "tsplat_euler_update_async": ([_vp] * 3 + [_i, _i64, _vp], _i),
+    "tsplat_ab2_update_async": ([_vp] * 5 + [_i, _i64, _vp], _i),
     "tsplat_abi_version": ([], _i),
     "tsplat_last_hip_error": ([], _i),
     "tsplat_build_arch": ([], ctypes.c_char_p),

@@ -9,8 +9,12 @@ literal layer list of config 4: NF24 QKV + self SDPA + NF24 out, cross
 attention (NF24 q on the latent, NF24 kv on the condition tokens, NF24 out),
 NF24 MLP fc1 / GELU(tanh) / fc2.  Every Linear is an NF24 packed weight run
 by the gfx950 GEMM; self attention uses the fused NF24 QKV projection +
-RoPE/RMSNorm/pack and the packed exact SDPA; elementwise work (LayerNorm,
-modulation, GELU, residuals, cross q/k RMSNorm) is torch on the device.
+RoPE/RMSNorm/pack and the packed exact SDPA.  The elementwise work runs in
+the block_ops kernels, fused where the data allows: LayerNorm + modulation
+in one pass, GELU in the fc1 epilogue, the gated residuals in the out / fc2
+epilogues, the cross-attention residual add in the xout epilogue, the
+cross q/k RMSNorm with the [B,H,L,64] permute; CFG and the Euler update are
+the sampler kernels.  torch only allocates, copies and stacks.
 
 Frozen choices (not pinned by the reference; recorded here):
   * LayerNorm eps 1e-6; norm1/norm3 without affine, the cross-attention
@@ -37,6 +41,8 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass
 
+from . import block_ops as bo
+from .native_sampler_backend import NativeSamplerBackend
 from .native_sdpa_ctypes import native_sdpa_f32_ex
 from .nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
 from .qkv import gemm_nf24_qkv_direct
@@ -88,6 +94,11 @@ class PackedLinear:
     def __call__(self, x2, out=None):
         return nf24_linear(x2, self.code01_t, self.q2_t, self.scale, self.bias, out=out)
 
+    def epilogue(self, x2, kind, out=None, gate=None):
+        """This Linear with a fused elementwise epilogue (block_ops.EPILOGUE_*)."""
+        return bo.nf24_linear_epilogue(x2, self.code01_t, self.q2_t, self.scale, self.bias, kind,
+                                       out=out, gate=gate)
+
     def host(self):
         return {k: getattr(self, k).cpu().numpy() for k in ("code01_t", "q2_t", "scale", "bias")}
 
@@ -119,12 +130,6 @@ class FlowBlock:
         for k in ("shift_table", "q_gamma", "k_gamma", "xq_gamma", "xk_gamma", "xnorm_w", "xnorm_b"):
             out[k] = getattr(self, k).cpu().numpy()
         return out
-
-
-def head_rmsnorm(torch, y, gamma):
-    """[..., H, 64]: y * 8 / max(||y||, 1e-12) * gamma[h]."""
-    n = torch.linalg.vector_norm(y, dim=-1, keepdim=True).clamp_min(1e-12)
-    return y * (8.0 / n) * gamma
 
 
 def rope_frequencies(torch, L, H, theta, device):
@@ -164,6 +169,7 @@ class FlowModel:
         self.final_shift_table = _randn(torch, (2, C), 49999, device, 0.02)
         self.blocks = [FlowBlock(torch, cfg, i, device, 1010 + 10 * i) for i in range(nb)]
         self._freqs = {}
+        self.sampler = NativeSamplerBackend()
 
     def freqs(self, L):
         if L not in self._freqs:
@@ -173,62 +179,62 @@ class FlowModel:
     # -------------------------------------------------------------- pieces
     def timestep(self, t):
         torch = self.torch
-        F = torch.nn.functional
         emb = timestep_embedding(torch, t, self.cfg.freq_dim, self.device).contiguous()
-        t_emb = self.t_fc2(F.silu(self.t_fc1(emb)).contiguous())
-        t_mod = self.adaln(F.silu(t_emb).contiguous())
+        t_emb = self.t_fc2(bo.silu(self.t_fc1(emb)))
+        t_mod = self.adaln(bo.silu(t_emb))
         return t_emb, t_mod
 
     def block_forward(self, blk: FlowBlock, x, cond, t_mod):
-        """x [B, L, C], cond [B, Lc, C], t_mod [B, 6C] -> x (new tensor)."""
-        torch = self.torch
-        F = torch.nn.functional
+        """x [B, L, C] (updated in place and returned), cond [B, Lc, C], t_mod [B, 6C]."""
         cfg = self.cfg
         B, L, C = (int(s) for s in x.shape)
         Lc = int(cond.shape[1])
         H = cfg.heads
-        mod = (t_mod + blk.shift_table).unsqueeze(1)  # [B, 1, 6C]
-        shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = mod.chunk(6, dim=-1)
-
-        # self attention: fused NF24 QKV + RoPE/RMSNorm/pack, packed exact SDPA, NF24 out
-        h = F.layer_norm(x, (C,), eps=cfg.ln_eps) * (1 + scale_msa) + shift_msa
+        mod = t_mod.clone()  # [B, 6C] = t_mod + shift_table, chunks (shift, scale, gate) x 2
+        for b in range(B):
+            bo.add_inplace(mod[b], blk.shift_table)
+        shift_msa, scale_msa, gate_msa = mod[:, 0:C], mod[:, C:2 * C], mod[:, 2 * C:3 * C]
+        shift_mlp, scale_mlp, gate_mlp = mod[:, 3 * C:4 * C], mod[:, 4 * C:5 * C], mod[:, 5 * C:]
+        x2 = x.view(B * L, C)
         lin = blk.lin
-        q, pk, pv = gemm_nf24_qkv_direct(h.reshape(B * L, C), lin["qkv"].code01_t, lin["qkv"].q2_t,
+
+        # self attention: LN + modulate, fused NF24 QKV + RoPE/RMSNorm/pack,
+        # packed exact SDPA, NF24 out with the gated residual in its epilogue
+        h = bo.layer_norm(x, cfg.ln_eps, scale=scale_msa, shift=shift_msa)
+        q, pk, pv = gemm_nf24_qkv_direct(h.view(B * L, C), lin["qkv"].code01_t, lin["qkv"].q2_t,
                                          lin["qkv"].scale, lin["qkv"].bias, self.freqs(L),
                                          blk.q_gamma, blk.k_gamma, B, L, H)
         a = native_sdpa_f32_ex(q, pk, pv, kv_packed=True, key_count=L, out_layout="blhd")
-        a = lin["out"](a.view(B * L, C)).view(B, L, C)
-        x = x + gate_msa * a
+        lin["out"].epilogue(a.view(B * L, C), bo.EPILOGUE_GATED, out=x2, gate=gate_msa)
 
-        # cross attention to the condition tokens
-        h = F.layer_norm(x, (C,), weight=blk.xnorm_w, bias=blk.xnorm_b, eps=cfg.ln_eps)
-        xq = lin["xq"](h.reshape(B * L, C)).view(B, L, H, 64)
-        xq = head_rmsnorm(torch, xq, blk.xq_gamma).permute(0, 2, 1, 3).contiguous()
-        kv = lin["xkv"](cond.reshape(B * Lc, C)).view(B, Lc, 2, H, 64)
-        xk = head_rmsnorm(torch, kv[:, :, 0], blk.xk_gamma).permute(0, 2, 1, 3).contiguous()
-        xv = kv[:, :, 1].permute(0, 2, 1, 3).contiguous()
+        # cross attention to the condition tokens (no RoPE)
+        h = bo.layer_norm(x, cfg.ln_eps, blk.xnorm_w, blk.xnorm_b)
+        xq = bo.head_rmsnorm(lin["xq"](h.view(B * L, C)), blk.xq_gamma, B, L, H)
+        kv = lin["xkv"](cond.reshape(B * Lc, C))  # [B*Lc, 2C] = [k | v]
+        xk = bo.head_rmsnorm(kv, blk.xk_gamma, B, Lc, H, token_stride=2 * C)
+        xv = bo.head_rmsnorm(kv[:, C:], None, B, Lc, H, token_stride=2 * C, normalize=False)
         a = native_sdpa_f32_ex(xq, xk, xv, out_layout="blhd")
-        x = x + lin["xout"](a.view(B * L, C)).view(B, L, C)
+        lin["xout"].epilogue(a.view(B * L, C), bo.EPILOGUE_ADD, out=x2)
 
-        # MLP
-        h = F.layer_norm(x, (C,), eps=cfg.ln_eps) * (1 + scale_mlp) + shift_mlp
-        h = lin["fc1"](h.reshape(B * L, C))
-        h = F.gelu(h, approximate="tanh")
-        h = lin["fc2"](h).view(B, L, C)
-        return x + gate_mlp * h
+        # MLP: LN + modulate, fc1 with GELU, fc2 with the gated residual
+        h = bo.layer_norm(x, cfg.ln_eps, scale=scale_mlp, shift=shift_mlp)
+        h = lin["fc1"].epilogue(h.view(B * L, C), bo.EPILOGUE_GELU)
+        lin["fc2"].epilogue(h, bo.EPILOGUE_GATED, out=x2, gate=gate_mlp)
+        return x
 
     def velocity(self, z, cond, t):
         """z [B, L, C], cond [B, Lc, C], t [B] (already x1000) -> v [B, L, C]."""
         torch = self.torch
-        F = torch.nn.functional
         B, L, C = (int(s) for s in z.shape)
         t_emb, t_mod = self.timestep(t)
         x = self.input_layer(z.reshape(B * L, C)).view(B, L, C)
         for blk in self.blocks:
             x = self.block_forward(blk, x, cond, t_mod)
-        shift, scale = (self.final_shift_table[None] + t_emb[:, None, :]).unbind(1)
-        h = F.layer_norm(x, (C,), eps=self.cfg.final_ln_eps) * (1 + scale[:, None]) + shift[:, None]
-        return self.out_layer(h.reshape(B * L, C)).view(B, L, C)
+        fs = t_emb[:, None, :].expand(B, 2, C).contiguous()  # [B, (shift, scale), C]
+        for b in range(B):
+            bo.add_inplace(fs[b], self.final_shift_table)
+        h = bo.layer_norm(x, self.cfg.final_ln_eps, scale=fs[:, 1], shift=fs[:, 0])
+        return self.out_layer(h.view(B * L, C)).view(B, L, C)
 
     def schedule(self):
         s = self.cfg.shift
@@ -244,9 +250,12 @@ class FlowModel:
         zz = torch.stack((z, z))
         cc = torch.stack((cond, torch.zeros_like(cond)))
         v = self.velocity(zz, cc, t)
-        g = self.cfg.guidance
-        v_cfg = g * v[0] - (g - 1.0) * v[1]
-        return z - dt * v_cfg, v_cfg
+        v_cfg, z_next = v[0:1].clone(), z[None].clone()
+        g = torch.full((1,), self.cfg.guidance, dtype=torch.float32, device=self.device)
+        d = torch.full((1,), dt, dtype=torch.float32, device=self.device)
+        self.sampler.cfg_combine_inplace({"x": v_cfg}, {"x": v[1:2]}, g)
+        self.sampler.euler_update_inplace({"x": z_next}, {"x": v_cfg}, d)
+        return z_next[0], v_cfg[0]
 
     def host(self):
         """All parameters as NumPy arrays (for the CPU restatement)."""
