@@ -173,6 +173,13 @@ int tsplat_nf24_pack_async(const float* weight, int out_features, int in_feature
                            const float* alphabet, int alphabet_len, float* base_workspace,
                            int16_t* code01_t, int8_t* q2_t, float* scale, void* stream);
 
+/* scripts/native_linear_nf24_prepacked.py:17-36 (decode_nf24_i16_weight_t /
+ * decode_nf24_i16_weight): exact fp32 weights, out [in, out] like the codes,
+ * or [out, in] (the nn.Linear layout) when transposed != 0. */
+int tsplat_nf24_decode_async(const int16_t* code01_t, const int8_t* q2_t, const float* scale,
+                             float* out, int in_features, int out_features, int transposed,
+                             void* stream);
+
 /* ---------------- NF24 GEMM with an elementwise epilogue --------------- */
 
 /* The GEMM of tsplat_nf24_gemm_async with the block's next elementwise step

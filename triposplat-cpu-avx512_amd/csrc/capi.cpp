@@ -405,6 +405,22 @@ int tsplat_nf24_pack_async(const float* weight, int out_features, int in_feature
   return st;
 }
 
+int tsplat_nf24_decode_async(const int16_t* code01_t, const int8_t* q2_t, const float* scale,
+                             float* out, int in_features, int out_features, int transposed,
+                             void* stream) {
+  if (!code01_t || !q2_t || !scale || !out) return kErrNull;
+  if (in_features <= 0 || out_features <= 0) return kErrDims;
+  const int64_t count = (int64_t)in_features * out_features;
+  TSPLAT_CHECK(check_dev(code01_t, count * 2));
+  TSPLAT_CHECK(check_dev(q2_t, count));
+  TSPLAT_CHECK(check_dev(scale, (int64_t)out_features * 4));
+  TSPLAT_CHECK(check_dev(out, count * 4));
+  const int st = launch_nf24_decode(code01_t, q2_t, scale, out, in_features, out_features,
+                                    transposed ? 1 : 0, static_cast<hipStream_t>(stream));
+  if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
+  return st;
+}
+
 // ------------------------------------------------------------------ library
 int tsplat_abi_version(void) { return kAbiVersion; }
 int tsplat_last_hip_error(void) { return g_last_hip_error.load(); }

@@ -104,7 +104,56 @@ __global__ __launch_bounds__(kThreads) void nf24_quantize_kernel(
   }
 }
 
+// Exact decode (scripts/native_linear_nf24_prepacked.py:17-36): w = fp32(256 *
+// q01 + q2) * scale[n] (the integer is exact in fp32, one rounding in the
+// multiply), written [in, out] like the codes or transposed to [out, in]
+// through a 64 x 64 LDS tile so both sides stay coalesced.
+template <bool kTransposed>
+__global__ __launch_bounds__(kThreads) void nf24_decode_kernel(const int16_t* code01_t,
+                                                               const int8_t* q2_t,
+                                                               const float* scale, float* out,
+                                                               int in_f, int out_f) {
+#pragma clang fp contract(off)
+  __shared__ float tile[64][65];
+  const int tiles_n = (out_f + 63) / 64;
+  const int k0 = (blockIdx.x / tiles_n) * 64;
+  const int n0 = (blockIdx.x % tiles_n) * 64;
+  for (int e = threadIdx.x; e < 64 * 64; e += kThreads) {
+    const int kl = e / 64, nl = e % 64;
+    const int k = k0 + kl, n = n0 + nl;
+    if (k < in_f && n < out_f) {
+      const int64_t i = (int64_t)k * out_f + n;
+      const float w = (float)((int32_t)code01_t[i] * 256 + (int32_t)q2_t[i]) * scale[n];
+      if (kTransposed)
+        tile[nl][kl] = w;
+      else
+        out[i] = w;
+    }
+  }
+  if (!kTransposed) return;
+  __syncthreads();
+  for (int e = threadIdx.x; e < 64 * 64; e += kThreads) {
+    const int nl = e / 64, kl = e % 64;
+    const int k = k0 + kl, n = n0 + nl;
+    if (k < in_f && n < out_f) out[(int64_t)n * in_f + k] = tile[nl][kl];
+  }
+}
+
 }  // namespace
+
+int launch_nf24_decode(const int16_t* code01_t, const int8_t* q2_t, const float* scale, float* out,
+                       int in_f, int out_f, int transposed, hipStream_t stream) {
+  if (in_f <= 0 || out_f <= 0) return kErrDims;
+  const int64_t blocks = (int64_t)((in_f + 63) / 64) * ((out_f + 63) / 64);
+  if (blocks > 0x7fffffff) return kErrDims;
+  if (transposed)
+    hipLaunchKernelGGL((nf24_decode_kernel<true>), dim3((unsigned)blocks), dim3(kThreads), 0,
+                       stream, code01_t, q2_t, scale, out, in_f, out_f);
+  else
+    hipLaunchKernelGGL((nf24_decode_kernel<false>), dim3((unsigned)blocks), dim3(kThreads), 0,
+                       stream, code01_t, q2_t, scale, out, in_f, out_f);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
 
 int launch_nf24_pack(const float* w, int out_f, int in_f, const float* alphabet, int alphabet_len,
                      float* base_tmp, int16_t* code01_t, int8_t* q2_t, float* scale,

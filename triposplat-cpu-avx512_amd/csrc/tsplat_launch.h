@@ -143,6 +143,11 @@ int launch_nf24_pack(const float* w, int out_f, int in_f, const float* alphabet,
                      float* base_tmp, int16_t* code01_t, int8_t* q2_t, float* scale,
                      hipStream_t stream);
 
+// Exact NF24 decode to fp32: [in_f, out_f] like the codes, or [out_f, in_f]
+// (the nn.Linear weight) when transposed.
+int launch_nf24_decode(const int16_t* code01_t, const int8_t* q2_t, const float* scale, float* out,
+                       int in_f, int out_f, int transposed, hipStream_t stream);
+
 // Grow-only device scratch owned by the library, one buffer per (device,
 // stream, slot); null on allocation failure.  Valid until the next call with
 // the same key that asks for more bytes.

@@ -92,9 +92,7 @@ def quantize_nf24_i16_per_output_channel(weight, codebook=None):
     return [code01_t, q2_t, q2_t], [scale, scale, scale], error
 
 
-def decode_nf24_i16_weight_t(code01_t, q2_t, scale):
-    """Exact fp32 weights in the GEMM's [in, out] layout
-    (scripts/native_linear_nf24_prepacked.py:17-31)."""
+def _decode(code01_t, q2_t, scale, transposed):
     import torch
 
     if code01_t.dtype != torch.int16 or q2_t.dtype != torch.int8:
@@ -103,16 +101,31 @@ def decode_nf24_i16_weight_t(code01_t, q2_t, scale):
         raise ValueError("NF24 code tensor shape mismatch")
     if scale.dtype != torch.float32 or scale.ndim != 1 or scale.numel() != code01_t.shape[1]:
         raise ValueError("NF24 scale shape mismatch")
-    combined = torch.bitwise_left_shift(code01_t.to(torch.int32), 8)
-    combined.add_(q2_t.to(torch.int32))
-    weight_t = combined.to(torch.float32)
-    weight_t.mul_(scale.reshape(1, -1))
-    return weight_t
+    for name, t in (("code01_t", code01_t), ("q2_t", q2_t), ("scale", scale)):
+        if t.device.type != "cuda" or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous GPU tensor")
+    in_f, out_f = (int(s) for s in code01_t.shape)
+    shape = (out_f, in_f) if transposed else (in_f, out_f)
+    out = torch.empty(shape, dtype=torch.float32, device=code01_t.device)
+    lib = load_library()
+    with torch.cuda.device(code01_t.device):
+        status = lib.tsplat_nf24_decode_async(code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(),
+                                              out.data_ptr(), in_f, out_f, int(transposed),
+                                              current_stream_handle(code01_t.device))
+    check_status(status, "tsplat_nf24_decode_async")
+    return out
+
+
+def decode_nf24_i16_weight_t(code01_t, q2_t, scale):
+    """Exact fp32 weights in the GEMM's [in, out] layout
+    (scripts/native_linear_nf24_prepacked.py:17-31), decoded on the device."""
+    return _decode(code01_t, q2_t, scale, False)
 
 
 def decode_nf24_i16_weight(code01_t, q2_t, scale):
-    """Exact fp32 weights as a contiguous [out, in] Linear weight."""
-    return decode_nf24_i16_weight_t(code01_t, q2_t, scale).t().contiguous()
+    """Exact fp32 weights as a contiguous [out, in] Linear weight
+    (native_linear_nf24_prepacked.py:34-36)."""
+    return _decode(code01_t, q2_t, scale, True)
 
 
 def nf24_linear(x2, code01_t, q2_t, scale, bias, *, output_start=0, output_count=None, out=None,
