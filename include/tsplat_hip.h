@@ -137,6 +137,27 @@ int triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2(const float* qkv, const float
                                                    int L_padded, int frequency_batches,
                                                    int threads);
 
+/* scripts/native_qkv_postprocess_v2_avx512.c:107-191: selected query rows.
+ * q [B, Lq, H*64] (a Q-only projection), kv [B, Lk, 2*H*64] = [k | v];
+ * query t is rotated with frequency row selected_indices[t] (int64, device
+ * array; any index outside [0, Lk) -> -3 before any work, as the
+ * reference); q_bhld [B,H,Lq,64], packed k/v [B,H,64,Lk_padded] with zero
+ * tail.  Used for the final block, whose outputs are read only at the
+ * latent rows. */
+int triposplat_q_kv_selected_rope_rmsnorm_pack_f32_avx512_v2(
+    const float* q, const float* kv, const float* frequencies, const int64_t* selected_indices,
+    const float* q_gamma, const float* k_gamma, float* q_bhld, float* packed_k, float* packed_v,
+    int B, int Lq, int Lk, int H, int D, int Lk_padded, int frequency_batches, int threads);
+/* Asynchronous form; the indices are not read on the host: a query whose
+ * index is outside [0, Lk) gets an all-zero q row. */
+int tsplat_q_kv_selected_postprocess_async(const float* q, const float* kv,
+                                           const float* frequencies,
+                                           const int64_t* selected_indices,
+                                           const float* q_gamma, const float* k_gamma,
+                                           float* q_bhld, float* packed_k, float* packed_v, int B,
+                                           int Lq, int Lk, int H, int D, int Lk_padded,
+                                           int frequency_batches, void* stream);
+
 /* scripts/gemm_nf24_qkv_direct_avx512.c:87-199: NF24 QKV GEMM (N = 3*H*64)
  * followed by the postprocess above, without returning the [B*L, N]
  * projection to the caller. */

@@ -164,6 +164,37 @@ def qkv_rope_rmsnorm_pack(qkv, freqs, q_gamma, k_gamma, B, L, H, L_padded=None):
     return q, pk, pv
 
 
+def _selected_call(fn, q, kv, freqs, selected, q_gamma, k_gamma, B, Lq, Lk, H, Lk_padded, extra):
+    q, kv, freqs = _f32(q), _f32(kv), _f32(freqs)
+    q_gamma, k_gamma = _f32(q_gamma), _f32(k_gamma)
+    sel = np.ascontiguousarray(selected, dtype=np.int64)
+    Lp = ((Lk + 15) // 16) * 16 if Lk_padded is None else Lk_padded
+    qo = np.empty((B, H, Lq, 64), np.float32)
+    pk = np.empty((B, H, 64, Lp), np.float32)
+    pv = np.empty((B, H, 64, Lp), np.float32)
+    st = fn(_ptr(q), _ptr(kv), _ptr(freqs), _ptr(sel), _ptr(q_gamma), _ptr(k_gamma), _ptr(qo),
+            _ptr(pk), _ptr(pv), B, Lq, Lk, H, 64, Lp, freqs.shape[0], *extra)
+    return st, (qo, pk, pv)
+
+
+def q_kv_selected_rope_rmsnorm_pack(q, kv, freqs, selected, q_gamma, k_gamma, B, Lq, Lk, H,
+                                    Lk_padded=None):
+    """scripts/native_qkv_postprocess_v2_avx512.c:107-191 (returns (status, outputs))."""
+    fn = lib().oracle_q_kv_selected_rope_rmsnorm_pack
+    fn.argtypes = [_vp] * 9 + [_i] * 7
+    fn.restype = _i
+    return _selected_call(fn, q, kv, freqs, selected, q_gamma, k_gamma, B, Lq, Lk, H, Lk_padded, ())
+
+
+def ref_q_kv_selected(q, kv, freqs, selected, q_gamma, k_gamma, B, Lq, Lk, H, Lk_padded=None,
+                      threads=0):
+    fn = ref_lib("libref_qkv_postprocess_v2.so").triposplat_q_kv_selected_rope_rmsnorm_pack_f32_avx512_v2
+    fn.argtypes = [_vp] * 9 + [_i] * 8
+    fn.restype = _i
+    return _selected_call(fn, q, kv, freqs, selected, q_gamma, k_gamma, B, Lq, Lk, H, Lk_padded,
+                          (threads,))
+
+
 def gemm_nf24_qkv_direct(x, code01_t, q2_t, scale, bias, freqs, q_gamma, k_gamma, B, L, H,
                          L_padded=None):
     """scripts/gemm_nf24_qkv_direct_avx512.c:87-199."""

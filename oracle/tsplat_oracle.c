@@ -353,6 +353,49 @@ int oracle_qkv_rope_rmsnorm_pack(const float* qkv, const float* freqs, const flo
   return 0;
 }
 
+/* scripts/native_qkv_postprocess_v2_avx512.c:107-191: q [B,Lq,H*64] rows
+ * rotated with frequency row selected[t], kv [B,Lk,2*H*64] = [k | v] packed
+ * with a zero tail; an index outside [0, Lk) is -3 before any work. */
+int oracle_q_kv_selected_rope_rmsnorm_pack(const float* q, const float* kv, const float* freqs,
+                                           const int64_t* selected, const float* q_gamma,
+                                           const float* k_gamma, float* q_bhld, float* packed_k,
+                                           float* packed_v, int B, int Lq, int Lk, int H, int D,
+                                           int Lk_padded, int frequency_batches) {
+  if (!q || !kv || !freqs || !selected || !q_gamma || !k_gamma || !q_bhld || !packed_k || !packed_v)
+    return -1;
+  if (B <= 0 || Lq <= 0 || Lk <= 0 || H <= 0 || D != OR_HEAD_DIM || Lk_padded < Lk ||
+      (Lk_padded & 15) != 0 || (frequency_batches != 1 && frequency_batches != B))
+    return -2;
+  for (int t = 0; t < Lq; ++t)
+    if (selected[t] < 0 || selected[t] >= Lk) return -3;
+  for (int64_t bh = 0; bh < (int64_t)B * H; ++bh) {
+    const int b = (int)(bh / H), h = (int)(bh % H);
+    const int fb = frequency_batches == 1 ? 0 : b;
+    for (int t = 0; t < Lq; ++t)
+      rope_rmsnorm64(q + (((int64_t)b * Lq + t) * H + h) * D,
+                     freqs + (((int64_t)fb * Lk + selected[t]) * H + h) * D,
+                     q_gamma + (int64_t)h * D, q_bhld + (bh * Lq + t) * D);
+    float* pk = packed_k + bh * D * (int64_t)Lk_padded;
+    float* pv = packed_v + bh * D * (int64_t)Lk_padded;
+    for (int t = 0; t < Lk; ++t) {
+      const float* ks = kv + (((int64_t)b * Lk + t) * 2 * H + h) * D;
+      const float* vs = ks + (int64_t)H * D;
+      float kn[OR_HEAD_DIM];
+      rope_rmsnorm64(ks, freqs + (((int64_t)fb * Lk + t) * H + h) * D, k_gamma + (int64_t)h * D, kn);
+      for (int d = 0; d < D; ++d) {
+        pk[(int64_t)d * Lk_padded + t] = kn[d];
+        pv[(int64_t)d * Lk_padded + t] = vs[d];
+      }
+    }
+    for (int d = 0; d < D; ++d)
+      for (int t = Lk; t < Lk_padded; ++t) {
+        pk[(int64_t)d * Lk_padded + t] = 0.0f;
+        pv[(int64_t)d * Lk_padded + t] = 0.0f;
+      }
+  }
+  return 0;
+}
+
 /* scripts/gemm_nf24_qkv_direct_avx512.c:87-199: the NF24 QKV GEMM (same
  * per-output chain as the plain GEMM) immediately followed by the
  * postprocess above; N must be 3*H*64.  Bit-identical to GEMM followed by

@@ -96,6 +96,22 @@ def main():
     out["qkv_direct_1x17x2_k128"] = dict(x=x, code01_t=c01, q2_t=q2, scale=s, bias=b, freqs=fr,
                                          q_gamma=qg, k_gamma=kg, q=qo, packed_k=pko, packed_v=pvo)
 
+    # selected-rows postprocess (the final block's latent queries), one index out of order
+    r = np.random.default_rng(23)
+    B, Lq, Lk, H = 2, 21, 37, 2
+    C = H * 64
+    qsel = r.standard_normal((B, Lq, C), dtype=np.float32)
+    kv = r.standard_normal((B, Lk, 2 * C), dtype=np.float32)
+    ang = r.standard_normal((B, Lk, H, 32)).astype(np.float32)
+    fr = np.stack([np.cos(ang), np.sin(ang)], -1).reshape(B, Lk, H, 64).astype(np.float32)
+    sel = np.concatenate([np.arange(Lq - 1), [Lk - 1]]).astype(np.int64)
+    qg = (r.standard_normal((H, 64)) * 0.05 + 1.0).astype(np.float32)
+    kg = (r.standard_normal((H, 64)) * 0.05 + 1.0).astype(np.float32)
+    st, (qo, pko, pvo) = O.ref_q_kv_selected(qsel, kv, fr, sel, qg, kg, B, Lq, Lk, H, threads=2)
+    assert st == 0
+    out["qkv_selected_2x21x37"] = dict(q=qsel, kv=kv, freqs=fr, selected=sel, q_gamma=qg, k_gamma=kg,
+                                       q_out=qo, packed_k=pko, packed_v=pvo)
+
     ew = ew_fixture()
     out["ew_ops"] = ew
     only = set(sys.argv[1:])

@@ -73,6 +73,23 @@ def test_golden_qkv(oracle):
         assert _bits_equal(a, g[key])
 
 
+def test_golden_qkv_selected(oracle):
+    g = _load("qkv_selected_2x21x37")
+    st, got = oracle.q_kv_selected_rope_rmsnorm_pack(g["q"], g["kv"], g["freqs"], g["selected"],
+                                                     g["q_gamma"], g["k_gamma"], 2, 21, 37, 2)
+    assert st == 0
+    for a, key in zip(got, ("q_out", "packed_k", "packed_v")):
+        assert _bits_equal(a, g[key])
+    # an index outside [0, Lk) is rejected (-3) before any work, as the reference does
+    bad = g["selected"].copy()
+    bad[5] = 37
+    assert oracle.q_kv_selected_rope_rmsnorm_pack(g["q"], g["kv"], g["freqs"], bad, g["q_gamma"],
+                                                  g["k_gamma"], 2, 21, 37, 2)[0] == -3
+    if oracle.ref_available():
+        assert oracle.ref_q_kv_selected(g["q"], g["kv"], g["freqs"], bad, g["q_gamma"], g["k_gamma"],
+                                        2, 21, 37, 2)[0] == -3
+
+
 # ---------------------------------------------------------------- _ref
 def test_oracle_matches_reference_build(oracle):
     if not oracle.ref_available():

@@ -8,6 +8,7 @@
 #include <atomic>
 #include <chrono>
 #include <cstdint>
+#include <vector>
 
 #include "tsplat_common.h"
 #include "tsplat_launch.h"
@@ -152,6 +153,30 @@ int post_checked(const float* qkv, const float* freqs, const float* qg, const fl
   TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lp * 4));
   QkvPostParams p{qkv, freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb};
   const int st = launch_qkv_postprocess(p, stream);
+  if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
+  return st;
+}
+
+int selected_checked(const float* q, const float* kv, const float* freqs, const int64_t* sel,
+                     const float* qg, const float* kg, float* q_out, float* pk, float* pv, int B,
+                     int Lq, int Lk, int H, int D, int Lkp, int fb, hipStream_t stream) {
+  if (!q || !kv || !freqs || !sel || !qg || !kg || !q_out || !pk || !pv) return kErrNull;
+  if (B <= 0 || Lq <= 0 || Lk <= 0 || H <= 0 || D != kHeadDim || Lkp < Lk || (Lkp & 15) != 0 ||
+      (fb != 1 && fb != B))
+    return kErrDims;
+  if (!aligned16(pk) || !aligned16(pv)) return kErrAlign;
+  const int64_t C = (int64_t)H * kHeadDim;
+  TSPLAT_CHECK(check_dev(q, (int64_t)B * Lq * C * 4));
+  TSPLAT_CHECK(check_dev(kv, (int64_t)B * Lk * 2 * C * 4));
+  TSPLAT_CHECK(check_dev(freqs, (int64_t)fb * Lk * C * 4));
+  TSPLAT_CHECK(check_dev(sel, (int64_t)Lq * 8));
+  TSPLAT_CHECK(check_dev(qg, C * 4));
+  TSPLAT_CHECK(check_dev(kg, C * 4));
+  TSPLAT_CHECK(check_dev(q_out, (int64_t)B * Lq * C * 4));
+  TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * Lkp * 4));
+  TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lkp * 4));
+  QkvSelectedParams p{q, kv, freqs, sel, qg, kg, q_out, pk, pv, B, Lq, Lk, H, Lkp, fb};
+  const int st = launch_qkv_selected_postprocess(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
   return st;
 }
@@ -360,6 +385,43 @@ int triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512(
                               frequencies, q_gamma, k_gamma, q_bhld, packed_k, packed_v, B, L, K,
                               N, H, D, L_padded, frequency_batches, nullptr);
   return st == kOk ? sync_null_stream() : st;
+}
+
+int triposplat_q_kv_selected_rope_rmsnorm_pack_f32_avx512_v2(
+    const float* q, const float* kv, const float* frequencies, const int64_t* selected_indices,
+    const float* q_gamma, const float* k_gamma, float* q_bhld, float* packed_k, float* packed_v,
+    int B, int Lq, int Lk, int H, int D, int Lk_padded, int frequency_batches, int threads) {
+  (void)threads;
+  if (!q || !kv || !frequencies || !selected_indices || !q_gamma || !k_gamma || !q_bhld ||
+      !packed_k || !packed_v)
+    return kErrNull;
+  if (B <= 0 || Lq <= 0 || Lk <= 0 || H <= 0 || D != kHeadDim || Lk_padded < Lk ||
+      (Lk_padded & 15) != 0 || (frequency_batches != 1 && frequency_batches != B))
+    return kErrDims;
+  // The reference rejects an index outside [0, Lk) with -3 before any work;
+  // the indices are device data, so they are read back first.
+  TSPLAT_CHECK(check_dev(selected_indices, (int64_t)Lq * 8));
+  std::vector<int64_t> host((size_t)Lq);
+  if (note(hipMemcpy(host.data(), selected_indices, (size_t)Lq * 8, hipMemcpyDeviceToHost)) != kOk)
+    return kErrLaunch;
+  for (int64_t v : host)
+    if (v < 0 || v >= Lk) return kErrRange;
+  const int st = selected_checked(q, kv, frequencies, selected_indices, q_gamma, k_gamma, q_bhld,
+                                  packed_k, packed_v, B, Lq, Lk, H, D, Lk_padded,
+                                  frequency_batches, nullptr);
+  return st == kOk ? sync_null_stream() : st;
+}
+
+int tsplat_q_kv_selected_postprocess_async(const float* q, const float* kv,
+                                           const float* frequencies,
+                                           const int64_t* selected_indices,
+                                           const float* q_gamma, const float* k_gamma,
+                                           float* q_bhld, float* packed_k, float* packed_v, int B,
+                                           int Lq, int Lk, int H, int D, int Lk_padded,
+                                           int frequency_batches, void* stream) {
+  return selected_checked(q, kv, frequencies, selected_indices, q_gamma, k_gamma, q_bhld, packed_k,
+                          packed_v, B, Lq, Lk, H, D, Lk_padded, frequency_batches,
+                          static_cast<hipStream_t>(stream));
 }
 
 int triposplat_gemm_nf24_qkv_direct_row_tile(void) { return 128; }

@@ -75,24 +75,32 @@ struct GemmArgs {
 // kEpilogue* of tsplat_launch.h, plus the fused QKV epilogue.
 enum Epilogue : int { kEpiStore = kEpilogueStore, kEpiQkv = 1 };
 
-// Sum over the 32 lanes of a half-wave (lanes that hold one output row).
-__device__ __forceinline__ float sum32(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
-  v += __shfl_xor(v, 16);
-  return v;
+// ||y||^2 of one head row whose dims d and 32+d sit in lane d (r0, r1) of a
+// half-wave, summed in the reference's order (native_qkv_postprocess_v2_avx512.c:3-24):
+// the AVX-512 lane j chains fma over dims j, 16+j, 32+j, 48+j, then the
+// _mm512_reduce_add_ps tree.  Lanes j < 16 of the half gather the two dims
+// they lack from lane j+16; every lane receives the sum.
+__device__ __forceinline__ float head_sumsq_ref(float r0, float r1, int g, int l32) {
+#pragma clang fp contract(off)
+  const int src = (g << 5) | ((l32 + 16) & 31);
+  const float rb = __shfl(r0, src);
+  const float rd = __shfl(r1, src);
+  float acc = fmaf(r0, r0, 0.0f);
+  acc = fmaf(rb, rb, acc);
+  acc = fmaf(r1, r1, acc);
+  acc = fmaf(rd, rd, acc);
+  return __shfl(reduce_add16(acc), g << 5);
 }
 
 // QKV epilogue of one wave: its 64 columns are one head of q, k or v
 // (colw = first column, a multiple of 64); lane l32 holds dims l32 and
 // 32 + l32 of rows 8*(r/4) + 4*g + r%4 of each 32-row block.  q and k get
 // RoPE (the partner of dim 2i / 2i+1 is the neighbouring lane) then
-// y * 8 / max(||y||, 1e-12) * gamma, with ||y||^2 summed over the half-wave;
+// y * 8 / max(||y||, 1e-12) * gamma with ||y||^2 in the reference's order;
 // q is stored [B, H, L, 64], k and v key-contiguous [B, H, 64, Lpad] (four
-// consecutive tokens per 128-bit store when L % 4 == 0).  Same fmaf forms as
-// qkv_postprocess.hip; only the order of the 64-term sum of squares differs.
+// consecutive tokens per 128-bit store when L % 4 == 0).  Same arithmetic as
+// qkv_postprocess.hip, so GEMM + this epilogue equals GEMM + postprocess
+// bit for bit.
 template <class C>
 __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, floatx16 (&acc)[C::kMB][C::kNB],
                                              int row_base, int colw, int g, int l32) {
@@ -132,7 +140,7 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, floatx16 (&acc)[
           const float fp0 = __shfl_xor(f0, 1), fp1 = __shfl_xor(f1, 1);
           const float r0 = odd ? fmaf(p0, f0, v0 * fp0) : fmaf(v0, f0, -(p0 * fp0));
           const float r1 = odd ? fmaf(p1, f1, v1 * fp1) : fmaf(v1, f1, -(p1 * fp1));
-          const float ss = sum32(r0 * r0 + r1 * r1);
+          const float ss = head_sumsq_ref(r0, r1, g, l32);
           const float fac = 8.0f / fmaxf(sqrtf(ss), 1.0e-12f);
           v0 = (r0 * fac) * g0;
           v1 = (r1 * fac) * g1;

@@ -54,6 +54,23 @@ struct QkvPostParams {
 };
 int launch_qkv_postprocess(const QkvPostParams& p, hipStream_t stream);
 
+// Selected-rows form: q [B, Lq, H*64] rows take their frequency row from
+// selected[t] (in [0, Lk); a row with an index outside is written as zeros),
+// kv [B, Lk, 2*H*64] = [k | v] -> packed k/v [B, H, 64, Lk_padded].
+struct QkvSelectedParams {
+  const float* q;
+  const float* kv;
+  const float* freqs;       // [fb, Lk, H, 64]
+  const int64_t* selected;  // [Lq]
+  const float* q_gamma;
+  const float* k_gamma;
+  float* q_out;             // [B, H, Lq, 64]
+  float* packed_k;
+  float* packed_v;
+  int B, Lq, Lk, H, Lk_padded, freq_batches;
+};
+int launch_qkv_selected_postprocess(const QkvSelectedParams& p, hipStream_t stream);
+
 // The NF24 projection x [B*L, K] -> [B*L, 3*H*64] with the postprocess
 // above applied in the GEMM's epilogue: no [B*L, 3*H*64] intermediate.
 // gemm.out is unused; gemm.M = B*L, gemm.N = gemm.n_count = 3*H*64.
