@@ -187,3 +187,57 @@ def combined_rmse(a, b):
     """RMSE as scripts/compare_latent_npz.py:22-48 reports it (float64)."""
     d = np.asarray(a, np.float64) - np.asarray(b, np.float64)
     return float(np.sqrt(np.mean(d * d)))
+
+
+class CpuJointFlow(CpuFlow):
+    """CPU restatement of tsplat/flow_joint.py's single-stream graph, computed
+    the long way: the full negative sequence (all condition rows, no key
+    bias) and the full final block, batch 1 per branch."""
+
+    def joint_freqs(self, L, Lc):
+        H = self.cfg.heads
+        i = np.arange(32, dtype=np.float64)
+        ang = np.arange(L, dtype=np.float64)[:, None] * self.cfg.rope_theta ** (-2.0 * i / 64.0)[None, :]
+        lat = np.stack((np.cos(ang), np.sin(ang)), -1).reshape(L, 64)
+        ident = np.zeros((Lc, 32, 2))
+        ident[..., 0] = 1.0
+        f = np.concatenate((lat, ident.reshape(Lc, 64)), 0).astype(np.float32)
+        return np.ascontiguousarray(np.broadcast_to(f[None, :, None, :], (1, L + Lc, H, 64)))
+
+    def joint_block(self, bp, x, t_mod, L):
+        cfg = self.cfg
+        _, Lt, C = x.shape
+        H = cfg.heads
+        x = np.array(x, dtype=np.float32, copy=True)
+        mod = (t_mod + bp["shift_table"]).astype(np.float32)
+        sm, cm, gm, s2, c2, g2 = (np.ascontiguousarray(a) for a in np.split(mod, 6, axis=-1))
+        h = self._modulate(self._ln(x, cfg.ln_eps), cm, sm)
+        q, pk, pv = self.qkv_direct(h.reshape(Lt, C), bp["qkv"], self.joint_freqs(L, Lt - L),
+                                    bp["q_gamma"], bp["k_gamma"], 1, Lt, H)
+        a = self.sdpa_packed_blhd(q, pk, pv, Lt).reshape(Lt, C)
+        x = self._gated(x, self.linear(a, bp["out"]).reshape(1, Lt, C), gm)
+        h = self._modulate(self._ln(x, cfg.ln_eps), c2, s2)
+        h = self._gelu(self.linear(h.reshape(Lt, C), bp["fc1"]))
+        return self._gated(x, self.linear(h, bp["fc2"]).reshape(1, Lt, C), g2)
+
+    def joint_velocity(self, z, cond, t):
+        L, C = z.shape
+        t_emb, t_mod = self.timestep(t)
+        x = np.concatenate((self.linear(z, self.p["input_layer"]), cond), 0)[None].astype(np.float32)
+        for bp in self.p["blocks"]:
+            x = self.joint_block(bp, x, t_mod, L)
+        fs = (self.p["final_shift_table"][None] + t_emb[:, None, :]).astype(np.float32)
+        h = self._modulate(self._ln(np.ascontiguousarray(x[:, :L]), self.cfg.final_ln_eps),
+                           np.ascontiguousarray(fs[:, 1]), np.ascontiguousarray(fs[:, 0]))
+        return self.linear(h.reshape(L, C), self.p["out_layer"])
+
+    def joint_euler_cfg_step(self, z, cond, step=0):
+        ts = self.schedule()
+        t = np.full(1, ts[step] * 1000.0, np.float32)
+        dt = np.float32(ts[step] - ts[step + 1])
+        v_pos = np.ascontiguousarray(self.joint_velocity(z, cond, t))
+        v_neg = np.ascontiguousarray(self.joint_velocity(z, np.zeros_like(cond), t))
+        self._ew("cfg_combine_inplace", v_pos, v_neg, np.array([self.cfg.guidance], np.float32), 1, v_pos.size)
+        z_next = np.array(z, np.float32, copy=True)
+        self._ew("euler_update_inplace", z_next, v_pos, np.array([dt], np.float32), 1, z_next.size)
+        return z_next, v_pos

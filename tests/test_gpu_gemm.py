@@ -172,3 +172,27 @@ def test_reference_named_entry_points(oracle, cuda, hiplib):
     hostp = ptrs[:-1] + [host.ctypes.data_as(ctypes.c_void_p).value]
     assert hiplib.triposplat_gemm_rnf8_avx512(*hostp, M, K, N, K, N, 4, 3) == -6
     assert hiplib.triposplat_gemm_rnf8_avx512_residual_mode() == 4
+
+
+@pytest.mark.parametrize("M,K,N", [(16385, 1024, 1024), (8194, 1024, 3072)])
+def test_gemm_tail_rows(oracle, cuda, hiplib, M, K, N):
+    """M = 256 k + r with r <= 32 (e.g. the compressed negative branch, L + 1
+    tokens) runs the r tail rows as a separate 32-row-tile launch.  Rows of
+    the 256-row part equal a GEMM over exactly those rows, the tail rows equal
+    the same rows computed inside a 256-row tile (a larger M with no tail),
+    all bit for bit; sampled rows and the tail against the oracle."""
+    import torch
+
+    print(f"gemm tail rows M={M} K={K} N={N}", flush=True)
+    x, w, b = seeded_linear(M + 7, M + 256, K, N, w_scale=0.02)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    r = M % 256
+    big = M - r + 256                                             # a multiple of 256: no tail split
+    got = _run_async(torch, hiplib, cuda, x[:M], c01, q2, s, b)
+    head = _run_async(torch, hiplib, cuda, x[:M - r], c01, q2, s, b)
+    full = _run_async(torch, hiplib, cuda, x[:big], c01, q2, s, b)
+    assert np.array_equal(got[:M - r].view(np.uint32), head.view(np.uint32))
+    assert np.array_equal(got[M - r:].view(np.uint32), full[M - r:M].view(np.uint32))
+    rows = np.concatenate([np.sort(np.random.default_rng(M).choice(M - r, 16, replace=False)),
+                           np.arange(M - r, M)])
+    _check(oracle, x[rows], c01, q2, s, b, got[rows])

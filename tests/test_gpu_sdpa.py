@@ -191,3 +191,33 @@ def test_sdpa_config2_sampled_rows(oracle, cuda):
     ref = oracle.sdpa_q8t512(q[:, :, rows], k, v)
     s = _assert_close(got[:, :, rows], ref, v)
     print("config2 sampled rows", s)
+
+
+@pytest.mark.parametrize("L,packed,bias", [(18432, True, False), (16385, True, True), (8704, False, False)])
+def test_sdpa_tail_split_sampled_rows(oracle, cuda, L, packed, bias):
+    """Tile counts that are not a multiple of the CU count (the joint
+    sequence 16384 + 2048 = 18432 -> 576 tiles; the compressed negative
+    branch 16385 keys with the log(M) bias -> 528; 8704 -> 272) run the
+    remainder tiles split along the keys plus a merge kernel.  Sampled rows
+    of the last head (the split tiles) and of head 0 against the oracle."""
+    import torch
+
+    print(f"sdpa tail split L={L} packed={packed} bias={bias}", flush=True)
+    B, H = 1, 16
+    r = np.random.default_rng(L)
+    q = _rope_rmsnorm(r.standard_normal((B, H, L, 64), dtype=np.float32))
+    k = _rope_rmsnorm(np.random.default_rng(L + 1).standard_normal((B, H, L, 64), dtype=np.float32))
+    v = np.random.default_rng(L + 2).standard_normal((B, H, L, 64), dtype=np.float32)
+    kb = None
+    if bias:
+        kb = np.zeros(L, np.float32)
+        kb[L - 1] = np.float32(math.log(2048.0))
+    got = _run(torch, cuda, q, k, v, bias=kb, packed=packed, blhd=packed)
+    if packed:
+        got = got.transpose(0, 2, 1, 3)  # BLHD -> BHLD
+    rows = np.sort(np.random.default_rng(5).choice(L, 16, replace=False))
+    rows[0], rows[-1] = 0, L - 1
+    for h in (0, H - 1):
+        ref = oracle.sdpa_q8t512(np.ascontiguousarray(q[:, h:h + 1, rows]), np.ascontiguousarray(k[:, h:h + 1]),
+                                 np.ascontiguousarray(v[:, h:h + 1]), kb)
+        _assert_close(np.ascontiguousarray(got[:, h:h + 1, rows]), ref, v[:, h:h + 1])

@@ -66,10 +66,11 @@ struct GemmArgs {
   float* out;
   int M, K, N, n_start, n_count, stride_x, stride_out;
   QkvArgs e;
-  // kEpilogueGated: gate row of batch m / rows_per_batch
+  // kEpilogueGated: gate row of batch (row0 + m) / rows_per_batch
   const float* gate;
   int64_t gate_stride;
   int rows_per_batch;
+  int row0;  // global index of row 0 of x / out (the epilogues' token mapping)
 };
 
 // kEpilogue* of tsplat_launch.h, plus the fused QKV epilogue.
@@ -130,8 +131,9 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, floatx16 (&acc)[
         if (sec < 2) {  // uniform over the wave
           const int row = row0 + t;
           const bool valid = row < a.M;  // uniform over the half-wave
-          const int b = valid ? row / e.L : 0;
-          const int l = valid ? row - b * e.L : 0;
+          const int tok = a.row0 + row;  // token index b * L + l
+          const int b = valid ? tok / e.L : 0;
+          const int l = valid ? tok - b * e.L : 0;
           const float* fr =
               e.freqs + (((int64_t)(e.fb == 1 ? 0 : b) * e.L + l) * e.H + h) * 64;
           const float f0 = valid ? fr[l32] : 0.0f;
@@ -153,7 +155,8 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, floatx16 (&acc)[
         for (int t = 0; t < 4; ++t) {
           const int row = row0 + t;
           if (row >= a.M) continue;
-          const int b = row / e.L, l = row - b * e.L;
+          const int tok = a.row0 + row;
+          const int b = tok / e.L, l = tok - b * e.L;
           float* dst = e.q + (((int64_t)b * e.H + h) * e.L + l) * 64;
           dst[l32] = y0[t];
           dst[32 + l32] = y1[t];
@@ -161,9 +164,10 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, floatx16 (&acc)[
       } else {
         float* base = sec == 1 ? e.pk : e.pv;
         const int64_t dim_stride = (int64_t)32 * e.Lpad;
-        if ((e.L & 3) == 0) {  // the four rows are four tokens of one sequence
+        if (((e.L | a.row0) & 3) == 0) {  // the four rows are four tokens of one sequence
           if (row0 < a.M) {
-            const int b = row0 / e.L, l = row0 - b * e.L;
+            const int tok = a.row0 + row0;
+            const int b = tok / e.L, l = tok - b * e.L;
             const int64_t off = (((int64_t)b * e.H + h) * 64 + l32) * e.Lpad + l;
             *reinterpret_cast<floatx4*>(base + off) = y0;
             *reinterpret_cast<floatx4*>(base + off + dim_stride) = y1;
@@ -173,7 +177,8 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, floatx16 (&acc)[
           for (int t = 0; t < 4; ++t) {
             const int row = row0 + t;
             if (row >= a.M) continue;
-            const int b = row / e.L, l = row - b * e.L;
+            const int tok = a.row0 + row;
+            const int b = tok / e.L, l = tok - b * e.L;
             const int64_t off = (((int64_t)b * e.H + h) * 64 + l32) * e.Lpad + l;
             base[off] = y0[t];
             base[off + dim_stride] = y1[t];
@@ -362,7 +367,7 @@ void nf24_gemm_kernel(GemmArgs a) {
         } else if constexpr (kEpi == kEpilogueGated) {
           // h = acc * gate, x = x + h: two roundings, as the reference's
           // native_block_elementwise_avx512.c:24-35
-          const float* gate = a.gate + (int64_t)(row / a.rows_per_batch) * a.gate_stride;
+          const float* gate = a.gate + (int64_t)((a.row0 + row) / a.rows_per_batch) * a.gate_stride;
           *dst = gated_residual_ref(*dst, v, gate[a.n_start + col]);
         } else if constexpr (kEpi == kEpilogueAdd) {
           *dst = *dst + v;
@@ -375,10 +380,11 @@ void nf24_gemm_kernel(GemmArgs a) {
 
 template <class C, int kEpi = kEpiStore>
 int launch_cfg(const GemmParams& p, hipStream_t stream, const QkvArgs& e = QkvArgs{},
-               const GemmEpilogueParams& ep = GemmEpilogueParams{kEpilogueStore, nullptr, 0, 1}) {
+               const GemmEpilogueParams& ep = GemmEpilogueParams{kEpilogueStore, nullptr, 0, 1},
+               int row0 = 0) {
   GemmArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out,
              p.M, p.K, p.N, p.n_start, p.n_count, p.stride_x, p.stride_out, e,
-             ep.gate, ep.gate_stride, ep.rows_per_batch};
+             ep.gate, ep.gate_stride, ep.rows_per_batch, row0};
   const int64_t tiles = (int64_t)((p.M + C::BM - 1) / C::BM) * ((p.n_count + C::BN - 1) / C::BN);
   if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
   const bool vec = (reinterpret_cast<uintptr_t>(p.x) % 16 == 0) && (p.stride_x % 4 == 0) &&
@@ -418,6 +424,7 @@ using CfgLarge = GemmCfg<256, 256, 16, 4, 4>;    // 16 waves, 1 workgroup / CU
 using CfgWide = GemmCfg<256, 192, 16, 4, 3>;     // 12 waves, 1 workgroup / CU
 using CfgSmall = GemmCfg<128, 128, 16, 2, 2, 3>; // 4 waves, 3 workgroups / CU
 using CfgSkinny = GemmCfg<32, 128, 32, 1, 4>;
+using CfgTail = GemmCfg<32, 128, 32, 1, 2>;      // <= 32 rows with an epilogue; 64-column waves
 
 struct Choice {
   int bm, bn, wgs_per_cu, waves;
@@ -464,6 +471,27 @@ int pick_config(int M, int n_count) {
   return best;
 }
 
+// Rows past the last multiple of 256 that number at most kTailRows would
+// occupy a whole extra round of 256-row tiles (e.g. M = 16385: 1040 tiles =
+// 4 rounds + 16 one-row tiles, ~270 us at K = 1024); they run as a second
+// launch of 32-row tiles instead (~30 us).  Every MFMA tile shape sums each
+// output in the same order, so the tail rows are bit-identical to what the
+// 256-row tiles would have produced.
+constexpr int kTailRows = 32;
+
+GemmParams rows_slice(const GemmParams& p, int first, int count) {
+  GemmParams q = p;
+  q.x = p.x + (int64_t)first * p.stride_x;
+  if (q.out != nullptr) q.out = p.out + (int64_t)first * p.stride_out;
+  q.M = count;
+  return q;
+}
+
+int tail_rows(int M) {
+  const int rem = M % 256;
+  return (M > 256 && rem != 0 && rem <= kTailRows) ? rem : 0;
+}
+
 }  // namespace
 
 int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
@@ -473,6 +501,10 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
     if (p.M > 8 && p.K <= 256) return launch_cfg<CfgSkinny>(p, stream);
     return launch_nf24_gemv(p, stream);
   }
+  if (const int rem = tail_rows(p.M)) {
+    const int st = launch_nf24_gemm(rows_slice(p, 0, p.M - rem), stream);
+    return st != kOk ? st : launch_cfg<CfgTail>(rows_slice(p, p.M - rem, rem), stream);
+  }
   const int best = pick_config(p.M, p.n_count);
   if (best == 0) return launch_cfg<CfgLarge>(p, stream);
   if (best == 1) return launch_cfg<CfgWide>(p, stream);
@@ -481,12 +513,20 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
 
 namespace {
 template <int kEpi>
-int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_t stream) {
-  // Few rows go to the 128x128 tile: the epilogue lives in the MFMA kernels.
-  const int best = p.M <= 32 ? 2 : pick_config(p.M, p.n_count);
-  if (best == 0) return launch_cfg<CfgLarge, kEpi>(p, stream, QkvArgs{}, e);
-  if (best == 1) return launch_cfg<CfgWide, kEpi>(p, stream, QkvArgs{}, e);
-  return launch_cfg<CfgSmall, kEpi>(p, stream, QkvArgs{}, e);
+int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_t stream,
+                    const QkvArgs& q = QkvArgs{}, int row0 = 0) {
+  if (const int rem = tail_rows(p.M)) {
+    const int st = launch_epi_kind<kEpi>(rows_slice(p, 0, p.M - rem), e, stream, q, row0);
+    return st != kOk ? st
+                     : launch_cfg<CfgTail, kEpi>(rows_slice(p, p.M - rem, rem), stream, q, e,
+                                                 row0 + p.M - rem);
+  }
+  // Few rows: the 32-row tile (the epilogues live in the MFMA kernels).
+  if (p.M <= 32) return launch_cfg<CfgTail, kEpi>(p, stream, q, e, row0);
+  const int best = pick_config(p.M, p.n_count);
+  if (best == 0) return launch_cfg<CfgLarge, kEpi>(p, stream, q, e, row0);
+  if (best == 1) return launch_cfg<CfgWide, kEpi>(p, stream, q, e, row0);
+  return launch_cfg<CfgSmall, kEpi>(p, stream, q, e, row0);
 }
 }  // namespace
 
@@ -518,10 +558,8 @@ int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream) {
   }
   const QkvArgs e{p.freqs, p.q_gamma, p.k_gamma, p.q, p.packed_k, p.packed_v,
                   p.L, p.H, p.L_padded, p.freq_batches};
-  const int best = pick_config(gp.M, gp.n_count);
-  if (best == 0) return launch_cfg<CfgLarge, kEpiQkv>(gp, stream, e);
-  if (best == 1) return launch_cfg<CfgWide, kEpiQkv>(gp, stream, e);
-  return launch_cfg<CfgSmall, kEpiQkv>(gp, stream, e);
+  const GemmEpilogueParams none{kEpilogueStore, nullptr, 0, 1};
+  return launch_epi_kind<kEpiQkv>(gp, none, stream, e);
 }
 
 }  // namespace tsplat

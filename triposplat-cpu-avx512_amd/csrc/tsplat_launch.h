@@ -168,7 +168,7 @@ int launch_nf24_decode(const int16_t* code01_t, const int8_t* q2_t, const float*
 // Grow-only device scratch owned by the library, one buffer per (device,
 // stream, slot); null on allocation failure.  Valid until the next call with
 // the same key that asks for more bytes.
-enum WorkspaceSlot : int { kSlotGemvPartial = 0 };
+enum WorkspaceSlot : int { kSlotGemvPartial = 0, kSlotSdpaPartial = 1 };
 void* stream_workspace(hipStream_t stream, size_t bytes, int slot);
 
 }  // namespace tsplat

@@ -68,3 +68,33 @@ def gemm_nf24_qkv_direct(x2, code01_t, q2_t, scale, bias, frequencies, q_gamma, 
         )
     check_status(status, "tsplat_gemm_nf24_qkv_direct_async")
     return q, pk, pv
+
+
+def q_kv_selected_rope_rmsnorm_pack(q, kv, frequencies, selected_indices, q_gamma, k_gamma, B, Lq, Lk, H,
+                                    *, L_padded=None, library=None):
+    """Selected query rows (scripts/native_qkv_postprocess_v2_avx512.c:107-191):
+    q [B, Lq, H*64] from a Q-only projection, kv [B, Lk, 2*H*64] = [k | v];
+    query t is rotated with frequency row selected_indices[t] (int64 GPU
+    tensor).  Returns q [B, H, Lq, 64] and packed k/v [B, H, 64, L_padded]."""
+    import torch
+
+    for name, t in (("q", q), ("kv", kv), ("frequencies", frequencies), ("q_gamma", q_gamma),
+                    ("k_gamma", k_gamma)):
+        _check(torch, name, t)
+    if (selected_indices.device.type != "cuda" or selected_indices.dtype != torch.int64
+            or not selected_indices.is_contiguous() or selected_indices.numel() != int(Lq)):
+        raise ValueError("selected_indices must be a contiguous int64 GPU tensor of length Lq")
+    Lp = padded_length(Lk) if L_padded is None else int(L_padded)
+    qo = torch.empty((B, H, Lq, 64), dtype=torch.float32, device=q.device)
+    pk = torch.empty((B, H, 64, Lp), dtype=torch.float32, device=q.device)
+    pv = torch.empty((B, H, 64, Lp), dtype=torch.float32, device=q.device)
+    lib = load_library(library)
+    with torch.cuda.device(q.device):
+        status = lib.tsplat_q_kv_selected_postprocess_async(
+            q.data_ptr(), kv.data_ptr(), frequencies.data_ptr(), selected_indices.data_ptr(),
+            q_gamma.data_ptr(), k_gamma.data_ptr(), qo.data_ptr(), pk.data_ptr(), pv.data_ptr(),
+            int(B), int(Lq), int(Lk), int(H), 64, Lp, int(frequencies.shape[0]),
+            current_stream_handle(q.device),
+        )
+    check_status(status, "tsplat_q_kv_selected_postprocess_async")
+    return qo, pk, pv
