@@ -61,8 +61,10 @@ def _check(oracle, x, c01, q2, s, b, got, start=0):
 SHAPES = [(25, 96, 64), (40, 96, 64), (10, 96, 64), (3, 96, 5), (1, 1024, 3072), (2, 1024, 256),
           (8, 4096, 64), (16, 64, 1024), (33, 130, 48), (129, 257, 200), (200, 64, 129),
           (7, 3, 17), (300, 1024, 96),
-          # few-row (HBM-bound) kernel: every row-count template, split and unsplit K
-          (4, 2048, 640), (16, 1024, 3072), (32, 512, 384), (5, 4096, 1024), (12, 1000, 130)]
+          # few-row (HBM-bound) kernels: every row-count template, split and unsplit K,
+          # ragged last K split, narrow and partial 512-column slabs
+          (4, 2048, 640), (16, 1024, 3072), (32, 512, 384), (5, 4096, 1024), (12, 1000, 130),
+          (3, 1000, 512), (7, 70, 1032), (1, 8200, 1024), (6, 4096, 8), (2, 1024, 6144)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)

@@ -156,6 +156,148 @@ __global__ __launch_bounds__(kReduceThreads) void nf24_gemv_reduce_kernel(
   out[(int64_t)m * stride_out + c] = bias[n_start + c] + v;
 }
 
+// ---------------------------------------------------------------------------
+// Wide form for M <= 8 with 8-aligned columns: a lane owns 8 adjacent columns
+// (one 128-bit code01 and one 64-bit q2 load per row: a wave reads 1 KB + 512 B
+// of one row), a wave owns 16 (or 8) consecutive rows and issues all of
+// their loads before consuming any (one HBM round trip), x comes through the
+// scalar cache (a wave's row is uniform), and a workgroup of 4 waves owns 512
+// columns x 64 (or 32) rows.  The 4 wave partials are added in wave order in
+// LDS; splits along K go to the workspace and nf24_gemv_merge_kernel adds
+// them in split order.
+constexpr int kWideWaves = 4;
+constexpr int kWideCols = 512;
+
+template <int MT, int kRows>
+__global__ __launch_bounds__(kWideWaves * 64) void nf24_gemv_wide_kernel(GemvArgs a) {
+  constexpr int rows_per_wave = kRows;
+  __shared__ float red[kWideWaves - 1][MT][kWideCols];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int slabs = (a.n_count + kWideCols - 1) / kWideCols;
+  const int slab = blockIdx.x % slabs;
+  const int split = blockIdx.x / slabs;
+  const int lc = slab * kWideCols + 8 * lane;        // first local column of this lane
+  const bool live = lc < a.n_count;                   // n_count % 8 == 0: all 8 or none
+  const int r0 = split * a.k_per_split + wave * rows_per_wave;
+  const int r1 = min(min(a.K, (split + 1) * a.k_per_split), r0 + rows_per_wave);
+  const int nr = max(0, r1 - r0);
+
+  // Issue every load of this wave's rows, then consume.  Loads are
+  // unconditional (rows past the range re-read a valid row, columns past
+  // n_count the first column) so they can all be in flight at once; such
+  // rows are multiplied by x = 0 and such columns get scale 0.
+  uint4 c[kRows];
+  uint2 q[kRows];
+  const int64_t col = a.n_start + (live ? lc : 0);
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    const int64_t off = (int64_t)min(r0 + i, a.K - 1) * a.N + col;
+    c[i] = *reinterpret_cast<const uint4*>(a.code01 + off);
+    q[i] = *reinterpret_cast<const uint2*>(a.q2 + off);
+  }
+  float sc[8];
+  {
+    const floatx4 s0 = *reinterpret_cast<const floatx4*>(a.scale + col);
+    const floatx4 s1 = *reinterpret_cast<const floatx4*>(a.scale + col + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sc[e] = live ? s0[e] : 0.0f;
+      sc[4 + e] = live ? s1[e] : 0.0f;
+    }
+  }
+  float acc[MT][8];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[m][e] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    const uint32_t cw[4] = {c[i].x, c[i].y, c[i].z, c[i].w};
+    const uint32_t qw[2] = {q[i].x, q[i].y};
+    float w[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int32_t code = (int32_t)(int16_t)((cw[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+      const int32_t res = (int32_t)(int8_t)((qw[e >> 2] >> (8 * (e & 3))) & 0xffu);
+      w[e] = (float)(code * 256 + res) * sc[e];
+    }
+    const int row = min(r0 + i, a.K - 1);
+    const bool row_ok = i < nr;  // uniform over the wave
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const float xv = (row_ok && m < a.M) ? a.x[(int64_t)m * a.stride_x + row] : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[m][e] = fmaf(xv, w[e], acc[m][e]);
+    }
+  }
+
+  // Waves 1..3 hand their sums to wave 0, which adds them in wave order.
+  if (wave > 0) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[wave - 1][m][8 * lane + e] = acc[m][e];
+  }
+  __syncthreads();
+  if (wave != 0 || !live) return;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    if (m >= a.M) break;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[e] = acc[m][e];
+#pragma unroll
+      for (int w = 0; w < kWideWaves - 1; ++w) v[e] += red[w][m][8 * lane + e];
+    }
+    if (a.splits > 1) {
+      float* dst = a.partial + ((int64_t)split * a.M + m) * a.n_count + lc;
+      *reinterpret_cast<floatx4*>(dst) = floatx4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<floatx4*>(dst + 4) = floatx4{v[4], v[5], v[6], v[7]};
+    } else {
+      float* dst = a.out + (int64_t)m * a.stride_out + lc;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[e] = a.bias[col + e] + v[e];
+    }
+  }
+}
+
+// out[m, c] = bias + sum over splits (in split order) of the partials: a
+// workgroup stages [splits][64 columns] of one row m in LDS with parallel
+// loads, then 64 threads add each column's splits in order.
+constexpr int kMergeCols = 64;
+constexpr int kMergeMaxSplits = 128;
+__global__ __launch_bounds__(kReduceThreads) void nf24_gemv_merge_kernel(
+    const float* partial, const float* bias, float* out, int M, int count, int n_start,
+    int stride_out, int splits) {
+  __shared__ float part[kMergeMaxSplits][kMergeCols + 1];
+  const int chunks = (count + kMergeCols - 1) / kMergeCols;
+  const int m = blockIdx.x / chunks;
+  const int c0 = (blockIdx.x % chunks) * kMergeCols;
+  for (int i = threadIdx.x; i < splits * kMergeCols; i += kReduceThreads) {
+    const int s = i / kMergeCols, c = i % kMergeCols;
+    part[s][c] = c0 + c < count ? partial[((int64_t)s * M + m) * count + c0 + c] : 0.0f;
+  }
+  __syncthreads();
+  const int c = threadIdx.x;
+  if (c >= kMergeCols || c0 + c >= count) return;
+  float v = part[0][c];
+  for (int s = 1; s < splits; ++s) v += part[s][c];
+  out[(int64_t)m * stride_out + c0 + c] = bias[n_start + c0 + c] + v;
+}
+
+template <int MT>
+int launch_wide(GemvArgs a, hipStream_t stream) {
+  const dim3 grid((unsigned)(((a.n_count + kWideCols - 1) / kWideCols) * a.splits));
+  if (a.k_per_split == kWideWaves * 16)
+    hipLaunchKernelGGL((nf24_gemv_wide_kernel<MT, 16>), grid, dim3(kWideWaves * 64), 0, stream, a);
+  else
+    hipLaunchKernelGGL((nf24_gemv_wide_kernel<MT, 8>), grid, dim3(kWideWaves * 64), 0, stream, a);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
 template <int MT, int W>
 int launch_mt(GemvArgs a, int cgroups, int splits, hipStream_t stream) {
   const size_t x_bytes = (size_t)MT * a.k_per_split * 4;
@@ -177,6 +319,40 @@ int launch_mt(GemvArgs a, int cgroups, int splits, hipStream_t stream) {
 // bytes; a split costs a second, small kernel.
 int launch_nf24_gemv(const GemmParams& p, hipStream_t stream) {
   if (p.M < 1 || p.M > 32) return kErrDims;
+  const bool wide = p.M <= 8 && ((p.N | p.n_start | p.n_count) & 7) == 0 &&
+                    (reinterpret_cast<uintptr_t>(p.code01) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(p.q2) & 7) == 0 &&
+                    (reinterpret_cast<uintptr_t>(p.scale) & 15) == 0;
+  if (wide) {
+    // 16 rows per wave (64 per workgroup); 8 when that leaves fewer than 128
+    // workgroups (one K split per 64 or 32 rows).
+    const int slabs = (p.n_count + kWideCols - 1) / kWideCols;
+    int kps = kWideWaves * 16;
+    if ((int64_t)slabs * ((p.K + kps - 1) / kps) < 128) kps /= 2;
+    const int splits = (p.K + kps - 1) / kps;
+    if (splits <= kMergeMaxSplits) {
+      GemvArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out, nullptr, p.M, p.K, p.N,
+                 p.n_start, p.n_count, p.stride_x, p.stride_out, kps, splits};
+      if (splits > 1) {
+        a.partial = static_cast<float*>(
+            stream_workspace(stream, (size_t)splits * p.M * p.n_count * 4, kSlotGemvPartial));
+        if (a.partial == nullptr) return kErrWorkspace;
+      }
+      int st;
+      switch (p.M <= 1 ? 1 : p.M <= 2 ? 2 : p.M <= 4 ? 4 : 8) {
+        case 1: st = launch_wide<1>(a, stream); break;
+        case 2: st = launch_wide<2>(a, stream); break;
+        case 4: st = launch_wide<4>(a, stream); break;
+        default: st = launch_wide<8>(a, stream); break;
+      }
+      if (st != kOk || splits == 1) return st;
+      const int chunks = (p.n_count + kMergeCols - 1) / kMergeCols;
+      hipLaunchKernelGGL(nf24_gemv_merge_kernel, dim3((unsigned)(p.M * chunks)), dim3(kReduceThreads),
+                         0, stream, a.partial, p.bias, p.out, p.M, p.n_count, p.n_start,
+                         p.stride_out, splits);
+      return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+    }
+  }
   const int mt = p.M <= 1 ? 1 : p.M <= 2 ? 2 : p.M <= 4 ? 4 : p.M <= 8 ? 8 : p.M <= 16 ? 16 : 32;
   const int w = mt <= 4 ? 16 : mt <= 8 ? 8 : 4;
   const int cgroups = (p.n_count + kCols - 1) / kCols;
