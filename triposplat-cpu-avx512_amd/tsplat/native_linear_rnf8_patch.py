@@ -261,3 +261,20 @@ def apply_triposplat_native_rnf8_avx512_patch(
         "runtime": runtime,
         "semantics": "All selected Linear weights are decoded in registers inside the gfx950 NF24 GEMM (fp32 MFMA accumulate); no fp32 weight copy is kept.",
     }
+
+
+def redirect_native_linear(flow_model, **kwargs):
+    """The hook the reference's NF24 runners install in place of
+    ``apply_triposplat_native_linear_avx512_patch``
+    (scripts/run_triposplat_rnf8_param_batch.py:40-50): the Linear patch with
+    the stage count / residual mode from TRIPOSPLAT_RNF8_STAGES and
+    TRIPOSPLAT_RNF8_RESIDUAL_MODE (defaults 3 / nf24_i16, the only form this
+    library implements)."""
+    import os
+
+    return apply_triposplat_native_rnf8_avx512_patch(
+        flow_model,
+        stages=int(os.environ.get("TRIPOSPLAT_RNF8_STAGES", "3")),
+        residual_mode=os.environ.get("TRIPOSPLAT_RNF8_RESIDUAL_MODE", "nf24_i16"),
+        **kwargs,
+    )
