@@ -36,6 +36,7 @@ sys.path.insert(0, str(ROOT / "triposplat-cpu-avx512_amd"))
 
 METRIC = "NF24 GEMM + exact SDPA TFLOP/s (% MFMA peak) at L=16384; s/denoise step"
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
+PEAK_BF16_MFMA = 2500.0  # TFLOP/s, MI355X dense bf16 matrix
 PEAK_HBM = 8000.0       # GB/s
 
 
@@ -225,6 +226,26 @@ def run_gemm(torch, dev, iters):
     g_ms = sorted(time_events(torch, step, iters) for _ in range(5))[2]
     g_flop = 2.0 * M * N * K
     g_tf = g_flop / (g_ms * 1e-3) / 1e12
+    strict = gout.clone()
+    opt_in = {}
+    for precision in ("bf16", "bf16x3"):
+        # the opt-in bf16-MFMA products, with their error against strict fp32
+        def step_p(p=precision):
+            nf24_linear(x, codes[0], codes[1], scales[0], bias, out=gout, precision=p)
+
+        for _ in range(3):
+            step_p()
+        torch.cuda.synchronize()
+        p_ms = sorted(time_events(torch, step_p, iters) for _ in range(5))[2]
+        d = (gout.double() - strict.double())
+        p_tf = g_flop / (p_ms * 1e-3) / 1e12
+        opt_in[precision] = {
+            "ms": p_ms, "tflops": p_tf, "frac_bf16_mfma_peak": p_tf / PEAK_BF16_MFMA,
+            "speedup_vs_fp32": g_ms / p_ms,
+            "rmse_vs_fp32": float(d.pow(2).mean().sqrt()),
+            "rel_rmse_vs_fp32": float(d.pow(2).mean().sqrt() / strict.double().pow(2).mean().sqrt()),
+            "max_abs_vs_fp32": float(d.abs().max()),
+        }
     return {
         "workload": "configs[0] NF24 Linear X[4096x1024] @ W[1024x3072] + bias, fp32 MFMA accumulate",
         "ms": g_ms,
@@ -232,6 +253,7 @@ def run_gemm(torch, dev, iters):
         "frac_fp32_mfma_peak": g_tf / PEAK_FP32_MFMA,
         "algorithmic_bytes": float(M * K * 4 + K * N * 3 + N * 8 + M * N * 4),
         "traffic": load_traffic("nf24_gemm_config0"),
+        "opt_in_bf16": opt_in,
     }
 
 
@@ -281,12 +303,32 @@ def run_flow(torch, dev, steps, with_cpu, validate):
         times.append(time.perf_counter() - t0)
     step_s = sorted(times)[len(times) // 2]
     step_flop = 2 * cfg.blocks * per_branch_flop
+    # opt-in: the block Linears with bf16x3 products (timestep / io Linears
+    # and everything else unchanged); latent RMSE against the strict step
+    model.set_precision("bf16x3")
+    model.euler_cfg_step(z, c)
+    torch.cuda.synchronize()
+    times3 = []
+    for _ in range(max(1, steps)):
+        t0 = time.perf_counter()
+        zn3, v3 = model.euler_cfg_step(z, c)
+        torch.cuda.synchronize()
+        times3.append(time.perf_counter() - t0)
+    model.set_precision("fp32")
+    step3_s = sorted(times3)[len(times3) // 2]
+    bf16x3_step = {
+        "s_per_denoise_step": step3_s, "speedup_vs_fp32": step_s / step3_s,
+        "latent_rmse_vs_fp32_step": float((zn3.double() - zn.double()).pow(2).mean().sqrt()),
+        "velocity_rmse_vs_fp32_step": float((v3.double() - v.double()).pow(2).mean().sqrt()),
+    }
+    del zn3, v3
     out = {
         "config3_block": {"workload": "configs[3] one flow block, L=16384 latent + 2048 condition tokens, one branch",
                           "ms": blk_ms, "tflops": per_branch_flop / (blk_ms * 1e-3) / 1e12},
         "config4_step": {"workload": "configs[4] 28 blocks, CFG batch 2, one Euler step (guidance 3, shift 3)",
                          "s_per_denoise_step": step_s, "tflops": step_flop / step_s / 1e12,
-                         "model_setup_s": setup_s, "finite": bool(torch.isfinite(zn).all().item())},
+                         "model_setup_s": setup_s, "finite": bool(torch.isfinite(zn).all().item()),
+                         "opt_in_bf16x3_block_linears": bf16x3_step},
     }
     if with_cpu or validate:
         sys.path.insert(0, str(ROOT / "oracle"))

@@ -219,6 +219,32 @@ int tsplat_nf24_gemm_epilogue_async(const float* x, const int16_t* code01_t, con
                                     int stride_x, int stride_out, int epilogue, const float* gate,
                                     int64_t gate_stride, int rows_per_batch, void* stream);
 
+/* ---------------- opt-in bf16-MFMA precision ----------------------------- */
+/* No counterpart in the reference, whose NF24 Linear is fp32 only; its
+ * bf16 evidence is a round-trip probe (triposplat_bf16_roundtrip_patch.py:
+ * 7-53, torch's round-to-nearest-even float32 -> bfloat16).  `precision`:
+ *   0 strict: fp32 products (the result of tsplat_nf24_gemm_epilogue_async)
+ *   1 bf16:   bf16(x) * bf16(w) on bf16 MFMA, fp32 accumulation
+ *   2 bf16x3: xh*wh + xh*wl + xl*wh, xh = bf16(x), xl = bf16(x - xh), same
+ *             for w; about 16 significant bits per product
+ * bf16() rounds the fp32 value (w: the exact NF24 decode) to nearest even.
+ * Calls with M <= 32 run the strict kernels in every precision (they are
+ * bound by the weight stream).  Other arguments and status codes as
+ * tsplat_nf24_gemm_epilogue_async; -2 for an unknown precision. */
+int tsplat_nf24_gemm_precision_async(const float* x, const int16_t* code01_t,
+                                     const int8_t* q2_t, const float* scale, const float* bias,
+                                     float* out, int M, int K, int N, int output_start,
+                                     int output_count, int stride_x, int stride_out, int epilogue,
+                                     const float* gate, int64_t gate_stride, int rows_per_batch,
+                                     int precision, void* stream);
+/* tsplat_gemm_nf24_qkv_direct_async with the projection in `precision`
+ * (the RoPE / RMSNorm / pack epilogue is the same fp32 arithmetic). */
+int tsplat_gemm_nf24_qkv_direct_precision_async(
+    const float* x, const int16_t* code01_t, const int8_t* q2_t, const float* scale,
+    const float* bias, const float* frequencies, const float* q_gamma, const float* k_gamma,
+    float* q_bhld, float* packed_k, float* packed_v, int B, int L, int K, int N, int H, int D,
+    int L_padded, int frequency_batches, int precision, void* stream);
+
 /* ---------------- flow-block elementwise -------------------------------- */
 /* Bit-identical per element to the reference kernels (same operation order,
  * same fused multiply-adds, the reductions in the AVX-512 lane order). */

@@ -112,6 +112,56 @@ def decode_nf24(code01_t, q2_t, scale):
 
 
 # --------------------------------------------------------------------------
+# Opt-in bf16-MFMA precision of the NF24 GEMM.  The reference has no bf16
+# GEMM; its bf16 evidence is the float32 -> bfloat16 -> float32 round trip of
+# scripts/triposplat_bf16_roundtrip_patch.py:27-31 (torch's conversion, round
+# to nearest even), the rounding bf16_round restates.  Pinned in
+# tests/test_oracle.py against torch's conversion, by the split invariants
+# and by operands that are exact in bf16 (the products then need no rounding).
+def bf16_round(a):
+    """fp32 -> nearest bf16, ties to even, returned as fp32 (finite inputs)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32).reshape(np.shape(a))
+
+
+def bf16_split(a):
+    """(hi, lo) = (bf16(a), bf16(a - hi)); a - hi is exact in fp32."""
+    a = np.asarray(a, dtype=np.float32)
+    hi = bf16_round(a)
+    return hi, bf16_round((a - hi).astype(np.float32))
+
+
+def nf24_gemm_bf16_terms(x, code01_t, q2_t, scale, bias, precision):
+    """float64 value of bias + sum_k of the products the bf16 modes form:
+    "bf16": xh*wh; "bf16x3": xh*wh + xh*wl + xl*wh (w = the exact decode).
+    Products of two bf16 values are exact in fp32 and float64, so a device
+    result differs from this only by its fp32 summation order."""
+    if precision not in ("bf16", "bf16x3"):
+        raise ValueError(precision)
+    w = decode_nf24(code01_t, q2_t, scale)
+    xh, xl = bf16_split(x)
+    wh, wl = bf16_split(w)
+    f = lambda a: a.astype(np.float64)  # noqa: E731
+    y = f(xh) @ f(wh)
+    if precision == "bf16x3":
+        y += f(xh) @ f(wl) + f(xl) @ f(wh)
+    return y + f(np.asarray(bias, np.float32))[None, :]
+
+
+def nf24_gemm_bf16_abs_terms(x, code01_t, q2_t, scale, bias, precision):
+    """|bias| + sum_k |terms| of nf24_gemm_bf16_terms (for order bounds)."""
+    w = decode_nf24(code01_t, q2_t, scale)
+    xh, xl = bf16_split(x)
+    wh, wl = bf16_split(w)
+    f = lambda a: np.abs(a.astype(np.float64))  # noqa: E731
+    y = f(xh) @ f(wh)
+    if precision == "bf16x3":
+        y += f(xh) @ f(wl) + f(xl) @ f(wh)
+    return y + f(np.asarray(bias, np.float32))[None, :]
+
+
+# --------------------------------------------------------------------------
 # SDPA
 def sdpa_q8t512(q, k, v, key_bias=None, bias_head_stride=0):
     """Exact SDPA of scripts/native_sdpa_avx512_exact_q8t512.c:137-332.

@@ -62,3 +62,35 @@ def test_flow_block_matches_cpu(oracle, cuda):
     want = cpu.block(cpu.p["blocks"][0], x, c, t_mod)
     rel = combined_rmse(got, want) / float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
     assert rel <= 2e-6, rel
+
+
+def test_flow_step_opt_in_bf16(oracle, cuda):
+    """The opt-in bf16-MFMA block Linears: bf16x3 products keep the step
+    within the latent gate against the CPU fp32 path; plain bf16 is reported
+    (it is expected to miss the gate) and must be coarser than bf16x3."""
+    import torch
+    from flow_ref import CpuFlow, combined_rmse
+    from tsplat.flow import FlowConfig, FlowModel
+
+    cfg = FlowConfig(hidden=256, heads=4, blocks=4, latent_tokens=300, cond_tokens=70)
+    model = FlowModel(cfg, cuda)
+    z, c = _inputs(cfg, seed=30)
+    zd, cd = torch.from_numpy(z).to(cuda), torch.from_numpy(c).to(cuda)
+    strict, _ = model.euler_cfg_step(zd, cd)
+    res = {}
+    for p in ("bf16x3", "bf16"):
+        model.set_precision(p)
+        zn, _ = model.euler_cfg_step(zd, cd)
+        res[p] = zn.cpu().numpy()
+    model.set_precision("fp32")
+    again, _ = model.euler_cfg_step(zd, cd)
+    torch.cuda.synchronize()
+    assert torch.equal(again, strict)
+    zn_c, _ = CpuFlow(model.host(), cfg, backend="oracle").euler_cfg_step(z, c)
+    rm = {p: combined_rmse(a, zn_c) for p, a in res.items()}
+    rm["fp32"] = combined_rmse(strict.cpu().numpy(), zn_c)
+    print({"latent_rmse_vs_cpu": rm})
+    assert np.all(np.isfinite(res["bf16"])) and np.all(np.isfinite(res["bf16x3"]))
+    assert rm["bf16x3"] <= 1e-4
+    assert not np.array_equal(res["bf16x3"], strict.cpu().numpy())
+    assert rm["bf16"] > 4 * rm["bf16x3"]

@@ -1,0 +1,213 @@
+"""GPU parity of the opt-in bf16-MFMA precision modes of the NF24 GEMM
+(tsplat_nf24_gemm_precision_async, tsplat_gemm_nf24_qkv_direct_precision_async).
+
+Oracle: oracle.nf24_gemm_bf16_terms, the float64 value of the terms the mode
+defines (bf16: xh*wh; bf16x3: xh*wh + xh*wl + xl*wh, bf16 = round to nearest
+even of the fp32 value).  Those products are exact in fp32, so the device
+result may differ from the oracle only by its fp32 summation order over the
+T*K products and the bias (T = 1 or 3): within 2 * gamma_{T*K+1} * sum|terms|
+(Higham Thm 3.1), checked elementwise.  The relative RMSE of each mode
+against the strict fp32 path is reported and held to its expected band
+(bf16 about 2^-9, bf16x3 about 2^-17 of the output RMS).  The epilogues and
+the fused QKV postprocess are fp32 functions of the accumulator, so each
+equals, bit for bit, the oracle's elementwise step / postprocess applied to
+the same mode's plain GEMM output.  Tile shapes sum in one order, so rows
+computed by the 128-row tail launch equal the same rows inside 256-row tiles.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _parity import U, seeded_linear, stats
+
+pytestmark = pytest.mark.gpu
+
+MODES = {"bf16": 1, "bf16x3": 2}
+TERMS = {"bf16": 1, "bf16x3": 3}
+
+
+def _dev(torch, a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def _run(torch, hiplib, device, x, c01, q2, s, b, precision, epilogue=0, out=None, gate=None,
+         rows_per_batch=1, stride_x=None):
+    M, K = x.shape
+    N = c01.shape[1]
+    sx = K if stride_x is None else stride_x
+    xs = np.zeros((M, sx), np.float32)
+    xs[:, :K] = x
+    d = [_dev(torch, a, device) for a in (xs, c01, q2, s, b)]
+    o = (torch.full((M, N), float("nan"), dtype=torch.float32, device=device) if out is None
+         else _dev(torch, out, device))
+    g = _dev(torch, gate, device) if gate is not None else None
+    st = hiplib.tsplat_nf24_gemm_precision_async(
+        d[0].data_ptr(), d[1].data_ptr(), d[2].data_ptr(), d[3].data_ptr(), d[4].data_ptr(),
+        o.data_ptr(), M, K, N, 0, N, sx, N, epilogue, g.data_ptr() if g is not None else None,
+        N if g is not None else 0, rows_per_batch, MODES.get(precision, 0),
+        torch.cuda.current_stream(device).cuda_stream)
+    assert st == 0, st
+    torch.cuda.synchronize(device)
+    return o.cpu().numpy()
+
+
+def _check_terms(oracle, x, c01, q2, s, b, got, precision):
+    ref = oracle.nf24_gemm_bf16_terms(x, c01, q2, s, b, precision)
+    mag = oracle.nf24_gemm_bf16_abs_terms(x, c01, q2, s, b, precision)
+    n = TERMS[precision] * x.shape[1] + 1
+    bound = 2.0 * (n * U / (1.0 - n * U)) * mag
+    diff = np.abs(got.astype(np.float64) - ref)
+    assert np.all(np.isfinite(got))
+    assert np.all(diff <= bound), (float(diff.max()), float((diff - bound).max()))
+    return stats(got, ref)
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+@pytest.mark.parametrize("M,K,N", [
+    (300, 1024, 3072),   # 256 x 256 tiles, partial row tile
+    (64, 256, 512),      # 128 x 128 tiles
+    (520, 96, 200),      # K not a multiple of 32, N below one 256-column tile
+    (100, 33, 50),       # K, N not multiples of 4: the scalar-load kernel
+    (544, 256, 512),     # 512 + 32 tail rows as a 128-row launch
+])
+def test_bf16_gemm_matches_oracle(oracle, cuda, hiplib, precision, M, K, N):
+    import torch
+
+    print(f"bf16 gemm {precision} M={M} K={K} N={N}", flush=True)
+    x, w, b = seeded_linear(M * 7 + K + N, M, K, N, w_scale=0.02)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    got = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision)
+    e = _check_terms(oracle, x, c01, q2, s, b, got, precision)
+    assert e["rel_rmse"] < 1e-6, e
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+def test_bf16_unaligned_x_stride(oracle, cuda, hiplib, precision):
+    import torch
+
+    x, w, b = seeded_linear(11, 272, 256, 256, w_scale=0.02)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    got = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision, stride_x=258)
+    _check_terms(oracle, x, c01, q2, s, b, got, precision)
+
+
+def test_bf16_few_rows_run_strict(oracle, cuda, hiplib):
+    """M <= 32 runs the strict kernels in every precision."""
+    import torch
+
+    x, w, b = seeded_linear(5, 16, 1024, 1024, w_scale=0.02)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    strict = _run(torch, hiplib, cuda, x, c01, q2, s, b, "fp32")
+    for p in MODES:
+        got = _run(torch, hiplib, cuda, x, c01, q2, s, b, p)
+        assert np.array_equal(got.view(np.uint32), strict.view(np.uint32))
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+def test_bf16_tail_rows_bitwise(oracle, cuda, hiplib, precision):
+    import torch
+
+    M, K, N = 528, 256, 512                       # 512 rows of 256-row tiles + 16 tail rows
+    x, w, b = seeded_linear(21, 768, K, N, w_scale=0.02)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    got = _run(torch, hiplib, cuda, x[:M], c01, q2, s, b, precision)
+    head = _run(torch, hiplib, cuda, x[:512], c01, q2, s, b, precision)
+    full = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision)
+    small = _run(torch, hiplib, cuda, x[:128], c01, q2, s, b[:N], precision)   # 128-row tiles
+    assert np.array_equal(got[:512].view(np.uint32), head.view(np.uint32))
+    assert np.array_equal(got[512:].view(np.uint32), full[512:M].view(np.uint32))
+    assert np.array_equal(small.view(np.uint32), full[:128].view(np.uint32))
+    _check_terms(oracle, x[:M], c01, q2, s, b, got, precision)
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+@pytest.mark.parametrize("M", [300, 100])
+def test_bf16_epilogues(oracle, cuda, hiplib, precision, M):
+    import torch
+
+    K, N, B = 256, 512, 2
+    x, w, b = seeded_linear(31 + M, M, K, N, w_scale=0.02)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    acc = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision)
+    r = np.random.default_rng(M)
+    gelu = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision, epilogue=2)
+    exp = np.empty_like(acc)
+    assert oracle.ew("gelu_tanh", acc, exp, acc.size) == 0
+    assert np.array_equal(gelu.view(np.uint32), exp.view(np.uint32))
+    base = r.standard_normal((M, N)).astype(np.float32)
+    gate = r.standard_normal((B, N)).astype(np.float32)
+    gated = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision, epilogue=3, out=base, gate=gate,
+                 rows_per_batch=M // B)
+    exp, delta = base.copy(), acc.copy()
+    assert oracle.ew("gated_residual_inplace", exp, delta, gate, B, M // B, N) == 0
+    assert np.array_equal(gated.view(np.uint32), exp.view(np.uint32))
+    added = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision, epilogue=4, out=base)
+    exp = base.copy()
+    assert oracle.ew("add_inplace", exp, acc, exp.size) == 0
+    assert np.array_equal(added.view(np.uint32), exp.view(np.uint32))
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+@pytest.mark.parametrize("B,L", [(1, 300), (2, 70)])
+def test_bf16_qkv_direct(oracle, cuda, hiplib, precision, B, L):
+    import torch
+    from tsplat.qkv import gemm_nf24_qkv_direct
+
+    H = 4
+    C = 64 * H
+    x, w, b = seeded_linear(41 + L, B * L, C, 3 * C, w_scale=0.02)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    r = np.random.default_rng(L)
+    ang = r.uniform(-np.pi, np.pi, (1, L, H, 32))
+    freqs = np.stack([np.cos(ang), np.sin(ang)], -1).reshape(1, L, H, 64).astype(np.float32)
+    qg = (1 + 0.05 * r.standard_normal((H, 64))).astype(np.float32)
+    kg = (1 + 0.05 * r.standard_normal((H, 64))).astype(np.float32)
+    qkv = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision)
+    exp = oracle.qkv_rope_rmsnorm_pack(qkv, freqs, qg, kg, B, L, H)
+    d = {k: _dev(torch, a, cuda) for k, a in (("x", x), ("c", c01), ("q", q2), ("s", s), ("b", b),
+                                             ("f", freqs), ("qg", qg), ("kg", kg))}
+    got = gemm_nf24_qkv_direct(d["x"], d["c"], d["q"], d["s"], d["b"], d["f"], d["qg"], d["kg"], B, L, H,
+                               precision=precision)
+    torch.cuda.synchronize(cuda)
+    for g_, e_ in zip(got, exp):
+        assert np.array_equal(g_.cpu().numpy().view(np.uint32), np.asarray(e_).view(np.uint32))
+
+
+def test_bf16_config0_rmse_vs_strict(oracle, cuda, hiplib):
+    """configs[0] (X [4096 x 1024], W [3072 x 1024] ~ 0.02 N(0,1)): each mode
+    against strict fp32, and sampled rows against the oracle terms."""
+    import torch
+    from tsplat.nf24 import nf24_linear
+
+    M, K, N = 4096, 1024, 3072
+    r = np.random.default_rng(0)
+    x = r.standard_normal((M, K), dtype=np.float32)
+    w = (r.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    b = (r.standard_normal(N, dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    d = [_dev(torch, a, cuda) for a in (x, c01, q2, s, b)]
+    strict = nf24_linear(*d).cpu().numpy()
+    rows = np.sort(r.choice(M, 48, replace=False))
+    rel = {}
+    for p in MODES:
+        got = nf24_linear(*d, precision=p).cpu().numpy()
+        _check_terms(oracle, x[rows], c01, q2, s, b, got[rows], p)
+        rel[p] = stats(got, strict)["rel_rmse"]
+    print("relative RMSE vs strict fp32:", rel, flush=True)
+    assert 2.0 ** -11 < rel["bf16"] < 2.0 ** -7, rel
+    assert rel["bf16x3"] < 2.0 ** -14, rel
+
+
+def test_bf16_rejects_unknown_precision(cuda, hiplib):
+    import torch
+
+    x = torch.zeros((64, 64), device=cuda)
+    c = torch.zeros((64, 64), dtype=torch.int16, device=cuda)
+    q = torch.zeros((64, 64), dtype=torch.int8, device=cuda)
+    v = torch.zeros(64, device=cuda)
+    out = torch.zeros((64, 64), device=cuda)
+    st = hiplib.tsplat_nf24_gemm_precision_async(x.data_ptr(), c.data_ptr(), q.data_ptr(), v.data_ptr(),
+                                                 v.data_ptr(), out.data_ptr(), 64, 64, 64, 0, 64, 64, 64,
+                                                 0, None, 0, 1, 3, None)
+    assert st == -2

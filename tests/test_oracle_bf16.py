@@ -1,0 +1,98 @@
+"""Pinning of the oracle's bf16 precision modes (no GPU).
+
+oracle.bf16_round is checked bit for bit against torch's float32 ->
+bfloat16 conversion (the conversion of the reference's bf16 round-trip
+probe, scripts/triposplat_bf16_roundtrip_patch.py:27-31) on random values
+and on the cases a rounding mistake shows first: exact ties with even and
+odd last kept bits, neighbours of ties, subnormals, the overflow threshold.
+The split and the two GEMM term sums are pinned by what the arithmetic
+fixes: hi and lo are bf16 values with |a - hi - lo| <= 2^-16 |a|; operands
+exact in bf16 make both modes equal the exact product; generic operands stay
+within the bf16 / bf16x3 product error bounds (2^-7 and 2^-14 of sum|x w|)
+and the bf16 mode is measurably coarser than bf16x3.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _parity import gemm_f64, gemm_abs_f64
+
+
+def _torch_bf16(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).to(torch.float32).numpy()
+
+
+def test_bf16_round_matches_torch(oracle):
+    r = np.random.default_rng(0)
+    vals = [r.standard_normal(20000).astype(np.float32) * np.float32(s) for s in (1e-30, 1e-3, 1.0, 1e4, 1e30)]
+    hi_bits = r.integers(0, 1 << 16, 4096, dtype=np.uint32) << 16
+    ties = (hi_bits | 0x8000).view(np.float32)               # exact ties, both parities of the kept lsb
+    below = (hi_bits | 0x7FFF).view(np.float32)
+    above = (hi_bits | 0x8001).view(np.float32)
+    sub = (r.integers(1, 1 << 23, 4096, dtype=np.uint32)).view(np.float32)  # subnormals
+    edge = np.array([0.0, -0.0, 3.3895314e38, 3.3961776e38, -3.3961776e38, 1.0 + 2 ** -8,
+                     1.0 + 3 * 2 ** -8, np.finfo(np.float32).max], np.float32)
+    a = np.concatenate(vals + [ties, below, above, sub, edge])
+    a = a[np.isfinite(a) & ~np.isnan(a)]
+    got = oracle.bf16_round(a)
+    exp = _torch_bf16(a)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+    # ties really went both ways (round to even), so the case is exercised
+    t = oracle.bf16_round(ties).view(np.uint32)
+    assert np.any(t > (hi_bits & 0xFFFF0000)) and np.any(t == (hi_bits & 0xFFFF0000))
+
+
+def test_bf16_split_invariants(oracle):
+    r = np.random.default_rng(1)
+    a = (r.standard_normal(50000) * np.exp(r.uniform(-20, 20, 50000))).astype(np.float32)
+    hi, lo = oracle.bf16_split(a)
+    assert not np.any(hi.view(np.uint32) & 0xFFFF) and not np.any(lo.view(np.uint32) & 0xFFFF)
+    res = np.abs(a.astype(np.float64) - hi.astype(np.float64) - lo.astype(np.float64))
+    assert np.all(res <= 2.0 ** -16 * np.abs(a.astype(np.float64)))
+    assert np.mean(res > 0) > 0.9          # 24 bits do not fit in 16: the residual is real
+    assert np.all(np.abs(lo) <= 2.0 ** -8 * np.abs(hi) * (1 + 2.0 ** -7))
+
+
+def _exact_bf16_linear(oracle, seed, M, K, N):
+    """x exact in bf16; NF24 codes with q2 = 0, |q01| < 128 and a power-of-two
+    scale, so every decoded weight has at most 8 significant bits."""
+    r = np.random.default_rng(seed)
+    x = oracle.bf16_round(r.standard_normal((M, K)).astype(np.float32))
+    c01 = r.integers(-127, 128, (K, N)).astype(np.int16)
+    q2 = np.zeros((K, N), np.int8)
+    s = np.full(N, 2.0 ** -14, np.float32)
+    b = r.standard_normal(N).astype(np.float32) * np.float32(0.01)
+    return x, c01, q2, s, b
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+def test_bf16_terms_exact_operands(oracle, precision):
+    x, c01, q2, s, b = _exact_bf16_linear(oracle, 2, 37, 96, 53)
+    w = oracle.decode_nf24(c01, q2, s)
+    assert np.array_equal(oracle.bf16_round(w), w)
+    got = oracle.nf24_gemm_bf16_terms(x, c01, q2, s, b, precision)
+    assert got.shape == (37, 53)
+    np.testing.assert_allclose(got, gemm_f64(x, w, b), rtol=0, atol=1e-12)
+
+
+def test_bf16_terms_error_bounds(oracle):
+    r = np.random.default_rng(3)
+    M, K, N = 64, 512, 96
+    x = r.standard_normal((M, K)).astype(np.float32)
+    w = (r.standard_normal((N, K)) * 0.02).astype(np.float32)
+    b = (r.standard_normal(N) * 0.01).astype(np.float32)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    wd = oracle.decode_nf24(c01, q2, s)
+    exact = gemm_f64(x, wd, b)
+    mag = gemm_abs_f64(x, wd, np.zeros_like(b))
+    e1 = oracle.nf24_gemm_bf16_terms(x, c01, q2, s, b, "bf16") - exact
+    e3 = oracle.nf24_gemm_bf16_terms(x, c01, q2, s, b, "bf16x3") - exact
+    assert np.all(np.abs(e1) <= 2.0 ** -7 * mag)
+    assert np.all(np.abs(e3) <= 2.0 ** -14 * mag)
+    rel1 = np.sqrt(np.mean(e1 ** 2) / np.mean(exact ** 2))
+    rel3 = np.sqrt(np.mean(e3 ** 2) / np.mean(exact ** 2))
+    assert 2.0 ** -12 < rel1 < 2.0 ** -6, rel1     # bf16 rounding is applied
+    assert rel3 < rel1 / 64, (rel1, rel3)          # the lo terms recover ~8 bits

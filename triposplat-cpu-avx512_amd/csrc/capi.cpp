@@ -64,7 +64,7 @@ using namespace tsplat;
 namespace {
 
 constexpr int kHeadDim = 64;
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 
 std::atomic<uint64_t> g_sdpa_calls{0};
 std::atomic<uint64_t> g_sdpa_ns{0};
@@ -184,9 +184,12 @@ int selected_checked(const float* q, const float* kv, const float* freqs, const 
 int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
                        const float* scale, const float* bias, const float* freqs,
                        const float* qg, const float* kg, float* q, float* pk, float* pv, int B,
-                       int L, int K, int N, int H, int D, int Lp, int fb, hipStream_t stream) {
+                       int L, int K, int N, int H, int D, int Lp, int fb, hipStream_t stream,
+                       int precision = kPrecisionFp32) {
   if (!x || !code01 || !q2 || !scale || !bias || !freqs || !qg || !kg || !q || !pk || !pv)
     return kErrNull;
+  if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
+    return kErrDims;
   if (B <= 0 || L <= 0 || K <= 0 || H <= 0 || D != kHeadDim || N != 3 * H * D || Lp < L ||
       (Lp & 15) != 0 || (fb != 1 && fb != B))
     return kErrDims;
@@ -206,7 +209,7 @@ int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
   TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * Lp * 4));
   TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lp * 4));
   // RoPE, RMSNorm and the q / packed k,v stores run in the GEMM's epilogue.
-  QkvFusedParams p{{x, code01, q2, scale, bias, nullptr, (int)M, K, N, 0, N, K, N},
+  QkvFusedParams p{{x, code01, q2, scale, bias, nullptr, (int)M, K, N, 0, N, K, N, precision},
                    freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb};
   const int st = launch_nf24_gemm_qkv(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
@@ -444,6 +447,16 @@ int tsplat_gemm_nf24_qkv_direct_async(const float* x, const int16_t* code01_t, c
   return qkv_direct_checked(x, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, q_bhld,
                             packed_k, packed_v, B, L, K, N, H, D, L_padded, frequency_batches,
                             static_cast<hipStream_t>(stream));
+}
+
+int tsplat_gemm_nf24_qkv_direct_precision_async(
+    const float* x, const int16_t* code01_t, const int8_t* q2_t, const float* scale,
+    const float* bias, const float* frequencies, const float* q_gamma, const float* k_gamma,
+    float* q_bhld, float* packed_k, float* packed_v, int B, int L, int K, int N, int H, int D,
+    int L_padded, int frequency_batches, int precision, void* stream) {
+  return qkv_direct_checked(x, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, q_bhld,
+                            packed_k, packed_v, B, L, K, N, H, D, L_padded, frequency_batches,
+                            static_cast<hipStream_t>(stream), precision);
 }
 
 // ------------------------------------------------------------------ packer

@@ -284,17 +284,20 @@ int tsplat_ab2_update_async(float* sample, const float* prediction,
                          elements_per_batch, as_stream(stream));
 }
 
-int tsplat_nf24_gemm_epilogue_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,
-                                    const float* scale, const float* bias, float* out, int M,
-                                    int K, int N, int output_start, int output_count,
-                                    int stride_x, int stride_out, int epilogue, const float* gate,
-                                    int64_t gate_stride, int rows_per_batch, void* stream) {
+int tsplat_nf24_gemm_precision_async(const float* x, const int16_t* code01_t,
+                                     const int8_t* q2_t, const float* scale, const float* bias,
+                                     float* out, int M, int K, int N, int output_start,
+                                     int output_count, int stride_x, int stride_out, int epilogue,
+                                     const float* gate, int64_t gate_stride, int rows_per_batch,
+                                     int precision, void* stream) {
   if (!x || !code01_t || !q2_t || !scale || !bias || !out) return kErrNull;
   if (M <= 0 || K <= 0 || N <= 0 || output_start < 0 || output_count <= 0) return kErrDims;
   if (output_start + output_count > N || stride_x < K || stride_out < output_count)
     return kErrRange;
   if (epilogue != kEpilogueStore && epilogue != kEpilogueGelu && epilogue != kEpilogueGated &&
       epilogue != kEpilogueAdd)
+    return kErrDims;
+  if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
     return kErrDims;
   TSPLAT_CHECK(check_dev(x, ((int64_t)(M - 1) * stride_x + K) * 4));
   TSPLAT_CHECK(check_dev(code01_t, (int64_t)K * N * 2));
@@ -309,9 +312,20 @@ int tsplat_nf24_gemm_epilogue_async(const float* x, const int16_t* code01_t, con
     TSPLAT_CHECK(check_dev(gate, ((batches - 1) * gate_stride + N) * 4));
   }
   GemmParams p{x, code01_t, q2_t, scale, bias, out, M, K, N, output_start, output_count,
-               stride_x, stride_out};
+               stride_x, stride_out, precision};
   GemmEpilogueParams e{epilogue, gate, gate_stride, rows_per_batch > 0 ? rows_per_batch : 1};
   return launched(launch_nf24_gemm_epilogue(p, e, as_stream(stream)));
+}
+
+int tsplat_nf24_gemm_epilogue_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,
+                                    const float* scale, const float* bias, float* out, int M,
+                                    int K, int N, int output_start, int output_count,
+                                    int stride_x, int stride_out, int epilogue, const float* gate,
+                                    int64_t gate_stride, int rows_per_batch, void* stream) {
+  return tsplat_nf24_gemm_precision_async(x, code01_t, q2_t, scale, bias, out, M, K, N,
+                                          output_start, output_count, stride_x, stride_out,
+                                          epilogue, gate, gate_stride, rows_per_batch,
+                                          kPrecisionFp32, stream);
 }
 
 }  // extern "C"

@@ -19,12 +19,12 @@
 // The next K step's codes and X are fetched into registers while the MFMAs
 // of the current step run (double-buffered LDS, one barrier per step).
 
-#include "tsplat_common.h"
-#include "tsplat_ew.h"
-#include "tsplat_launch.h"
+#include "nf24_gemm_common.h"
 
 namespace tsplat {
 namespace {
+
+using namespace nf24;
 
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int kMinWaves_ = 1>
 struct GemmCfg {
@@ -44,150 +44,6 @@ struct GemmCfg {
   static_assert(kTM % 32 == 0 && kTN % 32 == 0, "wave tile must be 32-aligned");
   static_assert(BK % 8 == 0 && BN % 2 == 0, "BK must be a multiple of 8, BN even");
 };
-
-// Fused QKV epilogue operands (kEpiQkv): rows are tokens b*L + l, columns
-// [q | k | v] with H heads of 64 each.
-struct QkvArgs {
-  const float* freqs;  // [fb, L, H, 64] interleaved (cos, sin)
-  const float* qg;     // [H, 64]
-  const float* kg;     // [H, 64]
-  float* q;            // [B, H, L, 64]
-  float* pk;           // [B, H, 64, Lpad]
-  float* pv;           // [B, H, 64, Lpad]
-  int L, H, Lpad, fb;
-};
-
-struct GemmArgs {
-  const float* x;
-  const int16_t* code01;
-  const int8_t* q2;
-  const float* scale;
-  const float* bias;
-  float* out;
-  int M, K, N, n_start, n_count, stride_x, stride_out;
-  QkvArgs e;
-  // kEpilogueGated: gate row of batch (row0 + m) / rows_per_batch
-  const float* gate;
-  int64_t gate_stride;
-  int rows_per_batch;
-  int row0;  // global index of row 0 of x / out (the epilogues' token mapping)
-};
-
-// kEpilogue* of tsplat_launch.h, plus the fused QKV epilogue.
-enum Epilogue : int { kEpiStore = kEpilogueStore, kEpiQkv = 1 };
-
-// ||y||^2 of one head row whose dims d and 32+d sit in lane d (r0, r1) of a
-// half-wave, summed in the reference's order (native_qkv_postprocess_v2_avx512.c:3-24):
-// the AVX-512 lane j chains fma over dims j, 16+j, 32+j, 48+j, then the
-// _mm512_reduce_add_ps tree.  Lanes j < 16 of the half gather the two dims
-// they lack from lane j+16; every lane receives the sum.
-__device__ __forceinline__ float head_sumsq_ref(float r0, float r1, int g, int l32) {
-#pragma clang fp contract(off)
-  const int src = (g << 5) | ((l32 + 16) & 31);
-  const float rb = __shfl(r0, src);
-  const float rd = __shfl(r1, src);
-  float acc = fmaf(r0, r0, 0.0f);
-  acc = fmaf(rb, rb, acc);
-  acc = fmaf(r1, r1, acc);
-  acc = fmaf(rd, rd, acc);
-  return __shfl(reduce_add16(acc), g << 5);
-}
-
-// QKV epilogue of one wave: its 64 columns are one head of q, k or v
-// (colw = first column, a multiple of 64); lane l32 holds dims l32 and
-// 32 + l32 of rows 8*(r/4) + 4*g + r%4 of each 32-row block.  q and k get
-// RoPE (the partner of dim 2i / 2i+1 is the neighbouring lane) then
-// y * 8 / max(||y||, 1e-12) * gamma with ||y||^2 in the reference's order;
-// q is stored [B, H, L, 64], k and v key-contiguous [B, H, 64, Lpad] (four
-// consecutive tokens per 128-bit store when L % 4 == 0).  Same arithmetic as
-// qkv_postprocess.hip, so GEMM + this epilogue equals GEMM + postprocess
-// bit for bit.
-template <class C>
-__device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, floatx16 (&acc)[C::kMB][C::kNB],
-                                             int row_base, int colw, int g, int l32) {
-  static_assert(C::kTN == 64 && C::kNB == 2, "the QKV epilogue needs one head per wave");
-  if (colw >= a.n_count) return;
-  const QkvArgs& e = a.e;
-  const int width = e.H * 64;
-  const int sec = colw / width;  // 0 q, 1 k, 2 v
-  const int h = (colw - sec * width) >> 6;
-  const bool odd = (l32 & 1) != 0;
-  float g0 = 1.0f, g1 = 1.0f;
-  if (sec < 2) {
-    const float* gp = (sec == 0 ? e.qg : e.kg) + h * 64;
-    g0 = gp[l32];
-    g1 = gp[32 + l32];
-  }
-#pragma unroll
-  for (int mb = 0; mb < C::kMB; ++mb) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row0 = row_base + mb * 32 + 8 * j + 4 * g;
-      floatx4 y0, y1;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        float v0 = acc[mb][0][4 * j + t];
-        float v1 = acc[mb][1][4 * j + t];
-        if (sec < 2) {  // uniform over the wave
-          const int row = row0 + t;
-          const bool valid = row < a.M;  // uniform over the half-wave
-          const int tok = a.row0 + row;  // token index b * L + l
-          const int b = valid ? tok / e.L : 0;
-          const int l = valid ? tok - b * e.L : 0;
-          const float* fr =
-              e.freqs + (((int64_t)(e.fb == 1 ? 0 : b) * e.L + l) * e.H + h) * 64;
-          const float f0 = valid ? fr[l32] : 0.0f;
-          const float f1 = valid ? fr[32 + l32] : 0.0f;
-          const float p0 = __shfl_xor(v0, 1), p1 = __shfl_xor(v1, 1);
-          const float fp0 = __shfl_xor(f0, 1), fp1 = __shfl_xor(f1, 1);
-          const float r0 = odd ? fmaf(p0, f0, v0 * fp0) : fmaf(v0, f0, -(p0 * fp0));
-          const float r1 = odd ? fmaf(p1, f1, v1 * fp1) : fmaf(v1, f1, -(p1 * fp1));
-          const float ss = head_sumsq_ref(r0, r1, g, l32);
-          const float fac = 8.0f / fmaxf(sqrtf(ss), 1.0e-12f);
-          v0 = (r0 * fac) * g0;
-          v1 = (r1 * fac) * g1;
-        }
-        y0[t] = v0;
-        y1[t] = v1;
-      }
-      if (sec == 0) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int row = row0 + t;
-          if (row >= a.M) continue;
-          const int tok = a.row0 + row;
-          const int b = tok / e.L, l = tok - b * e.L;
-          float* dst = e.q + (((int64_t)b * e.H + h) * e.L + l) * 64;
-          dst[l32] = y0[t];
-          dst[32 + l32] = y1[t];
-        }
-      } else {
-        float* base = sec == 1 ? e.pk : e.pv;
-        const int64_t dim_stride = (int64_t)32 * e.Lpad;
-        if (((e.L | a.row0) & 3) == 0) {  // the four rows are four tokens of one sequence
-          if (row0 < a.M) {
-            const int tok = a.row0 + row0;
-            const int b = tok / e.L, l = tok - b * e.L;
-            const int64_t off = (((int64_t)b * e.H + h) * 64 + l32) * e.Lpad + l;
-            *reinterpret_cast<floatx4*>(base + off) = y0;
-            *reinterpret_cast<floatx4*>(base + off + dim_stride) = y1;
-          }
-        } else {
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int row = row0 + t;
-            if (row >= a.M) continue;
-            const int tok = a.row0 + row;
-            const int b = tok / e.L, l = tok - b * e.L;
-            const int64_t off = (((int64_t)b * e.H + h) * 64 + l32) * e.Lpad + l;
-            base[off] = y0[t];
-            base[off + dim_stride] = y1[t];
-          }
-        }
-      }
-    }
-  }
-}
 
 // kVec: x rows 16-byte aligned with K % 4 == 0, and N, n_start, n_count even
 // (so a column pair is loaded with one 32-bit / 16-bit access).
@@ -350,32 +206,7 @@ void nf24_gemm_kernel(GemmArgs a) {
     qkv_epilogue<C>(a, acc, m0 + wm * C::kTM, c0 + wn * C::kTN, g, l32);
     return;
   }
-#pragma unroll
-  for (int mb = 0; mb < C::kMB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < C::kNB; ++nb) {
-      const int col = c0 + wn * C::kTN + nb * 32 + l32;
-      if (col >= a.n_count) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * C::kTM + mb * 32 + 8 * (r / 4) + 4 * g + (r % 4);
-        if (row >= a.M) continue;
-        float* dst = a.out + (int64_t)row * a.stride_out + col;
-        const float v = acc[mb][nb][r];
-        if constexpr (kEpi == kEpilogueGelu) {
-          *dst = gelu_tanh_ref(v);
-        } else if constexpr (kEpi == kEpilogueGated) {
-          // h = acc * gate, x = x + h: two roundings, as the reference's
-          // native_block_elementwise_avx512.c:24-35
-          const float* gate = a.gate + (int64_t)((a.row0 + row) / a.rows_per_batch) * a.gate_stride;
-          *dst = gated_residual_ref(*dst, v, gate[a.n_start + col]);
-        } else if constexpr (kEpi == kEpilogueAdd) {
-          *dst = *dst + v;
-        } else {
-          *dst = v;
-        }
-      }
-    }
+  store_result<C::kMB, C::kNB, kEpi>(a, acc, m0 + wm * C::kTM, c0 + wn * C::kTN, g, l32);
 }
 
 template <class C, int kEpi = kEpiStore>
@@ -495,6 +326,9 @@ int tail_rows(int M) {
 }  // namespace
 
 int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
+  if (p.precision != kPrecisionFp32 && p.M > 32)
+    return launch_gemm_bf16(p, kEpiStore, QkvArgs{},
+                            GemmEpilogueParams{kEpilogueStore, nullptr, 0, 1}, 0, stream);
   // Few rows: the weight stream is the cost; the MFMA skinny tile only wins
   // for 9..32 rows over a short K (measured at K = 256).
   if (p.M <= 32) {
@@ -515,6 +349,7 @@ namespace {
 template <int kEpi>
 int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_t stream,
                     const QkvArgs& q = QkvArgs{}, int row0 = 0) {
+  if (p.precision != kPrecisionFp32 && p.M > 32) return launch_gemm_bf16(p, kEpi, q, e, row0, stream);
   if (const int rem = tail_rows(p.M)) {
     const int st = launch_epi_kind<kEpi>(rows_slice(p, 0, p.M - rem), e, stream, q, row0);
     return st != kOk ? st

@@ -1,0 +1,330 @@
+// NF24 packed-weight GEMM on the bf16 matrix cores: the opt-in precision
+// modes kPrecisionBf16 and kPrecisionBf16x3 of tsplat_launch.h.
+//
+// Same operation as nf24_gemm.hip -- out = bias + X * decode(W), each weight
+// decoded as the reference does (scripts/gemm_nf24_i16_avx512.c:26-33:
+// fp32((int32)q01 * 256 + q2) * scale[n]) in registers, no weight copy in
+// HBM -- but the products run on v_mfma_f32_32x32x16_bf16 with fp32
+// accumulation:
+//   kPrecisionBf16:   bf16(x) * bf16(w)
+//   kPrecisionBf16x3: xh*wh + xh*wl + xl*wh with xh = bf16(x), xl = bf16(x - xh)
+//                     and likewise wh, wl
+// where bf16() rounds the fp32 value to nearest even (v_cvt_pk_bf16_f32,
+// the rounding torch's float32 -> bfloat16 conversion uses).  x - xh is
+// exact in fp32, so xh + xl holds 16 significant bits of x; the dropped
+// xl*wl term and the rounding of xl leave a product error near 2^-16
+// relative, against 2^-8 for bf16 alone.  Products of two bf16 values are
+// exact in fp32, so the only other difference from a float64 sum of the same
+// terms is the fp32 accumulation order.
+//
+// Tiling: BM x BN workgroup tile, WM x WN waves, a wave owns MB x NB blocks
+// of 32x32 (the accumulator layout of the fp32 kernel, so the epilogues of
+// nf24_gemm_common.h serve both).  K advances 32 per step, two MFMA k-slices
+// of 16.  x (converted on the way in) and the decoded W are staged in LDS as
+// bf16, k-contiguous: a row of the tile is 64 bytes, four 16-byte chunks of
+// 8 k; chunk c of row r sits at position c ^ (((r >> 1) ^ (r >> 3)) & 3),
+// which spreads the 128-bit fragment reads of 8 (or 16) consecutive rows
+// over distinct banks.  Lane l of an MFMA reads row l%32, chunk 2s + l/32
+// of slice s, the same k assignment for A and B.  LDS is double-buffered
+// with one barrier per step; the next step's codes and x are fetched into
+// registers while the current step's MFMAs run.
+
+#include "nf24_gemm_common.h"
+
+namespace tsplat {
+namespace nf24 {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+template <int BM_, int BN_, int WM_, int WN_>
+struct Bf16Cfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int BK = 32;
+  static constexpr int kThreads = WM * WN * 64;
+  static constexpr int kTM = BM / WM, kTN = BN / WN;
+  static constexpr int kMB = kTM / 32, kNB = kTN / 32;
+  // x: float4 units (row, 4 k); W: units of 4 columns x 4 k.
+  static constexpr int kXIter = BM * BK / 4 / kThreads;
+  static constexpr int kWIter = (BN / 4) * (BK / 4) / kThreads;
+  static_assert(kXIter * kThreads == BM * BK / 4, "x units must fill the workgroup");
+  static_assert(kWIter * kThreads == (BN / 4) * (BK / 4), "W units must fill the workgroup");
+  static_assert(kTM % 32 == 0 && kTN % 32 == 0, "wave tile must be 32-aligned");
+};
+
+using Bf16Large = Bf16Cfg<256, 256, 2, 4>;  // 8 waves, 128 x 64 per wave
+using Bf16Small = Bf16Cfg<128, 128, 2, 2>;  // 4 waves, 64 x 64 per wave
+
+// bf16 element offset of (row r, chunk c) in a 32-k tile row.
+__device__ __forceinline__ int chunk_offset(int r, int c) {
+  return r * 32 + ((c ^ (((r >> 1) ^ (r >> 3)) & 3)) << 3);
+}
+
+__device__ __forceinline__ bf16x8 lds_frag(const __bf16* base, int r, int c) {
+  return *reinterpret_cast<const bf16x8*>(base + chunk_offset(r, c));
+}
+
+// hi = bf16(v); lo = bf16(v - hi) (only with three terms).
+template <int kTerms>
+__device__ __forceinline__ void split4(const floatx4& v, bf16x4& hi, bf16x4& lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    hi[e] = (__bf16)v[e];
+    if constexpr (kTerms == 3) lo[e] = (__bf16)(v[e] - (float)hi[e]);
+  }
+}
+
+__device__ __forceinline__ floatx16 mfma_bf16(const bf16x8& a, const bf16x8& b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// kVec: x rows 16-byte aligned with K % 4 == 0; N, n_start, n_count
+// multiples of 4 with code01 8-byte and q2 4-byte aligned (four columns of
+// one k row per 64-bit / 32-bit load).
+template <class C, int kTerms, bool kVec, int kEpi>
+__global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a) {
+  constexpr int kPlanes = kTerms == 3 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) __bf16 xs[2][kPlanes][C::BM * C::BK];
+  __shared__ __attribute__((aligned(16))) __bf16 ws[2][kPlanes][C::BN * C::BK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int g = lane >> 5;
+  const int l32 = lane & 31;
+
+  const int tiles_n = (a.n_count + C::BN - 1) / C::BN;
+  const int tile = xcd_tile_index(blockIdx.x, gridDim.x);
+  const int m0 = (tile / tiles_n) * C::BM;
+  const int c0 = (tile % tiles_n) * C::BN;
+
+  // W units of this thread: columns w_col .. w_col+3 of the tile, k rows
+  // w_k .. w_k+3 of each step; the columns and their scales are fixed.
+  int w_col[C::kWIter], w_k[C::kWIter];
+  float w_sc[C::kWIter][4];
+  bool w_ok[C::kWIter][4];
+#pragma unroll
+  for (int j = 0; j < C::kWIter; ++j) {
+    const int u = tid + j * C::kThreads;
+    w_col[j] = 4 * (u % (C::BN / 4));
+    w_k[j] = 4 * (u / (C::BN / 4));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int lc = c0 + w_col[j] + e;
+      w_ok[j][e] = lc < a.n_count;
+      w_sc[j][e] = w_ok[j][e] ? a.scale[a.n_start + lc] : 0.0f;
+    }
+  }
+
+  floatx4 xr[C::kXIter];
+  uint32_t cr[C::kWIter][4][2];  // k row i: int16 codes of columns 0,1 | 2,3
+  uint32_t qr[C::kWIter][4];     // k row i: int8 codes of columns 0..3
+
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < C::kXIter; ++j) {
+      const int idx = tid + j * C::kThreads;
+      const int row = idx / (C::BK / 4);
+      const int gm = m0 + row;
+      const int gk = k0 + 4 * (idx % (C::BK / 4));
+      const float* src = a.x + (int64_t)gm * a.stride_x + gk;
+      if (kVec) {
+        xr[j] = (gm < a.M && gk < a.K) ? *reinterpret_cast<const floatx4*>(src)
+                                       : floatx4{0, 0, 0, 0};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xr[j][e] = (gm < a.M && gk + e < a.K) ? src[e] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::kWIter; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int gk = k0 + w_k[j] + i;
+        const int64_t off = (int64_t)gk * a.N + a.n_start + c0 + w_col[j];
+        if (kVec) {
+          const bool ok = w_ok[j][0] && gk < a.K;
+          const uint2 c = ok ? *reinterpret_cast<const uint2*>(a.code01 + off) : uint2{0u, 0u};
+          cr[j][i][0] = c.x;
+          cr[j][i][1] = c.y;
+          qr[j][i] = ok ? *reinterpret_cast<const uint32_t*>(a.q2 + off) : 0u;
+        } else {
+          uint32_t c[4], q = 0u;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool ok = w_ok[j][e] && gk < a.K;
+            c[e] = ok ? (uint16_t)a.code01[off + e] : 0u;
+            q |= (ok ? (uint32_t)(uint8_t)a.q2[off + e] : 0u) << (8 * e);
+          }
+          cr[j][i][0] = c[0] | (c[1] << 16);
+          cr[j][i][1] = c[2] | (c[3] << 16);
+          qr[j][i] = q;
+        }
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < C::kXIter; ++j) {
+      const int idx = tid + j * C::kThreads;
+      const int row = idx / (C::BK / 4);
+      const int kc = idx % (C::BK / 4);  // 4-k unit: chunk kc/2, half kc%2
+      bf16x4 hi, lo;
+      split4<kTerms>(xr[j], hi, lo);
+      const int off = chunk_offset(row, kc >> 1) + 4 * (kc & 1);
+      *reinterpret_cast<bf16x4*>(&xs[buf][0][off]) = hi;
+      if constexpr (kTerms == 3) *reinterpret_cast<bf16x4*>(&xs[buf][kPlanes - 1][off]) = lo;
+    }
+#pragma unroll
+    for (int j = 0; j < C::kWIter; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        floatx4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int32_t code = (int32_t)(int16_t)(cr[j][i][e >> 1] >> (16 * (e & 1)));
+          const int32_t q2 = (int32_t)(int8_t)(qr[j][i] >> (8 * e));
+          w[i] = (float)(code * 256 + q2) * w_sc[j][e];
+        }
+        bf16x4 hi, lo;
+        split4<kTerms>(w, hi, lo);
+        const int col = w_col[j] + e;
+        const int off = chunk_offset(col, w_k[j] >> 3) + (w_k[j] & 7);
+        *reinterpret_cast<bf16x4*>(&ws[buf][0][off]) = hi;
+        if constexpr (kTerms == 3) *reinterpret_cast<bf16x4*>(&ws[buf][kPlanes - 1][off]) = lo;
+      }
+    }
+  };
+
+  // Accumulators start at the bias.
+  floatx16 acc[C::kMB][C::kNB];
+#pragma unroll
+  for (int nb = 0; nb < C::kNB; ++nb) {
+    const int col = c0 + wn * C::kTN + nb * 32 + l32;
+    const float bv = col < a.n_count ? a.bias[a.n_start + col] : 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < C::kMB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = bv;
+  }
+
+  const int nk = (a.K + C::BK - 1) / C::BK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  const int arow = wm * C::kTM + l32;
+  const int bcol = wn * C::kTN + l32;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) load_tile((kt + 1) * C::BK);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int ch = 2 * s + g;
+      bf16x8 ah[C::kMB], bh[C::kNB];
+#pragma unroll
+      for (int mb = 0; mb < C::kMB; ++mb) ah[mb] = lds_frag(xs[buf][0], arow + mb * 32, ch);
+#pragma unroll
+      for (int nb = 0; nb < C::kNB; ++nb) bh[nb] = lds_frag(ws[buf][0], bcol + nb * 32, ch);
+#pragma unroll
+      for (int mb = 0; mb < C::kMB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < C::kNB; ++nb) acc[mb][nb] = mfma_bf16(ah[mb], bh[nb], acc[mb][nb]);
+      if constexpr (kTerms == 3) {
+        bf16x8 al[C::kMB], bl[C::kNB];
+#pragma unroll
+        for (int nb = 0; nb < C::kNB; ++nb) bl[nb] = lds_frag(ws[buf][1], bcol + nb * 32, ch);
+#pragma unroll
+        for (int mb = 0; mb < C::kMB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < C::kNB; ++nb)
+            acc[mb][nb] = mfma_bf16(ah[mb], bl[nb], acc[mb][nb]);
+#pragma unroll
+        for (int mb = 0; mb < C::kMB; ++mb) al[mb] = lds_frag(xs[buf][1], arow + mb * 32, ch);
+#pragma unroll
+        for (int mb = 0; mb < C::kMB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < C::kNB; ++nb)
+            acc[mb][nb] = mfma_bf16(al[mb], bh[nb], acc[mb][nb]);
+      }
+    }
+    if (kt + 1 < nk) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  if constexpr (kEpi == kEpiQkv) {
+    qkv_epilogue<C>(a, acc, m0 + wm * C::kTM, c0 + wn * C::kTN, g, l32);
+  } else {
+    store_result<C::kMB, C::kNB, kEpi>(a, acc, m0 + wm * C::kTM, c0 + wn * C::kTN, g, l32);
+  }
+}
+
+template <class C, int kTerms, bool kVec>
+int launch_terms(const GemmArgs& a, int epi, hipStream_t stream) {
+  const int64_t tiles = (int64_t)((a.M + C::BM - 1) / C::BM) * ((a.n_count + C::BN - 1) / C::BN);
+  if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
+  const dim3 grid((unsigned)tiles), block(C::kThreads);
+  switch (epi) {
+    case kEpiStore:
+      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpiStore>), grid, block, 0, stream, a);
+      break;
+    case kEpiQkv:
+      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpiQkv>), grid, block, 0, stream, a);
+      break;
+    case kEpilogueGelu:
+      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpilogueGelu>), grid, block, 0, stream, a);
+      break;
+    case kEpilogueGated:
+      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpilogueGated>), grid, block, 0, stream, a);
+      break;
+    case kEpilogueAdd:
+      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpilogueAdd>), grid, block, 0, stream, a);
+      break;
+    default:
+      return kErrDims;
+  }
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+template <class C, bool kVec>
+int launch_shape(const GemmArgs& a, int terms, int epi, hipStream_t stream) {
+  return terms == 3 ? launch_terms<C, 3, kVec>(a, epi, stream) : launch_terms<C, 1, kVec>(a, epi, stream);
+}
+
+// Rows [first, first + count) of the call as their own launch.
+GemmArgs rows_of(GemmArgs a, int first, int count) {
+  a.x += (int64_t)first * a.stride_x;
+  if (a.out != nullptr) a.out += (int64_t)first * a.stride_out;
+  a.M = count;
+  a.row0 += first;
+  return a;
+}
+
+}  // namespace
+
+int launch_gemm_bf16(const GemmParams& p, int epi, const QkvArgs& e, const GemmEpilogueParams& ep,
+                     int row0, hipStream_t stream) {
+  const int terms = p.precision == kPrecisionBf16x3 ? 3 : 1;
+  const GemmArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out,
+                   p.M, p.K, p.N, p.n_start, p.n_count, p.stride_x, p.stride_out, e,
+                   ep.gate, ep.gate_stride, ep.rows_per_batch, row0};
+  const bool vec = (reinterpret_cast<uintptr_t>(p.x) % 16 == 0) && (p.stride_x % 4 == 0) &&
+                   (p.K % 4 == 0) && (p.N % 4 == 0) && (p.n_start % 4 == 0) &&
+                   (p.n_count % 4 == 0) && (reinterpret_cast<uintptr_t>(p.code01) % 8 == 0) &&
+                   (reinterpret_cast<uintptr_t>(p.q2) % 4 == 0);
+  if (!vec) return launch_shape<Bf16Small, false>(a, terms, epi, stream);
+  // 256 x 256 tiles where there are rows and columns to fill them; rows past
+  // the last multiple of 256 that number at most 32 run as 128-row tiles
+  // (both shapes sum every output in the same order).
+  if (p.M < 256 || p.n_count < 256) return launch_shape<Bf16Small, true>(a, terms, epi, stream);
+  const int rem = p.M % 256;
+  if (rem == 0 || rem > 32) return launch_shape<Bf16Large, true>(a, terms, epi, stream);
+  const int st = launch_shape<Bf16Large, true>(rows_of(a, 0, p.M - rem), terms, epi, stream);
+  return st != kOk ? st : launch_shape<Bf16Small, true>(rows_of(a, p.M - rem, rem), terms, epi, stream);
+}
+
+}  // namespace nf24
+}  // namespace tsplat

@@ -10,6 +10,17 @@ namespace tsplat {
 
 // out[m, c] = bias[n0+c] + sum_k x[m, k] * w[k, n0+c],  c in [0, n_count),
 // w[k, n] = fp32((int32)code01[k, n] * 256 + q2[k, n]) * scale[n].
+//
+// Product precision (opt-in; kPrecisionFp32 is the strict default):
+//   kPrecisionFp32:   fp32 x * fp32 w on fp32 MFMA.
+//   kPrecisionBf16:   bf16(x) * bf16(w) on bf16 MFMA, fp32 accumulation;
+//                     bf16() rounds to nearest even from the fp32 value.
+//   kPrecisionBf16x3: x = xh + xl, w = wh + wl with xh = bf16(x),
+//                     xl = bf16(x - xh) (likewise w); the product is
+//                     xh*wh + xh*wl + xl*wh on bf16 MFMA, fp32 accumulation.
+// Calls with M <= 32 are weight-stream bound and run the fp32 path in every
+// precision.
+enum GemmPrecision : int { kPrecisionFp32 = 0, kPrecisionBf16 = 1, kPrecisionBf16x3 = 2 };
 struct GemmParams {
   const float* x;
   const int16_t* code01;  // [K, N] row-major (the reference's codes0_t)
@@ -20,6 +31,7 @@ struct GemmParams {
   int M, K, N;
   int n_start, n_count;
   int stride_x, stride_out;
+  int precision = kPrecisionFp32;
 };
 int launch_nf24_gemm(const GemmParams& p, hipStream_t stream);
 // Few-row form (1 <= M <= 32), HBM-bound; same result contract.

@@ -45,9 +45,11 @@ SIGNATURES = {
     "tsplat_q_kv_selected_postprocess_async": ([_vp] * 9 + [_i] * 7 + [_vp], _i),
     "tsplat_qkv_postprocess_async": ([_vp] * 7 + [_i] * 6 + [_vp], _i),
     "tsplat_gemm_nf24_qkv_direct_async": ([_vp] * 11 + [_i] * 8 + [_vp], _i),
+    "tsplat_gemm_nf24_qkv_direct_precision_async": ([_vp] * 11 + [_i] * 9 + [_vp], _i),
     "tsplat_nf24_pack_async": ([_vp, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp], _i),
     "tsplat_nf24_decode_async": ([_vp] * 4 + [_i] * 3 + [_vp], _i),
     "tsplat_nf24_gemm_epilogue_async": ([_vp] * 6 + [_i] * 8 + [_vp, _i64, _i, _vp], _i),
+    "tsplat_nf24_gemm_precision_async": ([_vp] * 6 + [_i] * 8 + [_vp, _i64, _i, _i, _vp], _i),
     "triposplat_layernorm_f32_avx512": ([_vp] * 4 + [_i64, _i, ctypes.c_float, _i, _i], _i),
     "triposplat_multihead_rmsnorm_f32_avx512": ([_vp] * 3 + [_i64, _i, _i, ctypes.c_float, _i], _i),
     "triposplat_rope_complex_f32_avx512": ([_vp] * 3 + [_i64, _i, _i], _i),

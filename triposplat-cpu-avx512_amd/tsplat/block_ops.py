@@ -160,11 +160,16 @@ def silu(x, out=None, library=None):
 
 
 def nf24_linear_epilogue(x2, code01_t, q2_t, scale, bias, epilogue, *, out=None, gate=None,
-                         rows_per_batch=None, library=None):
+                         rows_per_batch=None, precision="fp32", library=None):
     """NF24 Linear with the next elementwise step applied before the store:
     EPILOGUE_GELU -> gelu_tanh(x @ W + b); EPILOGUE_GATED -> out += (x @ W + b) * gate[b];
-    EPILOGUE_ADD -> out += x @ W + b.  gate is [B, N] (row stride may exceed N)."""
+    EPILOGUE_ADD -> out += x @ W + b.  gate is [B, N] (row stride may exceed N).
+    precision as tsplat.nf24.nf24_linear."""
     import torch
+
+    from .nf24 import precision_id
+
+    mode = precision_id(precision)
 
     _check(torch, "x", x2)
     M, K = (int(s) for s in x2.shape)
@@ -179,8 +184,11 @@ def nf24_linear_epilogue(x2, code01_t, q2_t, scale, bias, epilogue, *, out=None,
             raise ValueError("gate must be [B, N] with unit column stride")
         gate_stride = int(gate.stride(0))
         per_batch = int(rows_per_batch) if rows_per_batch is not None else M // int(gate.shape[0])
-    _call(load_library(library), "tsplat_nf24_gemm_epilogue_async", x2.device, x2.data_ptr(),
-          code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), bias.data_ptr(), out.data_ptr(),
-          M, K, N, 0, N, int(x2.stride(0)), int(out.stride(0)), int(epilogue),
-          gate.data_ptr() if gate is not None else None, gate_stride, per_batch)
+    args = (x2.data_ptr(), code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), bias.data_ptr(),
+            out.data_ptr(), M, K, N, 0, N, int(x2.stride(0)), int(out.stride(0)), int(epilogue),
+            gate.data_ptr() if gate is not None else None, gate_stride, per_batch)
+    if mode == 0:
+        _call(load_library(library), "tsplat_nf24_gemm_epilogue_async", x2.device, *args)
+    else:
+        _call(load_library(library), "tsplat_nf24_gemm_precision_async", x2.device, *args, mode)
     return out

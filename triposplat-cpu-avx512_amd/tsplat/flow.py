@@ -44,7 +44,7 @@ from dataclasses import dataclass
 from . import block_ops as bo
 from .native_sampler_backend import NativeSamplerBackend
 from .native_sdpa_ctypes import native_sdpa_f32_ex
-from .nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
+from .nf24 import nf24_linear, precision_id, quantize_nf24_i16_per_output_channel
 from .qkv import gemm_nf24_qkv_direct
 
 
@@ -82,6 +82,7 @@ class PackedLinear:
         self.code01_t, self.q2_t, self.scale, self.bias = code01_t, q2_t, scale, bias
         self.in_features = int(code01_t.shape[0])
         self.out_features = int(code01_t.shape[1])
+        self.precision = "fp32"  # GEMM product precision (tsplat.nf24.PRECISIONS)
 
     @classmethod
     def random(cls, torch, in_f, out_f, seed, device):
@@ -91,16 +92,36 @@ class PackedLinear:
         codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
         return cls(codes[0], codes[1], scales[0], b)
 
-    def __call__(self, x2, out=None):
-        return nf24_linear(x2, self.code01_t, self.q2_t, self.scale, self.bias, out=out)
+    def __call__(self, x2, out=None, output_start=0, output_count=None):
+        return nf24_linear(x2, self.code01_t, self.q2_t, self.scale, self.bias, out=out,
+                           output_start=output_start, output_count=output_count, precision=self.precision)
 
     def epilogue(self, x2, kind, out=None, gate=None):
         """This Linear with a fused elementwise epilogue (block_ops.EPILOGUE_*)."""
         return bo.nf24_linear_epilogue(x2, self.code01_t, self.q2_t, self.scale, self.bias, kind,
-                                       out=out, gate=gate)
+                                       out=out, gate=gate, precision=self.precision)
+
+    def qkv_direct(self, x2, freqs, q_gamma, k_gamma, B, L, H):
+        """Fused QKV projection + RoPE/RMSNorm/pack (tsplat.qkv.gemm_nf24_qkv_direct)."""
+        return gemm_nf24_qkv_direct(x2, self.code01_t, self.q2_t, self.scale, self.bias, freqs,
+                                    q_gamma, k_gamma, B, L, H, precision=self.precision)
 
     def host(self):
         return {k: getattr(self, k).cpu().numpy() for k in ("code01_t", "q2_t", "scale", "bias")}
+
+
+def set_model_precision(model, precision, include=("blocks",)):
+    """GEMM product precision of a flow model's block Linears ("fp32" strict,
+    or the opt-in "bf16" / "bf16x3"); the timestep / input / output Linears
+    stay fp32 unless include also names "io"."""
+    precision_id(precision)
+    for blk in model.blocks:
+        for lin in blk.lin.values():
+            lin.precision = precision
+    for lin in (model.t_fc1, model.t_fc2, model.adaln, model.input_layer, model.out_layer):
+        lin.precision = precision if "io" in include else "fp32"
+    model.precision = precision
+    return model
 
 
 def _randn(torch, shape, seed, device, std, mean=0.0):
@@ -170,6 +191,10 @@ class FlowModel:
         self.blocks = [FlowBlock(torch, cfg, i, device, 1010 + 10 * i) for i in range(nb)]
         self._freqs = {}
         self.sampler = NativeSamplerBackend()
+        self.precision = "fp32"
+
+    def set_precision(self, precision, include=("blocks",)):
+        return set_model_precision(self, precision, include)
 
     def freqs(self, L):
         if L not in self._freqs:
@@ -201,9 +226,8 @@ class FlowModel:
         # self attention: LN + modulate, fused NF24 QKV + RoPE/RMSNorm/pack,
         # packed exact SDPA, NF24 out with the gated residual in its epilogue
         h = bo.layer_norm(x, cfg.ln_eps, scale=scale_msa, shift=shift_msa)
-        q, pk, pv = gemm_nf24_qkv_direct(h.view(B * L, C), lin["qkv"].code01_t, lin["qkv"].q2_t,
-                                         lin["qkv"].scale, lin["qkv"].bias, self.freqs(L),
-                                         blk.q_gamma, blk.k_gamma, B, L, H)
+        q, pk, pv = lin["qkv"].qkv_direct(h.view(B * L, C), self.freqs(L), blk.q_gamma, blk.k_gamma,
+                                          B, L, H)
         a = native_sdpa_f32_ex(q, pk, pv, kv_packed=True, key_count=L, out_layout="blhd")
         lin["out"].epilogue(a.view(B * L, C), bo.EPILOGUE_GATED, out=x2, gate=gate_msa)
 

@@ -31,11 +31,10 @@ from __future__ import annotations
 import math
 
 from . import block_ops as bo
-from .flow import FlowConfig, PackedLinear, _randn, timestep_embedding
+from .flow import FlowConfig, PackedLinear, _randn, set_model_precision, timestep_embedding
 from .native_sampler_backend import NativeSamplerBackend
 from .native_sdpa_ctypes import native_sdpa_f32_ex
-from .nf24 import nf24_linear
-from .qkv import gemm_nf24_qkv_direct, q_kv_selected_rope_rmsnorm_pack
+from .qkv import q_kv_selected_rope_rmsnorm_pack
 
 JOINT_LINEARS = (("qkv", 1, 3), ("out", 1, 1), ("fc1", 1, 4), ("fc2", 4, 1))
 
@@ -86,6 +85,10 @@ class JointFlowModel:
         self.blocks = [JointBlock(torch, cfg, i, device) for i in range(nb)]
         self.sampler = NativeSamplerBackend()
         self._freqs, self._sel, self._bias = {}, {}, {}
+        self.precision = "fp32"
+
+    def set_precision(self, precision, include=("blocks",)):
+        return set_model_precision(self, precision, include)
 
     def freqs(self, L, Lc):
         if (L, Lc) not in self._freqs:
@@ -127,9 +130,8 @@ class JointFlowModel:
         sm, cm, gm, s2, c2, g2 = self._mod(blk, t_mod)
         lin = blk.lin
         h = bo.layer_norm(x, cfg.ln_eps, scale=cm, shift=sm)
-        q, pk, pv = gemm_nf24_qkv_direct(h.view(Ltot, C), lin["qkv"].code01_t, lin["qkv"].q2_t,
-                                         lin["qkv"].scale, lin["qkv"].bias, self.freqs(L, Ltot - L),
-                                         blk.q_gamma, blk.k_gamma, 1, Ltot, H)
+        q, pk, pv = lin["qkv"].qkv_direct(h.view(Ltot, C), self.freqs(L, Ltot - L), blk.q_gamma,
+                                          blk.k_gamma, 1, Ltot, H)
         a = native_sdpa_f32_ex(q, pk, pv, kv_packed=True, key_count=Ltot, key_bias=key_bias,
                                out_layout="blhd")
         x2 = x.view(Ltot, C)
@@ -148,8 +150,8 @@ class JointFlowModel:
         sm, cm, gm, s2, c2, g2 = self._mod(blk, t_mod)
         lin = blk.lin["qkv"]
         h = bo.layer_norm(x, cfg.ln_eps, scale=cm, shift=sm).view(Ltot, C)
-        q = nf24_linear(h[:L], lin.code01_t, lin.q2_t, lin.scale, lin.bias, output_start=0, output_count=C)
-        kv = nf24_linear(h, lin.code01_t, lin.q2_t, lin.scale, lin.bias, output_start=C, output_count=2 * C)
+        q = lin(h[:L], output_start=0, output_count=C)
+        kv = lin(h, output_start=C, output_count=2 * C)
         qo, pk, pv = q_kv_selected_rope_rmsnorm_pack(q, kv, self.freqs(L, Ltot - L), self.selected(L),
                                                      blk.q_gamma, blk.k_gamma, 1, L, Ltot, H)
         a = native_sdpa_f32_ex(qo, pk, pv, kv_packed=True, key_count=Ltot, key_bias=key_bias,

@@ -27,7 +27,8 @@ from typing import Any
 
 from ._lib import library_path as _default_library_path
 from ._lib import load_library
-from .nf24 import RESIDUAL_MODE_ID, make_nf8_codebook, nf24_linear, quantize_nf24_i16_per_output_channel
+from .nf24 import (RESIDUAL_MODE_ID, make_nf8_codebook, nf24_linear, precision_id,
+                   quantize_nf24_i16_per_output_channel)
 
 _MODE_NAMES = {0: "nf8", 1: "symmetric_int8", 4: "nf24_i16"}
 
@@ -45,9 +46,14 @@ def apply_triposplat_native_rnf8_avx512_patch(
     strict: bool = True,
     stages: int = 2,
     residual_mode: str = "nf8",
+    precision: str = "fp32",
 ) -> dict[str, Any]:
+    """``precision`` (no counterpart in the reference): "fp32" (strict, the
+    default) or the opt-in bf16-MFMA products "bf16" / "bf16x3" of
+    tsplat.nf24.nf24_linear; it is recorded in the returned metadata."""
     if not enabled:
         return {"enabled": False}
+    precision_id(precision)
     if not strict:
         raise ValueError("residual NF8 releases float32 weights and requires strict=True")
     if stages not in (2, 3):
@@ -145,7 +151,8 @@ def apply_triposplat_native_rnf8_avx512_patch(
         try:
             out = nf24_linear(x2, module._native_rnf8_codes0_t, module._native_rnf8_codes1_t,
                               module._native_rnf8_scales0, module._native_rnf8_bias,
-                              output_start=start, output_count=count, library=lib_path)
+                              output_start=start, output_count=count, precision=precision,
+                              library=lib_path)
         except RuntimeError as exc:
             runtime["fallbacks"] += 1
             kind = "range kernel" if is_range else "kernel"
@@ -236,6 +243,7 @@ def apply_triposplat_native_rnf8_avx512_patch(
         "residual_quantizer": residual_mode,
         "bits_per_weight": 24,
         "activation_dtype": "float32",
+        "gemm_precision": precision,
         "float32_weight_retained": False,
         "library_path": lib_path.as_posix(),
         "optimized_library_path": None if optimized_library_path is None else lib_path.as_posix(),
@@ -259,7 +267,10 @@ def apply_triposplat_native_rnf8_avx512_patch(
         "aggregate_weight_max_abs": max_abs_error,
         "packing": packing,
         "runtime": runtime,
-        "semantics": "All selected Linear weights are decoded in registers inside the gfx950 NF24 GEMM (fp32 MFMA accumulate); no fp32 weight copy is kept.",
+        "semantics": "All selected Linear weights are decoded in registers inside the gfx950 NF24 GEMM "
+                     + ("(fp32 MFMA accumulate)" if precision == "fp32" else
+                        f"({precision} products on bf16 MFMA, fp32 accumulate; opt-in)")
+                     + "; no fp32 weight copy is kept.",
     }
 
 

@@ -128,12 +128,26 @@ def decode_nf24_i16_weight(code01_t, q2_t, scale):
     return _decode(code01_t, q2_t, scale, True)
 
 
+# Product precision of the GEMM (tsplat_nf24_gemm_precision_async): "fp32" is
+# the strict default; "bf16" and "bf16x3" are the opt-in bf16-MFMA modes.
+PRECISIONS = {"fp32": 0, "bf16": 1, "bf16x3": 2}
+
+
+def precision_id(precision) -> int:
+    if precision not in PRECISIONS:
+        raise ValueError(f"unknown GEMM precision {precision!r}; expected one of {sorted(PRECISIONS)}")
+    return PRECISIONS[precision]
+
+
 def nf24_linear(x2, code01_t, q2_t, scale, bias, *, output_start=0, output_count=None, out=None,
-                library=None):
+                precision="fp32", library=None):
     """out[M, count] = bias[start:start+count] + x2[M, K] @ W[:, start:start+count]
-    on torch's current stream.  x2 must be a contiguous fp32 GPU matrix."""
+    on torch's current stream.  x2 must be a contiguous fp32 GPU matrix.
+    precision "bf16" / "bf16x3" selects the opt-in bf16-MFMA products
+    (include/tsplat_hip.h); M <= 32 always runs the strict kernels."""
     import torch
 
+    mode = precision_id(precision)
     M, K = (int(s) for s in x2.shape)
     N = int(code01_t.shape[1])
     count = N - int(output_start) if output_count is None else int(output_count)
@@ -141,12 +155,15 @@ def nf24_linear(x2, code01_t, q2_t, scale, bias, *, output_start=0, output_count
         out = torch.empty((M, count), dtype=torch.float32, device=x2.device)
     lib = load_library(library)
     with torch.cuda.device(x2.device):
-        status = lib.tsplat_nf24_gemm_async(
-            x2.data_ptr(), code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), bias.data_ptr(),
-            out.data_ptr(), M, K, N, int(output_start), count, int(x2.stride(0)), int(out.stride(0)),
-            current_stream_handle(x2.device),
-        )
-    check_status(status, "tsplat_nf24_gemm_async")
+        stream = current_stream_handle(x2.device)
+        args = (x2.data_ptr(), code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), bias.data_ptr(),
+                out.data_ptr(), M, K, N, int(output_start), count, int(x2.stride(0)), int(out.stride(0)))
+        if mode == 0:
+            name, status = "tsplat_nf24_gemm_async", lib.tsplat_nf24_gemm_async(*args, stream)
+        else:
+            name = "tsplat_nf24_gemm_precision_async"
+            status = lib.tsplat_nf24_gemm_precision_async(*args, 0, None, 0, 1, mode, stream)
+    check_status(status, name)
     return out
 
 

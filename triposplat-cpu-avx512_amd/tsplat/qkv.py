@@ -50,9 +50,14 @@ def qkv_rope_rmsnorm_pack(qkv, frequencies, q_gamma, k_gamma, B, L, H, *, L_padd
 
 
 def gemm_nf24_qkv_direct(x2, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, B, L, H, *,
-                         L_padded=None, library=None):
-    """NF24 QKV projection of x2 [B*L, K] (N = 3*H*64) then the postprocess."""
+                         L_padded=None, precision="fp32", library=None):
+    """NF24 QKV projection of x2 [B*L, K] (N = 3*H*64) then the postprocess;
+    precision of the projection as tsplat.nf24.nf24_linear."""
     import torch
+
+    from .nf24 import precision_id
+
+    mode = precision_id(precision)
 
     for name, t in (("x", x2), ("frequencies", frequencies), ("q_gamma", q_gamma), ("k_gamma", k_gamma)):
         _check(torch, name, t)
@@ -60,13 +65,17 @@ def gemm_nf24_qkv_direct(x2, code01_t, q2_t, scale, bias, frequencies, q_gamma, 
     q, pk, pv = _outputs(torch, B, L, H, Lp, x2.device)
     lib = load_library(library)
     with torch.cuda.device(x2.device):
-        status = lib.tsplat_gemm_nf24_qkv_direct_async(
-            x2.data_ptr(), code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), bias.data_ptr(),
-            frequencies.data_ptr(), q_gamma.data_ptr(), k_gamma.data_ptr(), q.data_ptr(), pk.data_ptr(),
-            pv.data_ptr(), int(B), int(L), int(x2.shape[1]), int(code01_t.shape[1]), int(H), 64, Lp,
-            int(frequencies.shape[0]), current_stream_handle(x2.device),
-        )
-    check_status(status, "tsplat_gemm_nf24_qkv_direct_async")
+        args = (x2.data_ptr(), code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), bias.data_ptr(),
+                frequencies.data_ptr(), q_gamma.data_ptr(), k_gamma.data_ptr(), q.data_ptr(), pk.data_ptr(),
+                pv.data_ptr(), int(B), int(L), int(x2.shape[1]), int(code01_t.shape[1]), int(H), 64, Lp,
+                int(frequencies.shape[0]))
+        stream = current_stream_handle(x2.device)
+        if mode == 0:
+            name, status = "tsplat_gemm_nf24_qkv_direct_async", lib.tsplat_gemm_nf24_qkv_direct_async(*args, stream)
+        else:
+            name = "tsplat_gemm_nf24_qkv_direct_precision_async"
+            status = lib.tsplat_gemm_nf24_qkv_direct_precision_async(*args, mode, stream)
+    check_status(status, name)
     return q, pk, pv
 
 
