@@ -19,10 +19,12 @@
 // d = 8*hh + 4*(lane/32) + t) identically for Q and K, so K fragments load
 // as ds_read_b128.
 //
-// Scores are kept in log2 units: x = (q.k) * (0.125 * log2 e) + bias * log2 e,
-// p = exp2(x - m) with v_exp_f32.  This is the reference's exp(s - m) up to
-// fp32 rounding of the argument; the merge is the usual rescale by
-// exp2(m_old - m_new).
+// Scores are kept in log2 units: x = (q * 0.125 * log2 e) . k + bias * log2 e
+// (Q is scaled once, in registers), p = exp2(x - m) with v_exp_f32.  This is
+// the reference's exp(s - m) up to fp32 rounding of the scaled operands and
+// of the argument; the maximal key still gets p = 1 exactly.  The merge is
+// the usual rescale by exp2(m_old - m_new), skipped when no lane's maximum
+// moved (alpha = 1 exactly).
 
 #include "tsplat_common.h"
 #include "tsplat_launch.h"
@@ -108,13 +110,19 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
   const int qrow = qb * kBQ + wave * 32 + l32;
   const bool q_ok = qrow < a.Lq;
 
-  // Q fragment for this lane's query: qf[hh][t] = q[8*hh + 4*g + t].
+  // Q fragment for this lane's query, pre-scaled into log2 units:
+  // qf[hh][t] = q[8*hh + 4*g + t] * 0.125 * log2(e), so the MFMA yields the
+  // scores x = (q . k) / 8 * log2(e) directly.
+  const float c1 = 0.125f * kLog2e;
   floatx4 qf[8];
   {
     const float* qp = a.q + ((int64_t)bh * a.Lq + (q_ok ? qrow : 0)) * kD + 4 * g;
 #pragma unroll
-    for (int hh = 0; hh < 8; ++hh)
+    for (int hh = 0; hh < 8; ++hh) {
       qf[hh] = q_ok ? *reinterpret_cast<const floatx4*>(qp + 8 * hh) : floatx4{0, 0, 0, 0};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) qf[hh][t] *= c1;
+    }
   }
 
   const float* kbase = a.k + (int64_t)bh * (kPacked ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
@@ -172,7 +180,6 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
     for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
   float m_run = -INFINITY;
   float l_run = 0.0f;
-  const float c1 = 0.125f * kLog2e;
 
   const int ntiles = (k_end - k_begin + kBKV - 1) / kBKV;
   load(k_begin);
@@ -216,8 +223,9 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
           for (int i = 0; i < kGB; ++i) s[i] = mfma32x32x2(kf[i][e], qf[hh][e], s[i]);
       }
 
-      // Scale (+ bias) in log2 units, mask keys past Lk, running max.
-      float mx = -INFINITY;
+      // Scores in log2 units (+ bias * log2 e).  Keys past Lk are masked only
+      // in a tile that reaches past Lk (a wave-uniform branch around the
+      // index compares).
 #pragma unroll
       for (int i = 0; i < kGB; ++i)
 #pragma unroll
@@ -228,12 +236,22 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * r4 + e;
-            float x = kBias ? fmaf(s[i][r], c1, bb[e]) : s[i][r] * c1;
-            if (tail && key0 + kb * 32 + 8 * r4 + 4 * g + e >= a.Lk) x = -INFINITY;
-            s[i][r] = x;
-            mx = fmaxf(mx, x);
+            if (kBias) s[i][r] += bb[e];
           }
         }
+      if (tail) {
+        const int valid = a.Lk - key0 - 4 * g;  // key index within the tile, minus 4*g
+#pragma unroll
+        for (int i = 0; i < kGB; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if ((kb0 + i) * 32 + 8 * (r / 4) + (r % 4) >= valid) s[i][r] = -INFINITY;
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < kGB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[i][r]);
       mx = pair_max(mx);
       const float m_new = fmaxf(m_run, mx);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -247,11 +265,15 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
           ls += pr;
         }
       l_run = fmaf(l_run, alpha, ls);
+      // alpha is exactly 1 where the max did not move; the rescale is skipped
+      // when that holds for every lane of the wave.
+      if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      }
       m_run = m_new;
-#pragma unroll
-      for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
 
       // O^T[d][query] += V^T P^T over these keys.
 #pragma unroll
