@@ -219,7 +219,9 @@ def run_gemm(torch, dev, iters):
     def step():
         nf24_linear(x, codes[0], codes[1], scales[0], bias, out=gout)
 
-    for _ in range(3):
+    # ~10 ms of warm-up calls: after a short warm-up the first timed batches
+    # still run while the GPU clock ramps (up to 15 % slower)
+    for _ in range(40):
         step()
     torch.cuda.synchronize()
     # median of 5 batches: clocks on these boxes vary by ~10 % between batches
@@ -233,7 +235,7 @@ def run_gemm(torch, dev, iters):
         def step_p(p=precision):
             nf24_linear(x, codes[0], codes[1], scales[0], bias, out=gout, precision=p)
 
-        for _ in range(3):
+        for _ in range(40):
             step_p()
         torch.cuda.synchronize()
         p_ms = sorted(time_events(torch, step_p, iters) for _ in range(5))[2]

@@ -26,10 +26,13 @@
 // which spreads the 128-bit fragment reads of 8 (or 16) consecutive rows
 // over distinct banks.  Lane l of an MFMA reads row l%32, chunk 2s + l/32
 // of slice s, the same k assignment for A and B.  LDS is double-buffered
-// with one barrier per step; the next step's codes and x are fetched into
-// registers while the current step's MFMAs run.
+// with one barrier per step; codes and x are fetched into registers two
+// steps ahead (bf16) or one step ahead (bf16x3, whose extra fragments leave
+// no registers for a second set).
 
 #include "nf24_gemm_common.h"
+
+#include <type_traits>
 
 namespace tsplat {
 namespace nf24 {
@@ -118,11 +121,16 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
     }
   }
 
-  floatx4 xr[C::kXIter];
-  uint32_t cr[C::kWIter][4][2];  // k row i: int16 codes of columns 0,1 | 2,3
-  uint32_t qr[C::kWIter][4];     // k row i: int8 codes of columns 0..3
+  // kStages register sets: the codes and x of step k arrive in set
+  // k % kStages while the kStages steps before it run.  Two stages for one
+  // term; three terms have no registers for a second set.
+  constexpr int kStages = kTerms == 3 ? 1 : 2;
+  floatx4 xr[kStages][C::kXIter];
+  uint32_t cr[kStages][C::kWIter][4][2];  // k row i: int16 codes of columns 0,1 | 2,3
+  uint32_t qr[kStages][C::kWIter][4];     // k row i: int8 codes of columns 0..3
 
-  auto load_tile = [&](int k0) {
+  auto load_tile = [&](auto set_c, int k0) {
+    constexpr int S = decltype(set_c)::value;
 #pragma unroll
     for (int j = 0; j < C::kXIter; ++j) {
       const int idx = tid + j * C::kThreads;
@@ -131,11 +139,11 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
       const int gk = k0 + 4 * (idx % (C::BK / 4));
       const float* src = a.x + (int64_t)gm * a.stride_x + gk;
       if (kVec) {
-        xr[j] = (gm < a.M && gk < a.K) ? *reinterpret_cast<const floatx4*>(src)
-                                       : floatx4{0, 0, 0, 0};
+        xr[S][j] = (gm < a.M && gk < a.K) ? *reinterpret_cast<const floatx4*>(src)
+                                          : floatx4{0, 0, 0, 0};
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xr[j][e] = (gm < a.M && gk + e < a.K) ? src[e] : 0.0f;
+        for (int e = 0; e < 4; ++e) xr[S][j][e] = (gm < a.M && gk + e < a.K) ? src[e] : 0.0f;
       }
     }
 #pragma unroll
@@ -147,9 +155,9 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
         if (kVec) {
           const bool ok = w_ok[j][0] && gk < a.K;
           const uint2 c = ok ? *reinterpret_cast<const uint2*>(a.code01 + off) : uint2{0u, 0u};
-          cr[j][i][0] = c.x;
-          cr[j][i][1] = c.y;
-          qr[j][i] = ok ? *reinterpret_cast<const uint32_t*>(a.q2 + off) : 0u;
+          cr[S][j][i][0] = c.x;
+          cr[S][j][i][1] = c.y;
+          qr[S][j][i] = ok ? *reinterpret_cast<const uint32_t*>(a.q2 + off) : 0u;
         } else {
           uint32_t c[4], q = 0u;
 #pragma unroll
@@ -158,22 +166,24 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
             c[e] = ok ? (uint16_t)a.code01[off + e] : 0u;
             q |= (ok ? (uint32_t)(uint8_t)a.q2[off + e] : 0u) << (8 * e);
           }
-          cr[j][i][0] = c[0] | (c[1] << 16);
-          cr[j][i][1] = c[2] | (c[3] << 16);
-          qr[j][i] = q;
+          cr[S][j][i][0] = c[0] | (c[1] << 16);
+          cr[S][j][i][1] = c[2] | (c[3] << 16);
+          qr[S][j][i] = q;
         }
       }
     }
   };
 
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](auto set_c, auto buf_c) {
+    constexpr int S = decltype(set_c)::value;
+    constexpr int buf = decltype(buf_c)::value;
 #pragma unroll
     for (int j = 0; j < C::kXIter; ++j) {
       const int idx = tid + j * C::kThreads;
       const int row = idx / (C::BK / 4);
       const int kc = idx % (C::BK / 4);  // 4-k unit: chunk kc/2, half kc%2
       bf16x4 hi, lo;
-      split4<kTerms>(xr[j], hi, lo);
+      split4<kTerms>(xr[S][j], hi, lo);
       const int off = chunk_offset(row, kc >> 1) + 4 * (kc & 1);
       *reinterpret_cast<bf16x4*>(&xs[buf][0][off]) = hi;
       if constexpr (kTerms == 3) *reinterpret_cast<bf16x4*>(&xs[buf][kPlanes - 1][off]) = lo;
@@ -185,8 +195,8 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
         floatx4 w;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int32_t code = (int32_t)(int16_t)(cr[j][i][e >> 1] >> (16 * (e & 1)));
-          const int32_t q2 = (int32_t)(int8_t)(qr[j][i] >> (8 * e));
+          const int32_t code = (int32_t)(int16_t)(cr[S][j][i][e >> 1] >> (16 * (e & 1)));
+          const int32_t q2 = (int32_t)(int8_t)(qr[S][j][i] >> (8 * e));
           w[i] = (float)(code * 256 + q2) * w_sc[j][e];
         }
         bf16x4 hi, lo;
@@ -212,23 +222,30 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
   }
 
   const int nk = (a.K + C::BK - 1) / C::BK;
-  load_tile(0);
-  store_tile(0);
+  using Set0 = std::integral_constant<int, 0>;
+  using Set1 = std::integral_constant<int, 1>;
+  load_tile(Set0{}, 0);
+  store_tile(Set0{}, Set0{});
+  if (kStages == 2 && nk > 1) load_tile(std::integral_constant<int, kStages - 1>{}, C::BK);
   __syncthreads();
 
   const int arow = wm * C::kTM + l32;
   const int bcol = wn * C::kTN + l32;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load_tile((kt + 1) * C::BK);
+  // Step kt reads LDS buffer P = kt % 2, fetches step kt + kStages into
+  // register set kt % kStages (free: its previous step was stored into LDS
+  // one step earlier) and stores step kt + 1 from set (kt + 1) % kStages into
+  // buffer 1 - P (read in step kt - 1, done before the last barrier).
+  auto step = [&](auto p_c, int kt) {
+    constexpr int P = decltype(p_c)::value;
+    if (kt + kStages < nk) load_tile(std::integral_constant<int, P % kStages>{}, (kt + kStages) * C::BK);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int ch = 2 * s + g;
       bf16x8 ah[C::kMB], bh[C::kNB];
 #pragma unroll
-      for (int mb = 0; mb < C::kMB; ++mb) ah[mb] = lds_frag(xs[buf][0], arow + mb * 32, ch);
+      for (int mb = 0; mb < C::kMB; ++mb) ah[mb] = lds_frag(xs[P][0], arow + mb * 32, ch);
 #pragma unroll
-      for (int nb = 0; nb < C::kNB; ++nb) bh[nb] = lds_frag(ws[buf][0], bcol + nb * 32, ch);
+      for (int nb = 0; nb < C::kNB; ++nb) bh[nb] = lds_frag(ws[P][0], bcol + nb * 32, ch);
 #pragma unroll
       for (int mb = 0; mb < C::kMB; ++mb)
 #pragma unroll
@@ -236,14 +253,14 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
       if constexpr (kTerms == 3) {
         bf16x8 al[C::kMB], bl[C::kNB];
 #pragma unroll
-        for (int nb = 0; nb < C::kNB; ++nb) bl[nb] = lds_frag(ws[buf][1], bcol + nb * 32, ch);
+        for (int nb = 0; nb < C::kNB; ++nb) bl[nb] = lds_frag(ws[P][1], bcol + nb * 32, ch);
 #pragma unroll
         for (int mb = 0; mb < C::kMB; ++mb)
 #pragma unroll
           for (int nb = 0; nb < C::kNB; ++nb)
             acc[mb][nb] = mfma_bf16(ah[mb], bl[nb], acc[mb][nb]);
 #pragma unroll
-        for (int mb = 0; mb < C::kMB; ++mb) al[mb] = lds_frag(xs[buf][1], arow + mb * 32, ch);
+        for (int mb = 0; mb < C::kMB; ++mb) al[mb] = lds_frag(xs[P][1], arow + mb * 32, ch);
 #pragma unroll
         for (int mb = 0; mb < C::kMB; ++mb)
 #pragma unroll
@@ -251,8 +268,13 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
             acc[mb][nb] = mfma_bf16(al[mb], bh[nb], acc[mb][nb]);
       }
     }
-    if (kt + 1 < nk) store_tile(buf ^ 1);
+    if (kt + 1 < nk)
+      store_tile(std::integral_constant<int, (P + 1) % kStages>{}, std::integral_constant<int, 1 - P>{});
     __syncthreads();
+  };
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(Set0{}, kt);
+    if (kt + 1 < nk) step(Set1{}, kt + 1);
   }
 
   if constexpr (kEpi == kEpiQkv) {
