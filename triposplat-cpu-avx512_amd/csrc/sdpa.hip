@@ -420,9 +420,12 @@ int launch_shape(SdpaArgs a, const SdpaParams& p, hipStream_t stream, int cus = 
 }  // namespace
 
 // Shapes measured on MI355X at B=1, H=16, L=16384 (fp32 TFLOP/s): 16 waves x
-// 64-key tiles 128 (no bias, 36 B/lane of spill that costs nothing there),
-// the same per-32-key split 128 with a key bias (the unsplit bias kernel
-// spills more and drops to 116), 8 x 64 about 118-125, 4 x 64 115-120.
+// 64-key tiles 140 (unpacked) / 135 (packed) without a bias, the same tile
+// split per 32-key block 134.7 with a key bias (unsplit 124: it spills), 16 x
+// 128 split 130-134, 8 x 64 135-137, 4 x 64 121-123.  Storing the operand
+// that arrives key-major for V (or dim-major for K) transposed in LDS, so all
+// fragments are 128-bit reads, costs 2-4 %: the wider fragments push the
+// 16-wave kernels into spills.
 // Grids too small to give every CU one 512-query workgroup use 4 waves;
 // larger grids whose tile count is not a multiple of the CU count split the
 // remainder's keys (launch_shape).
