@@ -285,7 +285,8 @@ def run_flow(torch, dev, steps, with_cpu, validate):
 
     # one block on one branch, t_mod from the step-0 timestep
     t_emb, t_mod = model.timestep(torch.full((1,), 1000.0, device=dev))
-    x1, c1 = z[None].contiguous(), c[None].contiguous()
+    # block_forward updates x in place: time it on a copy, not on z itself
+    x1, c1 = z[None].clone(), c[None].contiguous()
     for _ in range(2):
         model.block_forward(model.blocks[0], x1, c1, t_mod)
     torch.cuda.synchronize()
@@ -361,7 +362,11 @@ def run_flow(torch, dev, steps, with_cpu, validate):
                 "speedup_gpu_vs_cpu": est / step_s,
             }
         if validate:
+            t0 = time.perf_counter()
+            cpu.progress = lambda i: print(f"cpu step: block {i + 1}/{cfg.blocks} "
+                                           f"({time.perf_counter() - t0:.0f} s)", file=sys.stderr, flush=True)
             zc, vc = cpu.euler_cfg_step(z_h, c_h)
+            out["config4_step"]["cpu_step_s"] = time.perf_counter() - t0
             out["config4_step"]["latent_rmse_vs_cpu"] = combined_rmse(zn.cpu().numpy(), zc)
             out["config4_step"]["velocity_rmse_vs_cpu"] = combined_rmse(v.cpu().numpy(), vc)
     del model

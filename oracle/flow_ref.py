@@ -30,6 +30,7 @@ class CpuFlow:
         self.cfg = cfg
         self.backend = backend
         self.threads = threads
+        self.progress = None  # optional callable(block index) after each block
         if backend == "reference" and not O.ref_available():
             raise RuntimeError("oracle/_ref not built")
 
@@ -158,8 +159,10 @@ class CpuFlow:
         B, L, C = z.shape
         t_emb, t_mod = self.timestep(t)
         x = self.linear(z.reshape(B * L, C), self.p["input_layer"]).reshape(B, L, C)
-        for bp in self.p["blocks"]:
+        for i, bp in enumerate(self.p["blocks"]):
             x = self.block(bp, x, cond, t_mod)
+            if self.progress is not None:
+                self.progress(i)
         fs = (self.p["final_shift_table"][None] + t_emb[:, None, :]).astype(np.float32)
         shift, scale = np.ascontiguousarray(fs[:, 0]), np.ascontiguousarray(fs[:, 1])
         h = self._modulate(self._ln(x, self.cfg.final_ln_eps), scale, shift)
