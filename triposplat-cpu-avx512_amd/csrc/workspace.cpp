@@ -1,11 +1,15 @@
-// Per-stream device workspaces for kernels that need scratch memory (split-K
-// partial sums, the QKV projection between the GEMM and the postprocess).
+// Per-stream device workspaces for kernels that need scratch memory: the
+// split-K partial sums of the few-row GEMM and the key-split partials of the
+// SDPA tail.  Every user overwrites the part it reads, so buffers are not
+// cleared.
 //
-// One grow-only buffer per (device, stream, slot), zero-filled when
-// allocated.  Calls on one stream are ordered by the stream, so they may
-// share its buffer; calls on different streams get different buffers.
-// Growing waits for the stream before the old buffer is released.  Buffers
-// live until the process ends.
+// One grow-only buffer per (device, stream, slot).  Calls on one stream are
+// ordered by the stream, so they may share its buffer; calls on different
+// streams get different buffers.  Growing waits for the stream before the
+// old buffer is released.  A stream under HIP-graph capture cannot allocate
+// or wait, so a call there that needs a larger buffer fails (the caller
+// returns -5); one eager call of the same or a larger shape on that stream
+// beforehand provides the buffer.  Buffers live until the process ends.
 
 #include <hip/hip_runtime.h>
 
@@ -35,6 +39,12 @@ void* stream_workspace(hipStream_t stream, size_t bytes, int slot) {
   if (g_buffers == nullptr) g_buffers = new std::map<std::tuple<int, hipStream_t, int>, Buffer>();
   Buffer& b = (*g_buffers)[std::make_tuple(dev, stream, slot)];
   if (b.bytes >= bytes && b.ptr != nullptr) return b.ptr;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (capture != hipStreamCaptureStatusNone) return nullptr;
   if (b.ptr != nullptr) {
     if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
     (void)hipFree(b.ptr);
@@ -44,14 +54,6 @@ void* stream_workspace(hipStream_t stream, size_t bytes, int slot) {
   const size_t want = bytes < 256 ? 256 : bytes;
   if (hipMalloc(&b.ptr, want) != hipSuccess) {
     (void)hipGetLastError();
-    b.ptr = nullptr;
-    return nullptr;
-  }
-  // New buffers start zeroed (counters kept in a workspace rely on it); the
-  // fill is ordered on the stream that will use the buffer.
-  if (hipMemsetAsync(b.ptr, 0, want, stream) != hipSuccess) {
-    (void)hipGetLastError();
-    (void)hipFree(b.ptr);
     b.ptr = nullptr;
     return nullptr;
   }
