@@ -238,12 +238,15 @@ int tsplat_nf24_gemm_precision_async(const float* x, const int16_t* code01_t,
                                      const float* gate, int64_t gate_stride, int rows_per_batch,
                                      int precision, void* stream);
 /* tsplat_gemm_nf24_qkv_direct_async with the projection in `precision`
- * (the RoPE / RMSNorm / pack epilogue is the same fp32 arithmetic). */
-int tsplat_gemm_nf24_qkv_direct_precision_async(
+ * (the RoPE / RMSNorm epilogue is the same fp32 arithmetic) and a choice of
+ * K/V layout: kv_layout 0 packed [B, H, 64, L_padded] (the reference's),
+ * 1 [B, H, L, 64] like q (L_padded ignored), the layout the unpacked SDPA
+ * reads.  No counterpart in the reference. */
+int tsplat_gemm_nf24_qkv_direct_ex_async(
     const float* x, const int16_t* code01_t, const int8_t* q2_t, const float* scale,
     const float* bias, const float* frequencies, const float* q_gamma, const float* k_gamma,
-    float* q_bhld, float* packed_k, float* packed_v, int B, int L, int K, int N, int H, int D,
-    int L_padded, int frequency_batches, int precision, void* stream);
+    float* q_bhld, float* k_out, float* v_out, int B, int L, int K, int N, int H, int D,
+    int L_padded, int frequency_batches, int kv_layout, int precision, void* stream);
 
 /* ---------------- flow-block elementwise -------------------------------- */
 /* Bit-identical per element to the reference kernels (same operation order,

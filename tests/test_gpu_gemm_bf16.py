@@ -1,5 +1,5 @@
 """GPU parity of the opt-in bf16-MFMA precision modes of the NF24 GEMM
-(tsplat_nf24_gemm_precision_async, tsplat_gemm_nf24_qkv_direct_precision_async).
+(tsplat_nf24_gemm_precision_async, tsplat_gemm_nf24_qkv_direct_ex_async).
 
 Oracle: oracle.nf24_gemm_bf16_terms, the float64 value of the terms the mode
 defines (bf16: xh*wh; bf16x3: xh*wh + xh*wl + xl*wh, bf16 = round to nearest

@@ -127,6 +127,39 @@ def test_qkv_fused_matches_unfused(oracle, cuda, B, L, H, fb):
         assert torch.equal(a_, b_)
 
 
+@pytest.mark.parametrize("B,L,H", [(1, 16384, 16), (2, 300, 4), (3, 257, 2), (1, 5000, 16)])
+def test_qkv_direct_bhld_layout(cuda, B, L, H):
+    """kv_layout="bhld": the same epilogue arithmetic storing k and v
+    [B, H, L, 64] like q -- bit-identical to the packed outputs transposed
+    (and q unchanged), at shapes routed to each tile configuration."""
+    import torch
+    from tsplat.nf24 import quantize_nf24_i16_per_output_channel
+    from tsplat.qkv import gemm_nf24_qkv_direct
+
+    print(f"qkv direct bhld B={B} L={L} H={H}", flush=True)
+    C = H * 64
+    g = torch.Generator(device=cuda).manual_seed(L + 1)
+    x = torch.randn((B * L, 1024), generator=g, device=cuda)
+    w = torch.randn((3 * C, 1024), generator=g, device=cuda) * 0.02
+    bias = torch.randn((3 * C,), generator=g, device=cuda) * 0.01
+    codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+    fr = torch.from_numpy(_freqs(1, L, H, 11)).to(cuda)
+    qg, kg = (torch.from_numpy(a).to(cuda) for a in _gammas(H, 12))
+    args = (x, codes[0], codes[1], scales[0], bias, fr, qg, kg, B, L, H)
+    q0, pk, pv = gemm_nf24_qkv_direct(*args)
+    q1, k1, v1 = gemm_nf24_qkv_direct(*args, kv_layout="bhld")
+    torch.cuda.synchronize(cuda)
+    assert k1.shape == (B, H, L, 64) and v1.shape == (B, H, L, 64)
+    assert torch.equal(q0, q1)
+    assert torch.equal(k1, pk[..., :L].transpose(2, 3))
+    assert torch.equal(v1, pv[..., :L].transpose(2, 3))
+    for p_ in ("bf16x3",):
+        qb, kb, vb = gemm_nf24_qkv_direct(*args, kv_layout="bhld", precision=p_)
+        _, pkb, pvb = gemm_nf24_qkv_direct(*args, precision=p_)
+        torch.cuda.synchronize(cuda)
+        assert torch.equal(kb, pkb[..., :L].transpose(2, 3)) and torch.equal(vb, pvb[..., :L].transpose(2, 3))
+
+
 def test_qkv_postprocess_golden(oracle, cuda, hiplib):
     """The reference's own outputs (tests/golden) through the reference-named
     blocking symbols, bit for bit."""

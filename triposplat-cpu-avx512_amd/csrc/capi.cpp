@@ -185,11 +185,13 @@ int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
                        const float* scale, const float* bias, const float* freqs,
                        const float* qg, const float* kg, float* q, float* pk, float* pv, int B,
                        int L, int K, int N, int H, int D, int Lp, int fb, hipStream_t stream,
-                       int precision = kPrecisionFp32) {
+                       int precision = kPrecisionFp32, int kv_layout = 0) {
   if (!x || !code01 || !q2 || !scale || !bias || !freqs || !qg || !kg || !q || !pk || !pv)
     return kErrNull;
   if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
     return kErrDims;
+  if (kv_layout != 0 && kv_layout != 1) return kErrDims;
+  if (kv_layout == 1) Lp = ((L + 15) / 16) * 16;  // unused by the [B, H, L, 64] layout
   if (B <= 0 || L <= 0 || K <= 0 || H <= 0 || D != kHeadDim || N != 3 * H * D || Lp < L ||
       (Lp & 15) != 0 || (fb != 1 && fb != B))
     return kErrDims;
@@ -206,11 +208,12 @@ int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
   TSPLAT_CHECK(check_dev(qg, C * 4));
   TSPLAT_CHECK(check_dev(kg, C * 4));
   TSPLAT_CHECK(check_dev(q, M * C * 4));
-  TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * Lp * 4));
-  TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lp * 4));
+  const int64_t kv_keys = kv_layout == 1 ? L : Lp;
+  TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * kv_keys * 4));
+  TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * kv_keys * 4));
   // RoPE, RMSNorm and the q / packed k,v stores run in the GEMM's epilogue.
   QkvFusedParams p{{x, code01, q2, scale, bias, nullptr, (int)M, K, N, 0, N, K, N, precision},
-                   freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb};
+                   freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb, kv_layout};
   const int st = launch_nf24_gemm_qkv(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
   return st;
@@ -449,14 +452,14 @@ int tsplat_gemm_nf24_qkv_direct_async(const float* x, const int16_t* code01_t, c
                             static_cast<hipStream_t>(stream));
 }
 
-int tsplat_gemm_nf24_qkv_direct_precision_async(
+int tsplat_gemm_nf24_qkv_direct_ex_async(
     const float* x, const int16_t* code01_t, const int8_t* q2_t, const float* scale,
     const float* bias, const float* frequencies, const float* q_gamma, const float* k_gamma,
-    float* q_bhld, float* packed_k, float* packed_v, int B, int L, int K, int N, int H, int D,
-    int L_padded, int frequency_batches, int precision, void* stream) {
+    float* q_bhld, float* k_out, float* v_out, int B, int L, int K, int N, int H, int D,
+    int L_padded, int frequency_batches, int kv_layout, int precision, void* stream) {
   return qkv_direct_checked(x, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, q_bhld,
-                            packed_k, packed_v, B, L, K, N, H, D, L_padded, frequency_batches,
-                            static_cast<hipStream_t>(stream), precision);
+                            k_out, v_out, B, L, K, N, H, D, L_padded, frequency_batches,
+                            static_cast<hipStream_t>(stream), precision, kv_layout);
 }
 
 // ------------------------------------------------------------------ packer

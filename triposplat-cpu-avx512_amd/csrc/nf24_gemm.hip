@@ -383,7 +383,7 @@ int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream) {
   if (gp.n_start != 0 || gp.n_count != gp.N || gp.N != 3 * p.H * 64 ||
       (int64_t)p.B * p.L != gp.M || p.L_padded < p.L)
     return kErrDims;
-  if (p.L_padded > p.L) {
+  if (!p.kv_bhld && p.L_padded > p.L) {
     const int64_t rows = (int64_t)p.B * p.H * 64;
     const int64_t n = rows * (p.L_padded - p.L);
     hipLaunchKernelGGL(packed_tail_zero_kernel,
@@ -392,7 +392,7 @@ int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream) {
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
   }
   const QkvArgs e{p.freqs, p.q_gamma, p.k_gamma, p.q, p.packed_k, p.packed_v,
-                  p.L, p.H, p.L_padded, p.freq_batches};
+                  p.L, p.H, p.L_padded, p.freq_batches, p.kv_bhld};
   const GemmEpilogueParams none{kEpilogueStore, nullptr, 0, 1};
   return launch_epi_kind<kEpiQkv>(gp, none, stream, e);
 }

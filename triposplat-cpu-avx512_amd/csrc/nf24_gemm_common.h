@@ -31,9 +31,10 @@ struct QkvArgs {
   const float* qg;     // [H, 64]
   const float* kg;     // [H, 64]
   float* q;            // [B, H, L, 64]
-  float* pk;           // [B, H, 64, Lpad]
-  float* pv;           // [B, H, 64, Lpad]
+  float* pk;           // [B, H, 64, Lpad], or [B, H, L, 64] with kv_bhld
+  float* pv;           // same layout as pk
   int L, H, Lpad, fb;
+  int kv_bhld;         // 1: k and v stored [B, H, L, 64] like q
 };
 
 struct GemmArgs {
@@ -78,7 +79,8 @@ __device__ __forceinline__ float head_sumsq_ref(float r0, float r1, int g, int l
 // RoPE (the partner of dim 2i / 2i+1 is the neighbouring lane) then
 // y * 8 / max(||y||, 1e-12) * gamma with ||y||^2 in the reference's order;
 // q is stored [B, H, L, 64], k and v key-contiguous [B, H, 64, Lpad] (four
-// consecutive tokens per 128-bit store when L % 4 == 0).  Same arithmetic as
+// consecutive tokens per 128-bit store when L % 4 == 0) or, with kv_bhld,
+// [B, H, L, 64] like q.  Same arithmetic as
 // qkv_postprocess.hip, so GEMM + this epilogue equals GEMM + postprocess
 // bit for bit.
 template <class C>
@@ -131,14 +133,15 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, floatx16 (&acc)[
         y0[t] = v0;
         y1[t] = v1;
       }
-      if (sec == 0) {
+      if (sec == 0 || e.kv_bhld) {
+        float* base = sec == 0 ? e.q : (sec == 1 ? e.pk : e.pv);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int row = row0 + t;
           if (row >= a.M) continue;
           const int tok = a.row0 + row;
           const int b = tok / e.L, l = tok - b * e.L;
-          float* dst = e.q + (((int64_t)b * e.H + h) * e.L + l) * 64;
+          float* dst = base + (((int64_t)b * e.H + h) * e.L + l) * 64;
           dst[l32] = y0[t];
           dst[32 + l32] = y1[t];
         }

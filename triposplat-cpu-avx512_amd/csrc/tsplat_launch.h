@@ -92,9 +92,10 @@ struct QkvFusedParams {
   const float* q_gamma;
   const float* k_gamma;
   float* q;
-  float* packed_k;
+  float* packed_k;         // [B, H, 64, L_padded], or [B, H, L, 64] with kv_bhld
   float* packed_v;
   int B, L, H, L_padded, freq_batches;
+  int kv_bhld = 0;
 };
 int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream);
 

@@ -45,7 +45,7 @@ SIGNATURES = {
     "tsplat_q_kv_selected_postprocess_async": ([_vp] * 9 + [_i] * 7 + [_vp], _i),
     "tsplat_qkv_postprocess_async": ([_vp] * 7 + [_i] * 6 + [_vp], _i),
     "tsplat_gemm_nf24_qkv_direct_async": ([_vp] * 11 + [_i] * 8 + [_vp], _i),
-    "tsplat_gemm_nf24_qkv_direct_precision_async": ([_vp] * 11 + [_i] * 9 + [_vp], _i),
+    "tsplat_gemm_nf24_qkv_direct_ex_async": ([_vp] * 11 + [_i] * 10 + [_vp], _i),
     "tsplat_nf24_pack_async": ([_vp, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp], _i),
     "tsplat_nf24_decode_async": ([_vp] * 4 + [_i] * 3 + [_vp], _i),
     "tsplat_nf24_gemm_epilogue_async": ([_vp] * 6 + [_i] * 8 + [_vp, _i64, _i, _vp], _i),

@@ -130,10 +130,9 @@ class JointFlowModel:
         sm, cm, gm, s2, c2, g2 = self._mod(blk, t_mod)
         lin = blk.lin
         h = bo.layer_norm(x, cfg.ln_eps, scale=cm, shift=sm)
-        q, pk, pv = lin["qkv"].qkv_direct(h.view(Ltot, C), self.freqs(L, Ltot - L), blk.q_gamma,
-                                          blk.k_gamma, 1, Ltot, H)
-        a = native_sdpa_f32_ex(q, pk, pv, kv_packed=True, key_count=Ltot, key_bias=key_bias,
-                               out_layout="blhd")
+        q, k, v = lin["qkv"].qkv_direct(h.view(Ltot, C), self.freqs(L, Ltot - L), blk.q_gamma,
+                                        blk.k_gamma, 1, Ltot, H, kv_layout="bhld")
+        a = native_sdpa_f32_ex(q, k, v, key_bias=key_bias, out_layout="blhd")
         x2 = x.view(Ltot, C)
         lin["out"].epilogue(a.view(Ltot, C), bo.EPILOGUE_GATED, out=x2, gate=gm)
         h = bo.layer_norm(x, cfg.ln_eps, scale=c2, shift=s2)

@@ -50,19 +50,25 @@ def qkv_rope_rmsnorm_pack(qkv, frequencies, q_gamma, k_gamma, B, L, H, *, L_padd
 
 
 def gemm_nf24_qkv_direct(x2, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, B, L, H, *,
-                         L_padded=None, precision="fp32", library=None):
+                         L_padded=None, precision="fp32", kv_layout="packed", library=None):
     """NF24 QKV projection of x2 [B*L, K] (N = 3*H*64) then the postprocess;
-    precision of the projection as tsplat.nf24.nf24_linear."""
+    precision of the projection as tsplat.nf24.nf24_linear.  kv_layout
+    "packed" returns k/v [B, H, 64, L_padded] (the reference's layout),
+    "bhld" returns k/v [B, H, L, 64] like q (what the unpacked SDPA reads)."""
     import torch
 
     from .nf24 import precision_id
 
     mode = precision_id(precision)
-
+    if kv_layout not in ("packed", "bhld"):
+        raise ValueError(f"kv_layout must be 'packed' or 'bhld', not {kv_layout!r}")
     for name, t in (("x", x2), ("frequencies", frequencies), ("q_gamma", q_gamma), ("k_gamma", k_gamma)):
         _check(torch, name, t)
     Lp = padded_length(L) if L_padded is None else int(L_padded)
-    q, pk, pv = _outputs(torch, B, L, H, Lp, x2.device)
+    if kv_layout == "packed":
+        q, pk, pv = _outputs(torch, B, L, H, Lp, x2.device)
+    else:
+        q, pk, pv = (torch.empty((B, H, L, 64), dtype=torch.float32, device=x2.device) for _ in range(3))
     lib = load_library(library)
     with torch.cuda.device(x2.device):
         args = (x2.data_ptr(), code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), bias.data_ptr(),
@@ -70,11 +76,11 @@ def gemm_nf24_qkv_direct(x2, code01_t, q2_t, scale, bias, frequencies, q_gamma, 
                 pv.data_ptr(), int(B), int(L), int(x2.shape[1]), int(code01_t.shape[1]), int(H), 64, Lp,
                 int(frequencies.shape[0]))
         stream = current_stream_handle(x2.device)
-        if mode == 0:
+        if mode == 0 and kv_layout == "packed":
             name, status = "tsplat_gemm_nf24_qkv_direct_async", lib.tsplat_gemm_nf24_qkv_direct_async(*args, stream)
         else:
-            name = "tsplat_gemm_nf24_qkv_direct_precision_async"
-            status = lib.tsplat_gemm_nf24_qkv_direct_precision_async(*args, mode, stream)
+            name = "tsplat_gemm_nf24_qkv_direct_ex_async"
+            status = lib.tsplat_gemm_nf24_qkv_direct_ex_async(*args, int(kv_layout == "bhld"), mode, stream)
     check_status(status, name)
     return q, pk, pv
 
