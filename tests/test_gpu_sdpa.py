@@ -51,12 +51,15 @@ def _run(torch, device, q, k, v, bias=None, per_head=False, packed=False, blhd=F
     return out.cpu().numpy()
 
 
-def _assert_close(got, ref, v):
+def _assert_close(got, ref, v, score_scale=1.0):
+    """SDPA tolerance of tests/_parity.py.  It is derived for scores of the
+    unit-normal q, k scale; with q and k c times larger the fp32 rounding of
+    q.k and of the exponent argument grow c-fold, so both bounds do."""
     s = stats(got, ref)
-    tol = SDPA_ATOL_PER_MAXV * float(np.abs(v).max())
+    tol = score_scale * SDPA_ATOL_PER_MAXV * float(np.abs(v).max())
     assert np.all(np.isfinite(got))
     assert s["max_abs"] <= tol, (s, tol)
-    assert s["rmse"] <= SDPA_RMSE_PER_RMSV * float(np.sqrt(np.mean(v.astype(np.float64) ** 2))), s
+    assert s["rmse"] <= score_scale * SDPA_RMSE_PER_RMSV * float(np.sqrt(np.mean(v.astype(np.float64) ** 2))), s
     return s
 
 
@@ -117,6 +120,39 @@ def test_sdpa_packed_blhd(oracle, cuda, B, H, Lq, Lk, bspec):
     pv[..., :Lk] = v.transpose(0, 1, 3, 2)
     ref = oracle.sdpa_q8t512_packed_blhd(q, pk, pv, Lk, bias)
     _assert_close(got, ref, v)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_sdpa_extreme_scores_and_masking_bias(oracle, cuda, packed):
+    """Scores spanning +-40 (q, k ~ 3 N(0,1): most weights underflow), and a
+    key bias of -1e4 on whole 64-key tiles, on the first tile only and on all
+    but a handful of keys -- the running max then jumps by ~1e4 mid-row and
+    the rescale factor underflows to 0.  The device result equals the oracle
+    within the SDPA tolerance and the float64 textbook within 1e-4; nothing
+    is NaN or inf."""
+    import torch
+
+    B, H, Lq, Lk = 1, 2, 130, 300
+    q, k, v = _qkv(57, B, H, Lq, Lk)
+    q, k = (q * np.float32(3)).astype(np.float32), (k * np.float32(3)).astype(np.float32)
+    masks = []
+    b = np.zeros(Lk, np.float32)
+    b[64:128] = -1e4                     # one whole tile masked
+    masks.append(b)
+    b = np.zeros(Lk, np.float32)
+    b[:64] = -1e4                        # the first tile: the max jumps by 1e4 at the second
+    masks.append(b)
+    b = np.full(Lk, -1e4, np.float32)
+    b[[5, 77, 203, 299]] = 0.0           # only four keys survive
+    masks.append(b)
+    for bias in [None] + masks:
+        got = _run(torch, cuda, q, k, v, bias, packed=packed, blhd=packed)
+        if packed:
+            got = got.transpose(0, 2, 1, 3)
+        assert np.all(np.isfinite(got))
+        ref = oracle.sdpa_q8t512(q, k, v, bias)
+        _assert_close(got, ref, v, score_scale=9.0)   # q.k is 3 x 3 times the unit-normal case
+        assert stats(got, sdpa_f64(q, k, v, bias))["max_abs"] < 1e-4
 
 
 def test_sdpa_per_head_bias(oracle, cuda):
