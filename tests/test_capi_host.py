@@ -132,3 +132,43 @@ def test_nf8_codebook_matches_closed_form():
     assert np.all(np.diff(cb) >= 0)
     lv = np.array(nf8_levels())
     assert np.allclose(lv, -lv[::-1], atol=1e-15)
+
+
+def test_precision_and_layout_validation_before_any_device_call(lib):
+    """The opt-in precision / K-V layout entry points reject unknown values
+    with -2 before any pointer is examined (dummy pointers)."""
+    P = [0x1000 + 16 * i for i in range(11)]
+    g = lib.tsplat_nf24_gemm_precision_async
+    assert g(*P[:6], 64, 64, 64, 0, 64, 64, 64, 0, None, 0, 1, 3, None) == -2   # precision 3
+    assert g(*P[:6], 64, 64, 64, 0, 64, 64, 64, 1, None, 0, 1, 1, None) == -2   # epilogue 1 (QKV only)
+    assert g(*P[:6], 64, 64, 64, 32, 64, 64, 64, 0, None, 0, 1, 1, None) == -3  # range past N
+    d = lib.tsplat_gemm_nf24_qkv_direct_ex_async
+    assert d(*P, 1, 20, 128, 384, 2, 64, 32, 1, 2, 0, None) == -2   # kv_layout 2
+    assert d(*P, 1, 20, 128, 384, 2, 64, 32, 1, 0, 7, None) == -2   # precision 7
+    assert d(*P, 1, 20, 128, 380, 2, 64, 32, 1, 1, 0, None) == -2   # N != 3*H*64
+
+
+def test_python_wrappers_reject_bad_options():
+    import torch
+    from tsplat.nf24 import nf24_linear, precision_id
+    from tsplat.qkv import gemm_nf24_qkv_direct
+
+    assert [precision_id(p) for p in ("fp32", "bf16", "bf16x3")] == [0, 1, 2]
+    z = torch.zeros(4, 4)
+    with pytest.raises(ValueError, match="precision"):
+        nf24_linear(z, z, z, z, z, precision="fp16")
+    with pytest.raises(ValueError, match="kv_layout"):
+        gemm_nf24_qkv_direct(z, z, z, z, z, z, z, z, 1, 4, 1, kv_layout="bshd")
+
+
+def test_bench_refuses_more_than_one_gpu():
+    import json
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
