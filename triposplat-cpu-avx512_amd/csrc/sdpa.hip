@@ -196,8 +196,9 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
     // One pass per group of kGB 32-key blocks: scores S^T[key][query] for keys
     // key0 + 32*kb + (8*(r/4) + 4*g + r%4), running max, exponentials, PV.
     constexpr int kGB = kSplit ? 1 : kNKB;
+    constexpr int kGroupUnroll = kSplit ? 1 : kNKB;
     const bool tail = key0 + kBKV > a.Lk;
-#pragma unroll(kSplit ? 1 : kNKB)
+#pragma unroll kGroupUnroll
     for (int kb0 = 0; kb0 < kNKB; kb0 += kGB) {
       floatx16 s[kGB];
 #pragma unroll
