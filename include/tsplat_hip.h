@@ -169,6 +169,10 @@ int triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512(
     int L_padded, int frequency_batches, int threads, int stages);
 /* gemm_nf24_qkv_direct_avx512.c:201-207 probes. */
 int triposplat_gemm_nf24_qkv_direct_row_tile(void);
+/* gemm_nf24_qkv_direct_tile_avx512.c:149-151: bytes of the tile variant's
+ * per-row-tile projection cache; 0 here (the fused epilogue reads the
+ * projection from MFMA accumulators, no intermediate buffer). */
+int triposplat_gemm_nf24_qkv_direct_tile_bytes(void);
 int triposplat_gemm_nf24_qkv_direct_residual_mode(void);
 
 /* Asynchronous forms of the two QKV entries. */

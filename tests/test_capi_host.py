@@ -49,6 +49,8 @@ def test_every_declared_symbol_is_exported(lib):
 def test_query_symbols(lib):
     assert lib.triposplat_gemm_rnf8_avx512_residual_mode() == 4
     assert lib.triposplat_gemm_nf24_qkv_direct_residual_mode() == 4
+    assert lib.triposplat_gemm_nf24_qkv_direct_row_tile() > 0
+    assert lib.triposplat_gemm_nf24_qkv_direct_tile_bytes() == 0
     assert lib.triposplat_gemm_rnf8_avx512_row_tile() > 0
     assert lib.triposplat_sdpa_packed_output_is_blhd() == 1
     assert lib.triposplat_sdpa_key_tile() == 64

@@ -431,6 +431,8 @@ int tsplat_q_kv_selected_postprocess_async(const float* q, const float* kv,
 }
 
 int triposplat_gemm_nf24_qkv_direct_row_tile(void) { return 128; }
+// The projection tile stays in MFMA accumulators: no row-tile cache buffer.
+int triposplat_gemm_nf24_qkv_direct_tile_bytes(void) { return 0; }
 int triposplat_gemm_nf24_qkv_direct_residual_mode(void) { return 4; }
 
 int tsplat_qkv_postprocess_async(const float* qkv, const float* frequencies, const float* q_gamma,

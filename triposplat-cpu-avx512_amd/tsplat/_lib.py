@@ -40,6 +40,7 @@ SIGNATURES = {
     "triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2": ([_vp] * 7 + [_i] * 7, _i),
     "triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512": ([_vp] * 15 + [_i] * 10, _i),
     "triposplat_gemm_nf24_qkv_direct_row_tile": ([], _i),
+    "triposplat_gemm_nf24_qkv_direct_tile_bytes": ([], _i),
     "triposplat_gemm_nf24_qkv_direct_residual_mode": ([], _i),
     "triposplat_q_kv_selected_rope_rmsnorm_pack_f32_avx512_v2": ([_vp] * 9 + [_i] * 8, _i),
     "tsplat_q_kv_selected_postprocess_async": ([_vp] * 9 + [_i] * 7 + [_vp], _i),
