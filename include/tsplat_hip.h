@@ -137,6 +137,35 @@ int triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2(const float* qkv, const float
                                                    int L_padded, int frequency_batches,
                                                    int threads);
 
+/* scripts/native_qkv_postprocess_avx512.c:23-116, the first version: same
+ * arguments and result as the _v2 entry (it zeroed all of packed k/v before
+ * filling; the bytes left are identical). */
+int triposplat_qkv_rope_rmsnorm_pack_f32_avx512(const float* qkv, const float* frequencies,
+                                                const float* q_gamma, const float* k_gamma,
+                                                float* q_bhld, float* packed_k, float* packed_v,
+                                                int B, int L, int H, int D, int L_padded,
+                                                int frequency_batches, int threads);
+/* native_qkv_postprocess_avx512.c:118-120 probe: tokens per transpose tile
+ * (64 here: one workgroup transposes 64 tokens of one (b, h) through LDS). */
+int triposplat_qkv_postprocess_token_tile(void);
+/* native_qkv_postprocess_v2_avx512.c:193-195 probe: 1, only the padding
+ * tokens L..L_padded-1 are cleared. */
+int triposplat_qkv_postprocess_v2_tail_only_clear(void);
+
+/* bf16 sensitivity probe of the K/V cache,
+ * scripts/native_qkv_postprocess_bf16_probe_avx512.c:34-94 (a build of the
+ * postprocess whose packed k and/or v are rounded to bf16 after the exact
+ * computation; build_native_qkv_postprocess_bf16_probe_avx512.sh selects
+ * k, v or kv at compile time).  Here the selection is a process-wide mode:
+ * bit 0 rounds k, bit 1 rounds v (nearest bf16, ties to even, stored as
+ * fp32; probe file :11-22), applied by every QKV postprocess entry -- the
+ * two above, the selected-rows entries and the fused NF24 QKV entries --
+ * to the k/v they store.  Default 0: exact.  Mode outside 0..3 -> -2.
+ * Calls already enqueued keep the mode they were launched with. */
+int tsplat_set_qkv_bf16_round(int mode);
+/* native_qkv_postprocess_bf16_probe_avx512.c:96-105: the current mode. */
+int triposplat_qkv_postprocess_bf16_probe_mode(void);
+
 /* scripts/native_qkv_postprocess_v2_avx512.c:107-191: selected query rows.
  * q [B, Lq, H*64] (a Q-only projection), kv [B, Lk, 2*H*64] = [k | v];
  * query t is rotated with frequency row selected_indices[t] (int64, device

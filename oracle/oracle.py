@@ -119,9 +119,11 @@ def decode_nf24(code01_t, q2_t, scale):
 # tests/test_oracle.py against torch's conversion, by the split invariants
 # and by operands that are exact in bf16 (the products then need no rounding).
 def bf16_round(a):
-    """fp32 -> nearest bf16, ties to even, returned as fp32 (finite inputs)."""
+    """fp32 -> nearest bf16, ties to even, returned as fp32; Inf and NaN keep
+    their upper 16 bits (scripts/native_qkv_postprocess_bf16_probe_avx512.c:11-22)."""
     u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    finite = (u & 0x7F800000) != 0x7F800000
+    r = np.where(finite, u + 0x7FFF + ((u >> 16) & 1), u) & 0xFFFF0000
     return r.astype(np.uint32).view(np.float32).reshape(np.shape(a))
 
 

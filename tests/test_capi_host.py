@@ -89,9 +89,13 @@ def test_status_codes_before_any_device_call(lib):
     pk = lib.triposplat_sdpa_f32_avx512_exact_q8t512_packed_blhd
     assert pk(P[0], P[1], P[2], None, P[4], 1, 2, 16, 20, 64, 24, 0, 0, 1) == -2  # Lkp % 16
     assert pk(P[0], P[1], P[2], None, P[4], 1, 2, 16, 20, 64, 16, 0, 0, 1) == -2  # Lkp < Lk
-    post = lib.triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2
-    assert post(*P[:7], 1, 20, 2, 64, 24, 1, 1) == -2      # L_padded % 16
-    assert post(*P[:7], 2, 20, 2, 64, 32, 3, 1) == -2      # frequency_batches
+    for post in (lib.triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2,
+                 lib.triposplat_qkv_rope_rmsnorm_pack_f32_avx512):
+        assert post(*P[:7], 1, 20, 2, 64, 24, 1, 1) == -2      # L_padded % 16
+        assert post(*P[:7], 2, 20, 2, 64, 32, 3, 1) == -2      # frequency_batches
+        assert post(None, *P[1:7], 1, 20, 2, 64, 32, 1, 1) == -1
+    assert lib.triposplat_qkv_postprocess_token_tile() == 64
+    assert lib.triposplat_qkv_postprocess_v2_tail_only_clear() == 1
     d = lib.triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512
     assert d(*(P + P[:5]), 1, 20, 128, 384, 2, 64, 32, 1, 1, 2) == -2   # stages
     assert d(*(P + P[:5]), 1, 20, 128, 380, 2, 64, 32, 1, 1, 3) == -2   # N != 3*H*64
@@ -174,3 +178,26 @@ def test_bench_refuses_more_than_one_gpu():
                        timeout=120)
     assert r.returncode == 2
     assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
+
+
+def test_kv_bf16_round_mode_switch(lib):
+    """The K/V bf16 probe mode is host state: set, read back, rejected when
+    out of range (unchanged), and reset; the Python switch maps the probe
+    build targets k / v / kv."""
+    from tsplat.qkv import kv_bf16_round, set_kv_bf16_round
+
+    assert lib.triposplat_qkv_postprocess_bf16_probe_mode() == 0
+    try:
+        assert lib.tsplat_set_qkv_bf16_round(3) == 0
+        assert lib.triposplat_qkv_postprocess_bf16_probe_mode() == 3
+        assert lib.tsplat_set_qkv_bf16_round(4) == -2
+        assert lib.tsplat_set_qkv_bf16_round(-1) == -2
+        assert lib.triposplat_qkv_postprocess_bf16_probe_mode() == 3
+        assert kv_bf16_round() == "kv"
+        assert set_kv_bf16_round("v") == "kv"
+        assert lib.triposplat_qkv_postprocess_bf16_probe_mode() == 2
+        with pytest.raises(ValueError, match="mode"):
+            set_kv_bf16_round("q")
+    finally:
+        assert lib.tsplat_set_qkv_bf16_round(0) == 0
+    assert kv_bf16_round() is None

@@ -160,15 +160,19 @@ def test_qkv_direct_bhld_layout(cuda, B, L, H):
         assert torch.equal(kb, pkb[..., :L].transpose(2, 3)) and torch.equal(vb, pvb[..., :L].transpose(2, 3))
 
 
-def test_qkv_postprocess_golden(oracle, cuda, hiplib):
+@pytest.mark.parametrize("symbol", ["triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2",
+                                    "triposplat_qkv_rope_rmsnorm_pack_f32_avx512"])
+def test_qkv_postprocess_golden(oracle, cuda, hiplib, symbol):
     """The reference's own outputs (tests/golden) through the reference-named
-    blocking symbols, bit for bit."""
+    blocking symbols (the second version and the first, which zeroed all of
+    packed k/v), bit for bit; outputs start as NaN, so the padding tokens
+    must be written as zeros."""
     import torch
 
     g = np.load(GOLDEN / "qkv_postprocess_2x20x2.npz")
     d = {k: torch.from_numpy(np.ascontiguousarray(g[k])).to(cuda) for k in g.files}
-    q = torch.empty_like(d["q"]); pk = torch.empty_like(d["packed_k"]); pv = torch.empty_like(d["packed_v"])
-    assert hiplib.triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2(
+    q, pk, pv = (torch.full_like(d[k], float("nan")) for k in ("q", "packed_k", "packed_v"))
+    assert getattr(hiplib, symbol)(
         d["qkv"].data_ptr(), d["freqs"].data_ptr(), d["q_gamma"].data_ptr(), d["k_gamma"].data_ptr(),
         q.data_ptr(), pk.data_ptr(), pv.data_ptr(), 2, 20, 2, 64, int(pk.shape[-1]),
         int(g["freqs"].shape[0]), 0) == 0
@@ -234,3 +238,65 @@ def test_device_packer_bit_exact(oracle, cuda, out_f, in_f):
     assert np.array_equal(codes[1].cpu().numpy(), q2)
     assert np.array_equal(scales[0].cpu().numpy().view(np.uint32), s.view(np.uint32))
     assert err["weight_rmse"] < 1e-6 and err["nf8_derived_alphabet_size"] == 163
+
+
+@pytest.mark.parametrize("mode", ["k", "v", "kv"])
+def test_kv_bf16_round_probe(oracle, cuda, hiplib, mode):
+    """The bf16 K/V sensitivity probe (native_qkv_postprocess_bf16_probe_avx512.c):
+    with the mode set, every postprocess form stores k and/or v as the
+    nearest bf16 of the exact value -- the oracle's exact outputs passed
+    through oracle.bf16_round, bit for bit -- and q and the unselected
+    operand stay exact; the fused projection equals GEMM + postprocess."""
+    import torch
+    from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
+    from tsplat.qkv import (gemm_nf24_qkv_direct, kv_bf16_round, q_kv_selected_rope_rmsnorm_pack,
+                            qkv_rope_rmsnorm_pack, set_kv_bf16_round)
+
+    print(f"kv bf16 round mode={mode}", flush=True)
+    B, L, H = 2, 37, 3
+    C = H * 64
+    r = np.random.default_rng(77)
+    qkv = r.standard_normal((B * L, 3 * C), dtype=np.float32)
+    fr = _freqs(1, L, H, 13)
+    qg, kg = _gammas(H, 14)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    exact = oracle.qkv_rope_rmsnorm_pack(qkv, fr, qg, kg, B, L, H)
+    rk, rv = "k" in mode, "v" in mode
+    want = (exact[0], oracle.bf16_round(exact[1]) if rk else exact[1],
+            oracle.bf16_round(exact[2]) if rv else exact[2])
+    assert not np.array_equal(want[1 if rk else 2], exact[1 if rk else 2])   # the rounding is visible
+    assert set_kv_bf16_round(mode) is None
+    try:
+        assert kv_bf16_round() == mode
+        assert hiplib.triposplat_qkv_postprocess_bf16_probe_mode() == {"k": 1, "v": 2, "kv": 3}[mode]
+        got = qkv_rope_rmsnorm_pack(t(qkv), t(fr), t(qg), t(kg), B, L, H)
+        for g_, w_ in zip(got, want):
+            assert np.array_equal(g_.cpu().numpy().view(np.uint32), w_.view(np.uint32))
+
+        sel = np.sort(r.choice(L, 20, replace=False)).astype(np.int64)
+        qs = r.standard_normal((B, 20, C), dtype=np.float32)
+        kv = np.ascontiguousarray(qkv.reshape(B, L, 3 * C)[..., C:])
+        st, ref = oracle.q_kv_selected_rope_rmsnorm_pack(qs, kv, fr, sel, qg, kg, B, 20, L, H)
+        assert st == 0
+        got = q_kv_selected_rope_rmsnorm_pack(t(qs), t(kv), t(fr), t(sel), t(qg), t(kg), B, 20, L, H)
+        for g_, w_, rnd in zip(got, ref, (False, rk, rv)):
+            w_ = oracle.bf16_round(w_) if rnd else w_
+            assert np.array_equal(g_.cpu().numpy().view(np.uint32), w_.view(np.uint32))
+
+        x = torch.from_numpy(r.standard_normal((B * L, 256), dtype=np.float32)).to(cuda)
+        w = torch.from_numpy((r.standard_normal((3 * C, 256)) * 0.02).astype(np.float32)).to(cuda)
+        bias = torch.zeros(3 * C, device=cuda)
+        codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+        args = (x, codes[0], codes[1], scales[0], bias, t(fr), t(qg), t(kg), B, L, H)
+        fused = gemm_nf24_qkv_direct(*args)
+        unfused = qkv_rope_rmsnorm_pack(nf24_linear(*args[:5]), *args[5:])
+        bhld = gemm_nf24_qkv_direct(*args, kv_layout="bhld")
+        torch.cuda.synchronize(cuda)
+        for a_, b_ in zip(fused, unfused):
+            assert torch.equal(a_, b_)
+        assert torch.equal(bhld[1], fused[1][..., :L].transpose(2, 3))
+        assert torch.equal(bhld[2], fused[2][..., :L].transpose(2, 3))
+        assert not fused[1][..., L:].any() and not fused[2][..., L:].any()
+    finally:
+        set_kv_bf16_round(None)
+    assert hiplib.triposplat_qkv_postprocess_bf16_probe_mode() == 0

@@ -96,3 +96,20 @@ def test_bf16_terms_error_bounds(oracle):
     rel3 = np.sqrt(np.mean(e3 ** 2) / np.mean(exact ** 2))
     assert 2.0 ** -12 < rel1 < 2.0 ** -6, rel1     # bf16 rounding is applied
     assert rel3 < rel1 / 64, (rel1, rel3)          # the lo terms recover ~8 bits
+
+
+def test_bf16_round_non_finite(oracle):
+    """Inf stays Inf with its sign; every NaN whose upper 7 mantissa bits are
+    not all zero stays NaN (its lower 16 bits are dropped, never carried
+    into the exponent or the sign); largest finite values round to Inf."""
+    r = np.random.default_rng(4)
+    inf = np.array([np.inf, -np.inf], np.float32)
+    assert np.array_equal(oracle.bf16_round(inf), inf)
+    mant = r.integers(1 << 16, 1 << 23, 4096, dtype=np.uint32)
+    sign = r.integers(0, 2, 4096, dtype=np.uint32) << 31
+    nan = (sign | 0x7F800000 | mant).view(np.float32)
+    out = oracle.bf16_round(nan)
+    assert np.all(np.isnan(out))
+    assert np.array_equal(out.view(np.uint32) >> 31, sign >> 31)
+    big = np.array([3.4028235e38, -3.4028235e38], np.float32)
+    assert np.array_equal(oracle.bf16_round(big), inf)

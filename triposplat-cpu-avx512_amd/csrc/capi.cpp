@@ -18,6 +18,9 @@
 namespace tsplat {
 namespace {
 std::atomic<int> g_last_hip_error{0};
+// bf16 rounding of the stored k (bit 0) and v (bit 1) applied by every QKV
+// postprocess entry; 0 (exact) unless tsplat_set_qkv_bf16_round changes it.
+std::atomic<int> g_kv_round{0};
 }  // namespace
 
 int note(hipError_t e) {
@@ -152,6 +155,7 @@ int post_checked(const float* qkv, const float* freqs, const float* qg, const fl
   TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * Lp * 4));
   TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lp * 4));
   QkvPostParams p{qkv, freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb};
+  p.kv_round = g_kv_round.load(std::memory_order_relaxed);
   const int st = launch_qkv_postprocess(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
   return st;
@@ -176,6 +180,7 @@ int selected_checked(const float* q, const float* kv, const float* freqs, const 
   TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * Lkp * 4));
   TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lkp * 4));
   QkvSelectedParams p{q, kv, freqs, sel, qg, kg, q_out, pk, pv, B, Lq, Lk, H, Lkp, fb};
+  p.kv_round = g_kv_round.load(std::memory_order_relaxed);
   const int st = launch_qkv_selected_postprocess(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
   return st;
@@ -214,6 +219,7 @@ int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
   // RoPE, RMSNorm and the q / packed k,v stores run in the GEMM's epilogue.
   QkvFusedParams p{{x, code01, q2, scale, bias, nullptr, (int)M, K, N, 0, N, K, N, precision},
                    freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb, kv_layout};
+  p.kv_round = g_kv_round.load(std::memory_order_relaxed);
   const int st = launch_nf24_gemm_qkv(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
   return st;
@@ -373,6 +379,36 @@ int triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2(const float* qkv, const float
                         D, L_padded, frequency_batches, nullptr);
   return st == kOk ? sync_null_stream() : st;
 }
+
+// The first version zeroed the whole packed buffers before filling them; the
+// second clears only tokens L..L_padded-1.  Both leave the same bytes, so
+// both names run the same kernel.
+int triposplat_qkv_rope_rmsnorm_pack_f32_avx512(const float* qkv, const float* frequencies,
+                                                const float* q_gamma, const float* k_gamma,
+                                                float* q_bhld, float* packed_k, float* packed_v,
+                                                int B, int L, int H, int D, int L_padded,
+                                                int frequency_batches, int threads) {
+  return triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2(qkv, frequencies, q_gamma, k_gamma,
+                                                        q_bhld, packed_k, packed_v, B, L, H, D,
+                                                        L_padded, frequency_batches, threads);
+}
+
+// Selects the bf16 rounding of stored k (bit 0) / v (bit 1) for all later
+// QKV postprocess calls of the process.
+int tsplat_set_qkv_bf16_round(int mode) {
+  if (mode < 0 || mode > 3) return kErrDims;
+  g_kv_round.store(mode, std::memory_order_relaxed);
+  return kOk;
+}
+
+int triposplat_qkv_postprocess_bf16_probe_mode(void) {
+  return g_kv_round.load(std::memory_order_relaxed);
+}
+
+// Tokens per workgroup of the postprocess kernel's k/v transpose.
+int triposplat_qkv_postprocess_token_tile(void) { return 64; }
+// Only the padding tokens of packed k/v are written as zeros.
+int triposplat_qkv_postprocess_v2_tail_only_clear(void) { return 1; }
 
 int triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512(
     const float* x, const uint8_t* codes0_t, const uint8_t* codes1_t, const uint8_t* codes2_t,

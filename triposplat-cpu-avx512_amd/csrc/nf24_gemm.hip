@@ -392,7 +392,7 @@ int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream) {
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
   }
   const QkvArgs e{p.freqs, p.q_gamma, p.k_gamma, p.q, p.packed_k, p.packed_v,
-                  p.L, p.H, p.L_padded, p.freq_batches, p.kv_bhld};
+                  p.L, p.H, p.L_padded, p.freq_batches, p.kv_bhld, p.kv_round};
   const GemmEpilogueParams none{kEpilogueStore, nullptr, 0, 1};
   return launch_epi_kind<kEpiQkv>(gp, none, stream, e);
 }

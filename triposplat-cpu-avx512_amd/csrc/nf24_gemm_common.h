@@ -35,6 +35,7 @@ struct QkvArgs {
   float* pv;           // same layout as pk
   int L, H, Lpad, fb;
   int kv_bhld;         // 1: k and v stored [B, H, L, 64] like q
+  int kv_round;        // bit 0: k, bit 1: v stored rounded to bf16
 };
 
 struct GemmArgs {
@@ -132,6 +133,13 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, floatx16 (&acc)[
         }
         y0[t] = v0;
         y1[t] = v1;
+      }
+      if (sec > 0 && ((e.kv_round >> (sec - 1)) & 1)) {  // uniform over the wave
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          y0[t] = bf16_roundtrip(y0[t]);
+          y1[t] = bf16_roundtrip(y1[t]);
+        }
       }
       if (sec == 0 || e.kv_bhld) {
         float* base = sec == 0 ? e.q : (sec == 1 ? e.pk : e.pv);

@@ -42,6 +42,7 @@ struct PostArgs {
   float* pv;
   int B, Lq, Lk, H, Lkp, fb;
   int q_tiles;             // blocks [0, B*H*q_tiles) do queries, the rest keys
+  int kv_round;            // bit 0: k, bit 1: v stored rounded to bf16
 };
 
 // RoPE + RMSNorm of the head row held as x[c] = dim 16c + j by lane j of a
@@ -127,6 +128,12 @@ __global__ __launch_bounds__(kThreads) void qkv_postprocess_kernel(PostArgs a) {
       }
       rope_rmsnorm_row(x, f, g, odd);
     }
+    if (a.kv_round & 1)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) x[c] = bf16_roundtrip(x[c]);
+    if (a.kv_round & 2)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] = bf16_roundtrip(v[c]);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       kl[tl][16 * c + j] = x[c];
@@ -169,7 +176,7 @@ int launch_qkv_postprocess(const QkvPostParams& p, hipStream_t stream) {
   const int64_t C = (int64_t)p.H * kD;
   PostArgs a{p.qkv, p.qkv + C, p.qkv + 2 * C, 3 * C, 3 * C, nullptr, p.freqs, p.q_gamma,
              p.k_gamma, p.q, p.packed_k, p.packed_v, p.B, p.L, p.L, p.H, p.L_padded,
-             p.freq_batches, (p.L + kTok - 1) / kTok};
+             p.freq_batches, (p.L + kTok - 1) / kTok, p.kv_round};
   return launch_post(a, stream);
 }
 
@@ -177,7 +184,7 @@ int launch_qkv_selected_postprocess(const QkvSelectedParams& p, hipStream_t stre
   const int64_t C = (int64_t)p.H * kD;
   PostArgs a{p.q, p.kv, p.kv + C, C, 2 * C, p.selected, p.freqs, p.q_gamma, p.k_gamma,
              p.q_out, p.packed_k, p.packed_v, p.B, p.Lq, p.Lk, p.H, p.Lk_padded,
-             p.freq_batches, (p.Lq + kTok - 1) / kTok};
+             p.freq_batches, (p.Lq + kTok - 1) / kTok, p.kv_round};
   return launch_post(a, stream);
 }
 

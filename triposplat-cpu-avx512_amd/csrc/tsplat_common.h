@@ -30,6 +30,14 @@ __device__ __forceinline__ floatx16 mfma32x32x2(float a, float b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// fp32 -> bf16 -> fp32 round trip, nearest with ties to even; Inf and NaN
+// keep their upper 16 bits (scripts/native_qkv_postprocess_bf16_probe_avx512.c:11-22).
+__device__ __forceinline__ float bf16_roundtrip(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7f800000u) != 0x7f800000u) u += 0x7fffu + ((u >> 16) & 1u);
+  return __uint_as_float(u & 0xffff0000u);
+}
+
 // Workgroup i of a launch is placed on XCD i % 8.  Renumber so that each XCD
 // receives one contiguous run of tile indices (neighbouring tiles share L2).
 __device__ __forceinline__ int xcd_tile_index(int id, int count) {

@@ -54,6 +54,8 @@ int launch_sdpa(const SdpaParams& p, hipStream_t stream);
 
 // qkv [B*L, 3*H*64] -> RoPE then RMSNorm on q and k; q [B, H, L, 64],
 // packed k/v [B, H, 64, L_padded] with tokens L..L_padded-1 zero.
+// kv_round (every QKV postprocess form): bit 0 stores k, bit 1 stores v
+// rounded to the nearest bf16 (kept as fp32); 0 stores them exact.
 struct QkvPostParams {
   const float* qkv;
   const float* freqs;    // [fb, L, H, 64] interleaved (cos, sin)
@@ -63,6 +65,7 @@ struct QkvPostParams {
   float* packed_k;
   float* packed_v;
   int B, L, H, L_padded, freq_batches;
+  int kv_round = 0;
 };
 int launch_qkv_postprocess(const QkvPostParams& p, hipStream_t stream);
 
@@ -80,6 +83,7 @@ struct QkvSelectedParams {
   float* packed_k;
   float* packed_v;
   int B, Lq, Lk, H, Lk_padded, freq_batches;
+  int kv_round = 0;
 };
 int launch_qkv_selected_postprocess(const QkvSelectedParams& p, hipStream_t stream);
 
@@ -96,6 +100,7 @@ struct QkvFusedParams {
   float* packed_v;
   int B, L, H, L_padded, freq_batches;
   int kv_bhld = 0;
+  int kv_round = 0;
 };
 int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream);
 

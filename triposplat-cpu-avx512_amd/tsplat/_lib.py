@@ -38,6 +38,11 @@ SIGNATURES = {
     "triposplat_sdpa_q8t512_workspace_release": ([], None),
     "tsplat_sdpa_async": ([_vp] * 5 + [_i] * 7 + [_i64] + [_i] * 3 + [_vp], _i),
     "triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2": ([_vp] * 7 + [_i] * 7, _i),
+    "triposplat_qkv_rope_rmsnorm_pack_f32_avx512": ([_vp] * 7 + [_i] * 7, _i),
+    "triposplat_qkv_postprocess_token_tile": ([], _i),
+    "triposplat_qkv_postprocess_v2_tail_only_clear": ([], _i),
+    "tsplat_set_qkv_bf16_round": ([_i], _i),
+    "triposplat_qkv_postprocess_bf16_probe_mode": ([], _i),
     "triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512": ([_vp] * 15 + [_i] * 10, _i),
     "triposplat_gemm_nf24_qkv_direct_row_tile": ([], _i),
     "triposplat_gemm_nf24_qkv_direct_tile_bytes": ([], _i),

@@ -14,6 +14,28 @@ from __future__ import annotations
 from ._lib import check_status, current_stream_handle, load_library
 
 
+KV_BF16_ROUND_MODES = {None: 0, "k": 1, "v": 2, "kv": 3}
+
+
+def set_kv_bf16_round(mode, *, library=None):
+    """Process-wide bf16 rounding of the k and/or v that every QKV
+    postprocess form stores: None (exact, the default), "k", "v" or "kv" --
+    the three builds of scripts/build_native_qkv_postprocess_bf16_probe_avx512.sh
+    (BF16_TARGET), as one switch.  Returns the previous mode."""
+    if mode not in KV_BF16_ROUND_MODES:
+        raise ValueError(f"kv bf16 round mode must be one of {sorted(KV_BF16_ROUND_MODES, key=str)}")
+    lib = load_library(library)
+    previous = kv_bf16_round(library=library)
+    check_status(lib.tsplat_set_qkv_bf16_round(KV_BF16_ROUND_MODES[mode]), "tsplat_set_qkv_bf16_round")
+    return previous
+
+
+def kv_bf16_round(*, library=None):
+    """The current mode (triposplat_qkv_postprocess_bf16_probe_mode)."""
+    bits = load_library(library).triposplat_qkv_postprocess_bf16_probe_mode()
+    return {v: k for k, v in KV_BF16_ROUND_MODES.items()}[bits]
+
+
 def padded_length(L: int) -> int:
     return (int(L) + 15) & ~15
 
