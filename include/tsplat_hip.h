@@ -124,6 +124,18 @@ int tsplat_sdpa_async(const float* q, const float* k, const float* v,
                       const float* key_bias_or_null, float* out, int B, int H, int Lq, int Lk,
                       int D, int has_key_bias, int key_bias_len, int64_t bias_head_stride,
                       int kv_packed, int Lkp, int out_blhd, void* stream);
+/* No reference counterpart (an opt-in mode; the reference SDPA is fp32
+ * only): tsplat_sdpa_async with the product precision of Q K^T and P V --
+ * 0 fp32 (= tsplat_sdpa_async), 1 bf16 (bf16(q') bf16(k), bf16(p) bf16(v)),
+ * 2 bf16x3 (three bf16 terms per product: hi*hi + hi*lo + lo*hi, 16
+ * significant bits per operand); q' = q * 0.125 * log2(e) in fp32, p the
+ * unnormalised exponentials; max, exp2, sums and normalisation in fp32.
+ * Other values -> -2. */
+int tsplat_sdpa_precision_async(const float* q, const float* k, const float* v,
+                                const float* key_bias_or_null, float* out, int B, int H, int Lq,
+                                int Lk, int D, int has_key_bias, int key_bias_len,
+                                int64_t bias_head_stride, int kv_packed, int Lkp, int out_blhd,
+                                int precision, void* stream);
 
 /* ---------------- QKV RoPE -> RMSNorm -> pack -------------------------- */
 

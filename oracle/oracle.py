@@ -184,6 +184,47 @@ def sdpa_q8t512(q, k, v, key_bias=None, bias_head_stride=0):
     return out
 
 
+LOG2E_F32 = np.float32(1.4426950408889634)
+SDPA_Q_SCALE_F32 = np.float32(np.float32(0.125) * LOG2E_F32)
+
+
+def sdpa_bf16_terms(q, k, v, key_bias=None, precision="bf16x3"):
+    """float64 reference of the opt-in bf16-MFMA SDPA modes.
+
+    The scores are the float64 value of the terms the mode forms from
+    q' = fp32(q * 0.125 * log2 e) and k ("bf16": qh.kh; "bf16x3": qh.kh +
+    qh.kl + ql.kh, bf16 = nearest-even rounding, bf16_split), plus
+    fp32(bias * log2 e), in log2 units; the softmax is exact (base 2) and the
+    values are the mode's representation of v (vh, or vh + vl).  key_bias:
+    None, [Lk] shared or [H, Lk] per head.  Returns (out [B,H,Lq,64] float64,
+    s_abs [B,H,Lq] = max over keys of the sum of |terms| (+ |bias|),
+    x_abs [B,H,Lq] = max over keys of |score|).  What this leaves open -- the
+    fp32 summation order, exp2, the split of the unnormalised exponentials
+    and the fp32 accumulation of P V -- is bounded by the caller."""
+    if precision not in ("bf16", "bf16x3"):
+        raise ValueError(precision)
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    three = precision == "bf16x3"
+    qs = (q * SDPA_Q_SCALE_F32).astype(np.float32)
+    (qh, ql), (kh, kl), (vh, vl) = bf16_split(qs), bf16_split(k), bf16_split(v)
+    f = lambda a: a.astype(np.float64)  # noqa: E731
+    t = lambda a, b: a @ np.swapaxes(b, -1, -2)  # noqa: E731
+    x = t(f(qh), f(kh))
+    s_abs = t(np.abs(f(qh)), np.abs(f(kh)))
+    if three:
+        x += t(f(qh), f(kl)) + t(f(ql), f(kh))
+        s_abs += t(np.abs(f(qh)), np.abs(f(kl))) + t(np.abs(f(ql)), np.abs(f(kh)))
+    if key_bias is not None:
+        kb = f((_f32(key_bias) * LOG2E_F32).astype(np.float32))
+        kb = kb[None, None, None, :] if kb.ndim == 1 else kb[None, :, None, :]
+        x = x + kb
+        s_abs = s_abs + np.abs(kb)
+    w = np.exp2(x - x.max(-1, keepdims=True))
+    w /= w.sum(-1, keepdims=True)
+    vv = f(vh) + f(vl) if three else f(vh)
+    return w @ vv, s_abs.max(-1), np.abs(x).max(-1)
+
+
 def sdpa_q8t512_packed_blhd(q, packed_k, packed_v, Lk, key_bias=None):
     """scripts/native_sdpa_avx512_exact_q8t512_packed.c:3-158 -> out [B,Lq,H,64]."""
     q, pk, pv = _f32(q), _f32(packed_k), _f32(packed_v)

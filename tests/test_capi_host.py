@@ -152,6 +152,10 @@ def test_precision_and_layout_validation_before_any_device_call(lib):
     assert d(*P, 1, 20, 128, 384, 2, 64, 32, 1, 2, 0, None) == -2   # kv_layout 2
     assert d(*P, 1, 20, 128, 384, 2, 64, 32, 1, 0, 7, None) == -2   # precision 7
     assert d(*P, 1, 20, 128, 380, 2, 64, 32, 1, 1, 0, None) == -2   # N != 3*H*64
+    s = lib.tsplat_sdpa_precision_async
+    assert s(*P[:5], 1, 2, 16, 16, 64, 0, 0, 0, 0, 0, 0, 3, None) == -2     # precision 3
+    assert s(*P[:5], 1, 2, 16, 16, 64, 0, 0, 0, 0, 0, 0, -1, None) == -2    # precision -1
+    assert s(*P[:5], 1, 2, 16, 16, 32, 0, 0, 0, 0, 0, 0, 2, None) == -2     # D != 64
 
 
 def test_python_wrappers_reject_bad_options():
@@ -165,6 +169,11 @@ def test_python_wrappers_reject_bad_options():
         nf24_linear(z, z, z, z, z, precision="fp16")
     with pytest.raises(ValueError, match="kv_layout"):
         gemm_nf24_qkv_direct(z, z, z, z, z, z, z, z, 1, 4, 1, kv_layout="bshd")
+    from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
+
+    q = torch.zeros(1, 2, 16, 64)
+    with pytest.raises(ValueError, match="precision"):
+        native_sdpa_f32_ex(q, q, q, precision="fp16")
 
 
 def test_bench_refuses_more_than_one_gpu():

@@ -1,0 +1,188 @@
+"""GPU parity of the opt-in bf16-MFMA SDPA modes (tsplat_sdpa_precision_async,
+native_sdpa_f32_ex(precision=...)).
+
+Oracle: oracle.sdpa_bf16_terms -- the float64 softmax of the scores the mode
+forms (q' = fp32(q * 0.125 * log2 e) and k split into bf16 terms, products
+exact) over the mode's representation of v.  What it leaves open is bounded
+here, per output element, relative to max|v'| of the (b, h):
+  - the fp32 summation of the n score terms (n = 64 or 192, + the bias):
+    gamma_n * sum|terms| (Higham Thm 3.1), the exponent argument x - m
+    (2^-24 * 2 max|x|) and v_exp_f32 (2^-23 relative): a score error E moves
+    the normalised weights by at most 2^(2E) - 1;
+  - the split of the unnormalised exponential p: bf16x3 keeps
+    |p v - (ph vh + ph vl + pl vh)| <= 2^-17 |p v|, bf16 2^-9 |p v|;
+  - the fp32 accumulation of P V and of the row sum over Lk keys (plus
+    one rescale per key tile) and the final 1/l: gamma_{3 Lk + T} +
+    gamma_{Lk + T + 1} + 2^-22; a key-split tail adds one more exp2 per part.
+The bound is rigorous and is checked on every element for small shapes
+(both grids: 4-wave for small grids, the wide shape for grids that fill the
+GPU).  At L = 8192-16384 the accumulation term is loose, so sampled rows are
+also held to a relative RMSE against the oracle well below what a dropped
+bf16 term would leave (about 2^-9).  One key gives p = 1 exactly, so the
+output is the value's representation bit for bit (vh, or fp32(vh + vl)).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _parity import U, stats
+
+pytestmark = pytest.mark.gpu
+
+
+def _gamma(n):
+    return n * U / (1.0 - n * U)
+
+
+def _inputs(seed, B, H, Lq, Lk, scale=8.0):
+    r = np.random.default_rng(seed)
+
+    def rows(n):
+        a = r.standard_normal((B, H, n, 64))
+        return (a / np.linalg.norm(a, axis=-1, keepdims=True) * scale).astype(np.float32)
+
+    return rows(Lq), rows(Lk), r.standard_normal((B, H, Lk, 64)).astype(np.float32)
+
+
+def _run(torch, device, q, k, v, precision, bias=None, per_head=False, packed=False, blhd=False):
+    from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
+
+    qd = torch.from_numpy(np.ascontiguousarray(q)).to(device)
+    Lk = k.shape[2]
+    if packed:
+        Lkp = (Lk + 15) // 16 * 16
+        pk = np.zeros(k.shape[:2] + (64, Lkp), np.float32)
+        pv = np.zeros_like(pk)
+        pk[..., :Lk] = k.transpose(0, 1, 3, 2)
+        pv[..., :Lk] = v.transpose(0, 1, 3, 2)
+        kd, vd = torch.from_numpy(pk).to(device), torch.from_numpy(pv).to(device)
+    else:
+        kd = torch.from_numpy(np.ascontiguousarray(k)).to(device)
+        vd = torch.from_numpy(np.ascontiguousarray(v)).to(device)
+    kw = {}
+    if bias is not None:
+        kw["key_bias_per_head" if per_head else "key_bias"] = torch.from_numpy(bias).to(device)
+    out = native_sdpa_f32_ex(qd, kd, vd, kv_packed=packed, key_count=Lk,
+                             out_layout="blhd" if blhd else "bhld", precision=precision, **kw)
+    torch.cuda.synchronize(device)
+    out = out.cpu().numpy()
+    return out.transpose(0, 2, 1, 3) if blhd else out
+
+
+def _bound(oracle, q, k, v, bias, precision, rows=None, key_tile=64, splits=1):
+    """(reference, per-element bound) for query rows `rows` (all if None)."""
+    qs = q if rows is None else q[:, :, rows]
+    ref, s_abs, x_abs = oracle.sdpa_bf16_terms(qs, k, v, bias, precision)
+    Lk = k.shape[2]
+    three = precision == "bf16x3"
+    n = (192 if three else 64) + (bias is not None)
+    E = _gamma(n) * s_abs + 4 * U * x_abs + 2.0 ** -22
+    eps_p = 2.0 ** -17 if three else 2.0 ** -9 * 1.01
+    T = (Lk + key_tile - 1) // key_tile
+    eps_acc = _gamma((3 if three else 1) * Lk + T) + _gamma(Lk + T + 1) + 2.0 ** -22 + splits * 2.0 ** -22
+    vh, vl = oracle.bf16_split(v)
+    vrep = vh.astype(np.float64) + (vl.astype(np.float64) if three else 0.0)
+    vmax = np.abs(vrep).max(axis=(-1, -2))[:, :, None, None]
+    return ref, ((np.exp2(2 * E) - 1)[..., None] + eps_p + eps_acc) * vmax * (1 + 1e-6)
+
+
+def _check(got, ref, bound):
+    assert np.all(np.isfinite(got))
+    d = np.abs(got.astype(np.float64) - ref)
+    assert np.all(d <= bound), (float(d.max()), float((d - bound).max()))
+
+
+def _bias(kind, H, Lk, seed):
+    r = np.random.default_rng(seed)
+    if kind == "shared":
+        return r.uniform(-2, 0, Lk).astype(np.float32)
+    if kind == "per_head":
+        return r.uniform(-2, 0, (H, Lk)).astype(np.float32)
+    return None
+
+
+PRECISIONS = ["bf16", "bf16x3"]
+
+
+@pytest.mark.parametrize("precision", PRECISIONS)
+@pytest.mark.parametrize("B,H,Lq,Lk,bias,packed,blhd", [
+    (1, 2, 37, 45, None, False, False),
+    (2, 3, 70, 200, "shared", False, False),
+    (1, 2, 130, 64, "per_head", False, True),
+    (1, 2, 50, 77, None, True, False),
+    (1, 3, 33, 300, "shared", True, True),
+    (1, 1, 1, 1, None, False, False),
+])
+def test_bf16_sdpa_small_grid_bound(oracle, cuda, precision, B, H, Lq, Lk, bias, packed, blhd):
+    import torch
+
+    print(f"sdpa {precision} B={B} H={H} Lq={Lq} Lk={Lk} bias={bias} packed={packed}", flush=True)
+    q, k, v = _inputs(Lq * 31 + Lk, B, H, Lq, Lk)
+    b = _bias(bias, H, Lk, Lk)
+    got = _run(torch, cuda, q, k, v, precision, b, per_head=bias == "per_head", packed=packed, blhd=blhd)
+    ref, bound = _bound(oracle, q, k, v, b, precision)
+    _check(got, ref, bound)
+
+
+@pytest.mark.parametrize("precision", PRECISIONS)
+@pytest.mark.parametrize("L,Lk,bias,packed", [
+    (8192, 8192, None, False),          # 256 query tiles of 512: the wide grid, no key split
+    (8192, 2048, "per_head", False),    # cross-attention shape with a per-head bias
+    (8192 + 512, 8192 + 512, None, True),   # last round split along the keys, packed K/V
+    (8192 + 512, 8193, "shared", False),    # key split with a ragged key tail and a bias
+])
+def test_bf16_sdpa_wide_grid_rows(oracle, cuda, precision, L, Lk, bias, packed):
+    import torch
+
+    H = 16
+    print(f"sdpa wide {precision} L={L} Lk={Lk} bias={bias} packed={packed}", flush=True)
+    q, k, v = _inputs(L + Lk, 1, H, L, Lk)
+    b = _bias(bias, H, Lk, 3)
+    got = _run(torch, cuda, q, k, v, precision, b, per_head=bias == "per_head", packed=packed)
+    rows = np.unique(np.concatenate([np.random.default_rng(L).choice(L, 40, replace=False),
+                                     [0, L - 1, L - 512, L - 257]]))
+    ref, bound = _bound(oracle, q, k, v, b, precision, rows=rows, splits=16)
+    sub = got[:, :, rows]
+    _check(sub, ref, bound)
+    rel = stats(sub, ref)["rel_rmse"]
+    print("relative RMSE vs oracle", rel, flush=True)
+    assert rel < (2.0 ** -15 if precision == "bf16x3" else 2.0 ** -9), rel
+
+
+@pytest.mark.parametrize("precision", PRECISIONS)
+@pytest.mark.parametrize("Lq", [40, 8192])
+def test_bf16_sdpa_single_key_exact(oracle, cuda, precision, Lq):
+    """Lk = 1: p = exp2(0) = 1 splits exactly (ph = 1, pl = 0), the sum is 1,
+    so every output row is the value's representation bit for bit."""
+    import torch
+
+    H = 16
+    q, k, v = _inputs(Lq, 1, H, Lq, 1)
+    got = _run(torch, cuda, q, k, v, precision)
+    vh, vl = oracle.bf16_split(v)
+    rep = (vh + vl).astype(np.float32) if precision == "bf16x3" else vh
+    assert np.array_equal(got.view(np.uint32), np.broadcast_to(rep, got.shape).view(np.uint32))
+
+
+def test_bf16_sdpa_config1_vs_strict(oracle, cuda):
+    """configs[1] (B=1, H=16, Lq=Lk=16384, RMS-normalised q, k of norm 8 as
+    after the flow's RMSNorm, v ~ N(0, 1)): each mode against the strict
+    fp32 kernel, and sampled rows against the oracle within the bound."""
+    import torch
+    from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
+
+    B, H, L = 1, 16, 16384
+    q, k, v = _inputs(99, B, H, L, L)
+    d = [torch.from_numpy(a).to(cuda) for a in (q, k, v)]
+    strict = native_sdpa_f32_ex(*d).cpu().numpy()
+    rows = np.sort(np.random.default_rng(1).choice(L, 24, replace=False))
+    rel = {}
+    for p in PRECISIONS:
+        got = native_sdpa_f32_ex(*d, precision=p).cpu().numpy()
+        ref, bound = _bound(oracle, q, k, v, None, p, rows=rows)
+        _check(got[:, :, rows], ref, bound)
+        rel[p] = stats(got, strict)["rel_rmse"]
+    print("relative RMSE vs strict fp32:", rel, flush=True)
+    assert rel["bf16x3"] < 2.0 ** -15, rel
+    assert rel["bf16"] < 2.0 ** -6, rel

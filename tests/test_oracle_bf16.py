@@ -113,3 +113,63 @@ def test_bf16_round_non_finite(oracle):
     assert np.array_equal(out.view(np.uint32) >> 31, sign >> 31)
     big = np.array([3.4028235e38, -3.4028235e38], np.float32)
     assert np.array_equal(oracle.bf16_round(big), inf)
+
+
+def _sdpa_inputs(seed, B, H, Lq, Lk, scale=8.0):
+    """RMS-normalised rows of norm `scale` (the flow's q and k after RMSNorm
+    with unit gamma), v ~ N(0, 1)."""
+    r = np.random.default_rng(seed)
+
+    def rows(n):
+        a = r.standard_normal((B, H, n, 64))
+        return (a / np.linalg.norm(a, axis=-1, keepdims=True) * scale).astype(np.float32)
+
+    return rows(Lq), rows(Lk), r.standard_normal((B, H, Lk, 64)).astype(np.float32)
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+@pytest.mark.parametrize("bias_kind", [None, "shared", "per_head"])
+def test_sdpa_bf16_terms_error_bounds(oracle, precision, bias_kind):
+    """The mode's float64 reference stays within what its rounding allows of
+    the textbook softmax(q k^T / 8 + b) v: a score error E (log2 units) moves
+    the normalised weights by at most a factor 2^(2E) - 1, and the value
+    representation adds eps_v max|v|.  Per product, bf16x3 keeps
+    |a b - (ah bh + ah bl + al bh)| <= 3.01 * 2^-18 |a b| and bf16 2^-8 |a b|."""
+    from _parity import sdpa_f64
+
+    B, H, Lq, Lk = 1, 3, 40, 70
+    q, k, v = _sdpa_inputs(5, B, H, Lq, Lk)
+    r = np.random.default_rng(6)
+    bias = {None: None, "shared": r.uniform(-2, 0, Lk).astype(np.float32),
+            "per_head": r.uniform(-2, 0, (H, Lk)).astype(np.float32)}[bias_kind]
+    got, s_abs, _ = oracle.sdpa_bf16_terms(q, k, v, bias, precision)
+    exact = sdpa_f64(q, k, v, bias)
+    rel, eps_v = (3.01 * 2.0 ** -18, 2.0 ** -17) if precision == "bf16x3" else (2.0 ** -8 * 1.01, 2.0 ** -8)
+    E = (rel + 2.0 ** -22) * s_abs + 2.0 ** -22 * (0 if bias is None else 2.0)
+    vmax = np.abs(v.astype(np.float64)).max(axis=(-1, -2))[..., None, None]
+    bound = ((np.exp2(2 * E) - 1)[..., None] + eps_v) * vmax
+    assert np.all(np.abs(got - exact) <= bound * (1 + 1e-9) + 1e-12)
+    err = np.sqrt(np.mean((got - exact) ** 2) / np.mean(exact ** 2))
+    if precision == "bf16x3":
+        assert err < 2.0 ** -14, err
+    else:
+        assert 2.0 ** -12 < err < 2.0 ** -5, err
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+def test_sdpa_bf16_terms_closed_forms(oracle, precision):
+    """One key: the output is the value's representation itself (vh, or
+    vh + vl).  Identical keys: equal weights, the mean of the represented
+    values.  Both are independent of q and of the score terms."""
+    q, k, v = _sdpa_inputs(7, 1, 2, 9, 1)
+    got, _, _ = oracle.sdpa_bf16_terms(q, k, v, None, precision)
+    vh, vl = oracle.bf16_split(v)
+    rep = vh.astype(np.float64) + (vl.astype(np.float64) if precision == "bf16x3" else 0)
+    np.testing.assert_array_equal(got, np.broadcast_to(rep, got.shape))
+    q, k, v = _sdpa_inputs(8, 1, 2, 9, 33)
+    k[:] = k[:, :, :1]
+    got, _, _ = oracle.sdpa_bf16_terms(q, k, v, None, precision)
+    vh, vl = oracle.bf16_split(v)
+    rep = vh.astype(np.float64) + (vl.astype(np.float64) if precision == "bf16x3" else 0)
+    np.testing.assert_allclose(got, np.broadcast_to(rep.mean(axis=2, keepdims=True), got.shape),
+                               rtol=0, atol=1e-14)

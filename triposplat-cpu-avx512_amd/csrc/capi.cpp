@@ -97,9 +97,11 @@ bool ref_gemm_ptrs_ok(const void* a, const void* b, const void* c, const void* d
 int sdpa_checked(const float* q, const float* k, const float* v, const float* bias, float* out,
                  int B, int H, int Lq, int Lk, int D, int has_bias, int bias_len,
                  int64_t bias_head_stride, int kv_packed, int Lkp, int out_blhd,
-                 hipStream_t stream) {
+                 hipStream_t stream, int precision = kPrecisionFp32) {
   if (!q || !k || !v || !out) return kErrNull;
   if (B <= 0 || H <= 0 || Lq <= 0 || Lk <= 0 || D != kHeadDim) return kErrDims;
+  if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
+    return kErrDims;
   if (kv_packed && (Lkp < Lk || (Lkp & 15) != 0)) return kErrDims;
   if (has_bias && (bias == nullptr || bias_len != Lk)) return kErrRange;
   if (has_bias && bias_head_stride != 0 && bias_head_stride < Lk) return kErrRange;
@@ -112,7 +114,7 @@ int sdpa_checked(const float* q, const float* k, const float* v, const float* bi
   TSPLAT_CHECK(check_dev(out, bh * Lq * kHeadDim * 4));
   if (has_bias) TSPLAT_CHECK(check_dev(bias, ((int64_t)(H - 1) * bias_head_stride + Lk) * 4));
   SdpaParams p{q, k, v, has_bias ? bias : nullptr, out, B, H, Lq, Lk, kv_packed, Lkp,
-               bias_head_stride, out_blhd};
+               bias_head_stride, out_blhd, precision};
   const int st = launch_sdpa(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
   return st;
@@ -365,6 +367,16 @@ int tsplat_sdpa_async(const float* q, const float* k, const float* v,
   return sdpa_checked(q, k, v, key_bias_or_null, out, B, H, Lq, Lk, D, has_key_bias,
                       key_bias_len, bias_head_stride, kv_packed, Lkp, out_blhd,
                       static_cast<hipStream_t>(stream));
+}
+
+int tsplat_sdpa_precision_async(const float* q, const float* k, const float* v,
+                                const float* key_bias_or_null, float* out, int B, int H, int Lq,
+                                int Lk, int D, int has_key_bias, int key_bias_len,
+                                int64_t bias_head_stride, int kv_packed, int Lkp, int out_blhd,
+                                int precision, void* stream) {
+  return sdpa_checked(q, k, v, key_bias_or_null, out, B, H, Lq, Lk, D, has_key_bias,
+                      key_bias_len, bias_head_stride, kv_packed, Lkp, out_blhd,
+                      static_cast<hipStream_t>(stream), precision);
 }
 
 // ------------------------------------------------------------------ QKV

@@ -26,44 +26,11 @@
 // the usual rescale by exp2(m_old - m_new), skipped when no lane's maximum
 // moved (alpha = 1 exactly).
 
-#include "tsplat_common.h"
-#include "tsplat_launch.h"
+#include "sdpa_common.h"
 
 namespace tsplat {
+namespace sdpa {
 namespace {
-
-constexpr int kD = 64;
-constexpr float kLog2e = 1.4426950408889634f;
-
-struct SdpaArgs {
-  const float* q;
-  const float* k;
-  const float* v;
-  const float* bias;
-  float* out;
-  int B, H, Lq, Lk, Lkp;
-  int64_t bias_head_stride;
-  int out_blhd;
-  // Tail split: workgroups [0, full_tiles) each own one query tile over all
-  // keys; the rest take one of `splits` key ranges (keys_per_split keys, a
-  // multiple of the key tile) of tile full_tiles + j / splits and write the
-  // unnormalised output rows and (max, sum) to part_o / part_ml, which
-  // sdpa_combine_kernel merges.
-  int full_tiles, splits, keys_per_split;
-  float* part_o;   // [split item][query][64]
-  float* part_ml;  // [split item][query][2]
-};
-
-// max / sum of a value with the same register of lane l ^ 32.  Both lanes of
-// a pair obtain the identical result (the swap returns both halves).
-__device__ __forceinline__ float pair_max(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float pair_sum(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 
 // kPacked: k/v are [B, H, 64, Lkp] (key-contiguous rows per dimension), as
 // the reference's packed kernel takes them; otherwise [B, H, Lk, 64].
@@ -94,15 +61,8 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
   const int l32 = lane & 31;
 
   const int qblocks = (a.Lq + kBQ - 1) / kBQ;
-  int tile, part = -1, k_begin = 0, k_end = a.Lk;
-  if ((int)blockIdx.x < a.full_tiles) {
-    tile = xcd_tile_index(blockIdx.x, a.full_tiles);
-  } else {  // tail: one key range of a query tile
-    part = blockIdx.x - a.full_tiles;
-    tile = a.full_tiles + part / a.splits;
-    k_begin = (part % a.splits) * a.keys_per_split;
-    k_end = min(a.Lk, k_begin + a.keys_per_split);
-  }
+  const TileWork w = tile_work(a);
+  const int tile = w.tile, part = w.part, k_begin = w.k_begin, k_end = w.k_end;
   const int bh = tile / qblocks;
   const int qb = tile % qblocks;
   const int h = bh % a.H;
@@ -306,119 +266,27 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
   }
 
   if (!q_ok) return;  // lanes l and l ^ 32 share the query: both leave or neither
-  const float lsum = pair_sum(l_run);
-  if (part >= 0) {  // unnormalised rows + (max, sum) for the combine kernel
-    const int64_t row = (int64_t)part * kBQ + wave * 32 + l32;
-    float* po = a.part_o + row * kD;
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        floatx4 y;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = o[db][4 * r4 + e];
-        *reinterpret_cast<floatx4*>(po + db * 32 + 8 * r4 + 4 * g) = y;
-      }
-    if (g == 0) {
-      a.part_ml[2 * row] = m_run;
-      a.part_ml[2 * row + 1] = lsum;
-    }
-    return;
-  }
-  const float inv = 1.0f / lsum;
-  float* dst = a.out_blhd ? a.out + (((int64_t)b * a.Lq + qrow) * a.H + h) * kD
-                          : a.out + ((int64_t)bh * a.Lq + qrow) * kD;
-#pragma unroll
-  for (int db = 0; db < 2; ++db)
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      floatx4 y;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = o[db][4 * r4 + e] * inv;
-      *reinterpret_cast<floatx4*>(dst + db * 32 + 8 * r4 + 4 * g) = y;
-    }
-}
-
-// Merge of the tail's key-range partials, one thread per (query, dim):
-// m = max m_s, w_s = exp2(m_s - m), out = (sum_s o_s w_s) * (1 / sum_s l_s w_s).
-constexpr int kCombineThreads = 256;
-__global__ __launch_bounds__(kCombineThreads) void sdpa_combine_kernel(SdpaArgs a, int q_per_tile,
-                                                                       int64_t rows) {
-  const int64_t i = (int64_t)blockIdx.x * kCombineThreads + threadIdx.x;
-  if (i >= rows * kD) return;
-  const int d = (int)(i % kD);
-  const int64_t r = i / kD;  // (tail tile, query in tile)
-  const int ptile = (int)(r / q_per_tile), qi = (int)(r % q_per_tile);
-  const int tile = a.full_tiles + ptile;
-  const int qblocks = (a.Lq + q_per_tile - 1) / q_per_tile;
-  const int bh = tile / qblocks, qrow = (tile % qblocks) * q_per_tile + qi;
-  if (qrow >= a.Lq) return;
-  const int64_t base = (int64_t)ptile * a.splits * q_per_tile + qi;
-  float m = -INFINITY;
-  for (int s = 0; s < a.splits; ++s) m = fmaxf(m, a.part_ml[2 * (base + (int64_t)s * q_per_tile)]);
-  float l = 0.0f, o = 0.0f;
-  for (int s = 0; s < a.splits; ++s) {
-    const int64_t row = base + (int64_t)s * q_per_tile;
-    const float w = __builtin_amdgcn_exp2f(a.part_ml[2 * row] - m);
-    l = fmaf(a.part_ml[2 * row + 1], w, l);
-    o = fmaf(a.part_o[row * kD + d], w, o);
-  }
-  const int b = bh / a.H, h = bh % a.H;
-  float* dst = a.out_blhd ? a.out + (((int64_t)b * a.Lq + qrow) * a.H + h) * kD
-                          : a.out + ((int64_t)bh * a.Lq + qrow) * kD;
-  dst[d] = o * (1.0f / l);
+  store_rows<kBQ>(a, o, m_run, l_run, part, b, h, bh, wave, qrow, g, l32);
 }
 
 template <int kWaves, int kBKV, bool kSplit>
-int launch_shape(SdpaArgs a, const SdpaParams& p, hipStream_t stream, int cus = 0) {
-  const int64_t tiles = (int64_t)p.B * p.H * ((p.Lq + kWaves * 32 - 1) / (kWaves * 32));
-  if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
-  // A last round that would leave CUs idle (tiles % CUs workgroups of a
-  // one-workgroup-per-CU shape) is split along the keys instead, so that the
-  // tail fills every CU; the partial results are merged by a second kernel.
-  int64_t grid_n = tiles;
-  a.full_tiles = (int)tiles;
-  a.splits = 1;
-  a.keys_per_split = p.Lk;
-  const int64_t rest = cus > 0 ? tiles % cus : 0;
-  if (cus > 0 && tiles >= cus && rest != 0) {
-    int splits = (int)((cus + rest - 1) / rest);
-    if (splits > 16) splits = 16;
-    const int kps = ((p.Lk + splits - 1) / splits + kBKV - 1) / kBKV * kBKV;
-    splits = (p.Lk + kps - 1) / kps;
-    if (splits >= 2) {
-      const size_t items = (size_t)rest * splits * kWaves * 32;
-      float* ws = static_cast<float*>(stream_workspace(stream, items * (kD + 2) * 4, kSlotSdpaPartial));
-      if (ws == nullptr) return kErrWorkspace;
-      a.full_tiles = (int)(tiles - rest);
-      a.splits = splits;
-      a.keys_per_split = kps;
-      a.part_o = ws;
-      a.part_ml = ws + items * kD;
-      grid_n = a.full_tiles + rest * splits;
+int launch_shape(const SdpaParams& p, hipStream_t stream, int cus = 0) {
+  const bool packed = p.kv_packed != 0, bias = p.bias != nullptr;
+  return launch_tiles(make_args(p), p, kWaves * 32, kBKV, cus, stream, [&](dim3 grid, const SdpaArgs& a) {
+    const dim3 block(kWaves * 64);
+    if (packed) {
+      if (bias) hipLaunchKernelGGL((sdpa_kernel<true, true, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((sdpa_kernel<true, false, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
+    } else {
+      if (bias) hipLaunchKernelGGL((sdpa_kernel<false, true, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((sdpa_kernel<false, false, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
     }
-  }
-  dim3 grid((unsigned)grid_n), block(kWaves * 64);
-  const bool bias = p.bias != nullptr;
-  if (p.kv_packed) {
-    if (bias) hipLaunchKernelGGL((sdpa_kernel<true, true, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((sdpa_kernel<true, false, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
-  } else {
-    if (bias) hipLaunchKernelGGL((sdpa_kernel<false, true, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((sdpa_kernel<false, false, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
-  }
-  if (hipGetLastError() != hipSuccess) return kErrLaunch;
-  if (a.splits > 1) {
-    const int64_t rows = (tiles - a.full_tiles) * (int64_t)(kWaves * 32);
-    hipLaunchKernelGGL(sdpa_combine_kernel,
-                       dim3((unsigned)((rows * kD + kCombineThreads - 1) / kCombineThreads)),
-                       dim3(kCombineThreads), 0, stream, a, kWaves * 32, rows);
-    if (hipGetLastError() != hipSuccess) return kErrLaunch;
-  }
-  return kOk;
+  });
 }
 
 }  // namespace
+
+}  // namespace sdpa
 
 // Shapes measured on MI355X at B=1, H=16, L=16384 (fp32 TFLOP/s): 16 waves x
 // 64-key tiles 140 (unpacked) / 135 (packed) without a bias, the same tile
@@ -431,15 +299,13 @@ int launch_shape(SdpaArgs a, const SdpaParams& p, hipStream_t stream, int cus = 
 // larger grids whose tile count is not a multiple of the CU count split the
 // remainder's keys (launch_shape).
 int launch_sdpa(const SdpaParams& p, hipStream_t stream) {
-  SdpaArgs a{p.q, p.k, p.v, p.bias, p.out, p.B, p.H, p.Lq, p.Lk, p.Lkp, p.bias_head_stride,
-             p.out_blhd, 0, 1, p.Lk, nullptr, nullptr};
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess)
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  using namespace sdpa;
+  if (p.precision != kPrecisionFp32) return launch_sdpa_bf16(p, stream);
+  const int cus = device_cus();
   const int64_t wide_tiles = (int64_t)p.B * p.H * ((p.Lq + 511) / 512);
-  if (wide_tiles < cus) return launch_shape<4, 64, false>(a, p, stream);
-  if (p.bias != nullptr) return launch_shape<16, 64, true>(a, p, stream, cus);
-  return launch_shape<16, 64, false>(a, p, stream, cus);
+  if (wide_tiles < cus) return launch_shape<4, 64, false>(p, stream);
+  if (p.bias != nullptr) return launch_shape<16, 64, true>(p, stream, cus);
+  return launch_shape<16, 64, false>(p, stream, cus);
 }
 
 }  // namespace tsplat

@@ -1,0 +1,194 @@
+// Pieces shared by the fp32 SDPA kernel (sdpa.hip) and its bf16-MFMA
+// precision modes (sdpa_bf16.hip): the kernel arguments, the half-wave pair
+// reductions, the merge of key-split partial results and the launch plan
+// that splits the last, partial round of query tiles along the keys.
+#pragma once
+
+#include "tsplat_common.h"
+#include "tsplat_launch.h"
+
+namespace tsplat {
+namespace sdpa {
+
+constexpr int kD = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct SdpaArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* bias;
+  float* out;
+  int B, H, Lq, Lk, Lkp;
+  int64_t bias_head_stride;
+  int out_blhd;
+  // Tail split: workgroups [0, full_tiles) each own one query tile over all
+  // keys; the rest take one of `splits` key ranges (keys_per_split keys, a
+  // multiple of the key tile) of tile full_tiles + j / splits and write the
+  // unnormalised output rows and (max, sum) to part_o / part_ml, which
+  // sdpa_combine_kernel merges.
+  int full_tiles, splits, keys_per_split;
+  float* part_o;   // [split item][query][64]
+  float* part_ml;  // [split item][query][2]
+};
+
+inline SdpaArgs make_args(const SdpaParams& p) {
+  return SdpaArgs{p.q,   p.k,  p.v,  p.bias, p.out, p.B, p.H, p.Lq, p.Lk, p.Lkp, p.bias_head_stride,
+                  p.out_blhd, 0, 1, p.Lk, nullptr, nullptr};
+}
+
+namespace {
+
+// max / sum of a value with the same register of lane l ^ 32.  Both lanes of
+// a pair obtain the identical result (the swap returns both halves).
+__device__ __forceinline__ float pair_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Query tile and key range of this workgroup (see SdpaArgs).
+struct TileWork {
+  int tile, part, k_begin, k_end;
+};
+__device__ __forceinline__ TileWork tile_work(const SdpaArgs& a) {
+  TileWork w{0, -1, 0, a.Lk};
+  if ((int)blockIdx.x < a.full_tiles) {
+    w.tile = xcd_tile_index(blockIdx.x, a.full_tiles);
+  } else {  // tail: one key range of a query tile
+    w.part = blockIdx.x - a.full_tiles;
+    w.tile = a.full_tiles + w.part / a.splits;
+    w.k_begin = (w.part % a.splits) * a.keys_per_split;
+    w.k_end = min(a.Lk, w.k_begin + a.keys_per_split);
+  }
+  return w;
+}
+
+// Final store of a wave's 32 queries: o[db][r] holds O^T[db*32 + 8*(r/4) +
+// 4*g + r%4][query] (the 32x32 MFMA accumulator layout), m_run / l_run the
+// lane's running max and partial sum.  Split parts write the unnormalised
+// rows and (max, sum) for the combine kernel.
+template <int kBQ>
+__device__ __forceinline__ void store_rows(const SdpaArgs& a, const floatx16 (&o)[2], float m_run,
+                                           float l_run, int part, int b, int h, int bh, int wave,
+                                           int qrow, int g, int l32) {
+  const float lsum = pair_sum(l_run);
+  if (part >= 0) {
+    const int64_t row = (int64_t)part * kBQ + wave * 32 + l32;
+    float* po = a.part_o + row * kD;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        floatx4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = o[db][4 * r4 + e];
+        *reinterpret_cast<floatx4*>(po + db * 32 + 8 * r4 + 4 * g) = y;
+      }
+    if (g == 0) {
+      a.part_ml[2 * row] = m_run;
+      a.part_ml[2 * row + 1] = lsum;
+    }
+    return;
+  }
+  const float inv = 1.0f / lsum;
+  float* dst = a.out_blhd ? a.out + (((int64_t)b * a.Lq + qrow) * a.H + h) * kD
+                          : a.out + ((int64_t)bh * a.Lq + qrow) * kD;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      floatx4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = o[db][4 * r4 + e] * inv;
+      *reinterpret_cast<floatx4*>(dst + db * 32 + 8 * r4 + 4 * g) = y;
+    }
+}
+
+// Merge of the tail's key-range partials, one thread per (query, dim):
+// m = max m_s, w_s = exp2(m_s - m), out = (sum_s o_s w_s) * (1 / sum_s l_s w_s).
+constexpr int kCombineThreads = 256;
+__global__ __launch_bounds__(kCombineThreads) void sdpa_combine_kernel(SdpaArgs a, int q_per_tile,
+                                                                       int64_t rows) {
+  const int64_t i = (int64_t)blockIdx.x * kCombineThreads + threadIdx.x;
+  if (i >= rows * kD) return;
+  const int d = (int)(i % kD);
+  const int64_t r = i / kD;  // (tail tile, query in tile)
+  const int ptile = (int)(r / q_per_tile), qi = (int)(r % q_per_tile);
+  const int tile = a.full_tiles + ptile;
+  const int qblocks = (a.Lq + q_per_tile - 1) / q_per_tile;
+  const int bh = tile / qblocks, qrow = (tile % qblocks) * q_per_tile + qi;
+  if (qrow >= a.Lq) return;
+  const int64_t base = (int64_t)ptile * a.splits * q_per_tile + qi;
+  float m = -INFINITY;
+  for (int s = 0; s < a.splits; ++s) m = fmaxf(m, a.part_ml[2 * (base + (int64_t)s * q_per_tile)]);
+  float l = 0.0f, o = 0.0f;
+  for (int s = 0; s < a.splits; ++s) {
+    const int64_t row = base + (int64_t)s * q_per_tile;
+    const float w = __builtin_amdgcn_exp2f(a.part_ml[2 * row] - m);
+    l = fmaf(a.part_ml[2 * row + 1], w, l);
+    o = fmaf(a.part_o[row * kD + d], w, o);
+  }
+  const int b = bh / a.H, h = bh % a.H;
+  float* dst = a.out_blhd ? a.out + (((int64_t)b * a.Lq + qrow) * a.H + h) * kD
+                          : a.out + ((int64_t)bh * a.Lq + qrow) * kD;
+  dst[d] = o * (1.0f / l);
+}
+
+// Launches `main(grid, args)` over the query tiles of kBQ queries.  A last
+// round that would leave CUs idle (tiles % CUs workgroups of a
+// one-workgroup-per-CU shape) is split along the keys instead, so that the
+// tail fills every CU; the partial results are merged by a second kernel.
+// cus = 0 disables the split.
+template <class Main>
+int launch_tiles(SdpaArgs a, const SdpaParams& p, int kBQ, int kBKV, int cus, hipStream_t stream,
+                 Main&& main) {
+  const int64_t tiles = (int64_t)p.B * p.H * ((p.Lq + kBQ - 1) / kBQ);
+  if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
+  int64_t grid_n = tiles;
+  a.full_tiles = (int)tiles;
+  a.splits = 1;
+  a.keys_per_split = p.Lk;
+  const int64_t rest = cus > 0 ? tiles % cus : 0;
+  if (cus > 0 && tiles >= cus && rest != 0) {
+    int splits = (int)((cus + rest - 1) / rest);
+    if (splits > 16) splits = 16;
+    const int kps = ((p.Lk + splits - 1) / splits + kBKV - 1) / kBKV * kBKV;
+    splits = (p.Lk + kps - 1) / kps;
+    if (splits >= 2) {
+      const size_t items = (size_t)rest * splits * kBQ;
+      float* ws = static_cast<float*>(stream_workspace(stream, items * (kD + 2) * 4, kSlotSdpaPartial));
+      if (ws == nullptr) return kErrWorkspace;
+      a.full_tiles = (int)(tiles - rest);
+      a.splits = splits;
+      a.keys_per_split = kps;
+      a.part_o = ws;
+      a.part_ml = ws + items * kD;
+      grid_n = a.full_tiles + rest * splits;
+    }
+  }
+  main(dim3((unsigned)grid_n), a);
+  if (hipGetLastError() != hipSuccess) return kErrLaunch;
+  if (a.splits > 1) {
+    const int64_t rows = (tiles - a.full_tiles) * (int64_t)kBQ;
+    hipLaunchKernelGGL(sdpa_combine_kernel,
+                       dim3((unsigned)((rows * kD + kCombineThreads - 1) / kCombineThreads)),
+                       dim3(kCombineThreads), 0, stream, a, kBQ, rows);
+    if (hipGetLastError() != hipSuccess) return kErrLaunch;
+  }
+  return kOk;
+}
+
+inline int device_cus() {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  return cus;
+}
+
+}  // namespace
+}  // namespace sdpa
+}  // namespace tsplat

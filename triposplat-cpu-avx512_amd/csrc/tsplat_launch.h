@@ -49,8 +49,15 @@ struct SdpaParams {
   int Lkp;             // key stride of the packed layout
   int64_t bias_head_stride;  // 0: one [Lk] row shared by all heads
   int out_blhd;        // 1: write [B, Lq, H, 64]
+  // Product precision of Q K^T and P V (GemmPrecision): kPrecisionFp32 on
+  // fp32 MFMA (default); kPrecisionBf16 / kPrecisionBf16x3 split the
+  // operands into bf16 terms as the NF24 GEMM's modes do (q scaled first,
+  // p = the unnormalised exponentials); softmax arithmetic stays fp32.
+  int precision = kPrecisionFp32;
 };
 int launch_sdpa(const SdpaParams& p, hipStream_t stream);
+// The bf16-MFMA modes (called by launch_sdpa for precision != fp32).
+int launch_sdpa_bf16(const SdpaParams& p, hipStream_t stream);
 
 // qkv [B*L, 3*H*64] -> RoPE then RMSNorm on q and k; q [B, H, L, 64],
 // packed k/v [B, H, 64, L_padded] with tokens L..L_padded-1 zero.

@@ -37,6 +37,7 @@ SIGNATURES = {
     "triposplat_sdpa_q8t512_workspace_stats": ([ctypes.POINTER(ctypes.c_uint64)] * 2, _i),
     "triposplat_sdpa_q8t512_workspace_release": ([], None),
     "tsplat_sdpa_async": ([_vp] * 5 + [_i] * 7 + [_i64] + [_i] * 3 + [_vp], _i),
+    "tsplat_sdpa_precision_async": ([_vp] * 5 + [_i] * 7 + [_i64] + [_i] * 4 + [_vp], _i),
     "triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2": ([_vp] * 7 + [_i] * 7, _i),
     "triposplat_qkv_rope_rmsnorm_pack_f32_avx512": ([_vp] * 7 + [_i] * 7, _i),
     "triposplat_qkv_postprocess_token_tile": ([], _i),

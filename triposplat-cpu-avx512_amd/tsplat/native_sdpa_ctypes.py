@@ -81,15 +81,21 @@ def native_sdpa_f32(q, k, v, *, key_bias=None, library=None, symbol=None, thread
 
 
 def native_sdpa_f32_ex(q, k, v, *, key_bias=None, key_bias_per_head=None, kv_packed=False,
-                       key_count=None, out=None, out_layout="bhld", library=None):
+                       key_count=None, out=None, out_layout="bhld", precision="fp32", library=None):
     """Extended device SDPA.
 
     q [B,H,Lq,64] fp32.  k/v [B,H,Lk,64], or with kv_packed=True
     [B,H,64,Lkp] key-contiguous (Lkp % 16 == 0) with key_count = Lk valid keys.
     key_bias [Lk] (shared) or key_bias_per_head [H,Lk].  out_layout "bhld"
-    -> [B,H,Lq,64], "blhd" -> [B,Lq,H,64].  Returns the output tensor.
+    -> [B,H,Lq,64], "blhd" -> [B,Lq,H,64].  precision: "fp32" (strict, the
+    default), or the opt-in bf16-MFMA products "bf16" / "bf16x3" of
+    tsplat_sdpa_precision_async.  Returns the output tensor.
     """
     import torch
+
+    from .nf24 import precision_id
+
+    prec = precision_id(precision)
 
     for name, t in (("q", q), ("k", k), ("v", v)):
         if t.device.type != "cuda" or t.dtype != torch.float32 or not t.is_contiguous():
@@ -126,10 +132,10 @@ def native_sdpa_f32_ex(q, k, v, *, key_bias=None, key_bias_per_head=None, kv_pac
         raise ValueError(f"out must be a contiguous fp32 tensor of shape {shape}")
     lib = load_library(library)
     with torch.cuda.device(q.device):
-        status = lib.tsplat_sdpa_async(
+        status = lib.tsplat_sdpa_precision_async(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), 0 if bias is None else bias.data_ptr(),
             out.data_ptr(), B, H, Lq, Lk, 64, int(bias is not None), Lk if bias is not None else 0,
-            stride, int(bool(kv_packed)), Lkp, blhd, current_stream_handle(q.device),
+            stride, int(bool(kv_packed)), Lkp, blhd, prec, current_stream_handle(q.device),
         )
-    check_status(status, "tsplat_sdpa_async")
+    check_status(status, "tsplat_sdpa_precision_async")
     return out

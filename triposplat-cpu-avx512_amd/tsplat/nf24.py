@@ -135,7 +135,7 @@ PRECISIONS = {"fp32": 0, "bf16": 1, "bf16x3": 2}
 
 def precision_id(precision) -> int:
     if precision not in PRECISIONS:
-        raise ValueError(f"unknown GEMM precision {precision!r}; expected one of {sorted(PRECISIONS)}")
+        raise ValueError(f"unknown product precision {precision!r}; expected one of {sorted(PRECISIONS)}")
     return PRECISIONS[precision]
 
 
