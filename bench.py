@@ -165,6 +165,40 @@ def run_sdpa(torch, dev, steps, warmup, host):
     return wall, kernel_ms
 
 
+def run_sdpa_opt_in(torch, dev, host, fp32_ms, iters=5):
+    """configs[1] with the opt-in bf16-MFMA SDPA products: time, the
+    equivalent rate (the same 4*B*H*L^2*64 algorithmic FLOP), the MFMA work
+    against the bf16 peak (three products per term for bf16x3), and the
+    error against the strict fp32 output."""
+    from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
+
+    q_h, k_h, v_h = host
+    B, H, L, D = q_h.shape
+    q, k, v = (torch.from_numpy(a).to(dev) for a in (q_h, k_h, v_h))
+    flop = 4.0 * B * H * L * L * D
+    strict = native_sdpa_f32_ex(q, k, v)
+    out = torch.empty_like(strict)
+    res = {}
+    for precision, terms in (("bf16", 1), ("bf16x3", 3)):
+        def step(p=precision):
+            native_sdpa_f32_ex(q, k, v, out=out, precision=p)
+
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        ms = sorted(time_events(torch, step, iters) for _ in range(3))[1]
+        d = out.double() - strict.double()
+        res[precision] = {
+            "ms": ms, "tflops_equiv": flop / (ms * 1e-3) / 1e12,
+            "frac_bf16_mfma_peak": terms * flop / (ms * 1e-3) / 1e12 / PEAK_BF16_MFMA,
+            "speedup_vs_fp32": fp32_ms / ms,
+            "rel_rmse_vs_fp32": float(d.pow(2).mean().sqrt() / strict.double().pow(2).mean().sqrt()),
+            "max_abs_vs_fp32": float(d.abs().max()),
+        }
+    del strict, out
+    return res
+
+
 def run_sdpa_variants(torch, dev, host, iters=5):
     """key-bias self attention (per-head bias [16, 16384] ~ U(-2, 0),
     and the reference-faithful shared [Lk] bias with log(2048) on one key),
@@ -306,32 +340,37 @@ def run_flow(torch, dev, steps, with_cpu, validate):
         times.append(time.perf_counter() - t0)
     step_s = sorted(times)[len(times) // 2]
     step_flop = 2 * cfg.blocks * per_branch_flop
-    # opt-in: the block Linears with bf16x3 products (timestep / io Linears
-    # and everything else unchanged); latent RMSE against the strict step
-    model.set_precision("bf16x3")
-    model.euler_cfg_step(z, c)
-    torch.cuda.synchronize()
-    times3 = []
-    for _ in range(max(1, steps)):
-        t0 = time.perf_counter()
-        zn3, v3 = model.euler_cfg_step(z, c)
+    # opt-in: bf16x3 products in the block Linears, then also in the SDPA
+    # (timestep / io Linears and everything else unchanged); latent RMSE
+    # against the strict step
+    def opt_in_step(include):
+        model.set_precision("bf16x3", include=include)
+        model.euler_cfg_step(z, c)
         torch.cuda.synchronize()
-        times3.append(time.perf_counter() - t0)
-    model.set_precision("fp32")
-    step3_s = sorted(times3)[len(times3) // 2]
-    bf16x3_step = {
-        "s_per_denoise_step": step3_s, "speedup_vs_fp32": step_s / step3_s,
-        "latent_rmse_vs_fp32_step": float((zn3.double() - zn.double()).pow(2).mean().sqrt()),
-        "velocity_rmse_vs_fp32_step": float((v3.double() - v.double()).pow(2).mean().sqrt()),
-    }
-    del zn3, v3
+        times3 = []
+        for _ in range(max(1, steps)):
+            t0 = time.perf_counter()
+            zn3, v3 = model.euler_cfg_step(z, c)
+            torch.cuda.synchronize()
+            times3.append(time.perf_counter() - t0)
+        model.set_precision("fp32")
+        step3_s = sorted(times3)[len(times3) // 2]
+        return {
+            "s_per_denoise_step": step3_s, "speedup_vs_fp32": step_s / step3_s,
+            "latent_rmse_vs_fp32_step": float((zn3.double() - zn.double()).pow(2).mean().sqrt()),
+            "velocity_rmse_vs_fp32_step": float((v3.double() - v.double()).pow(2).mean().sqrt()),
+        }
+
+    bf16x3_step = opt_in_step(("blocks",))
+    bf16x3_attn_step = opt_in_step(("blocks", "attention"))
     out = {
         "config3_block": {"workload": "configs[3] one flow block, L=16384 latent + 2048 condition tokens, one branch",
                           "ms": blk_ms, "tflops": per_branch_flop / (blk_ms * 1e-3) / 1e12},
         "config4_step": {"workload": "configs[4] 28 blocks, CFG batch 2, one Euler step (guidance 3, shift 3)",
                          "s_per_denoise_step": step_s, "tflops": step_flop / step_s / 1e12,
                          "model_setup_s": setup_s, "finite": bool(torch.isfinite(zn).all().item()),
-                         "opt_in_bf16x3_block_linears": bf16x3_step},
+                         "opt_in_bf16x3_block_linears": bf16x3_step,
+                         "opt_in_bf16x3_block_linears_and_attention": bf16x3_attn_step},
     }
     if with_cpu or validate:
         sys.path.insert(0, str(ROOT / "oracle"))
@@ -533,6 +572,7 @@ def main():
         return 0
 
     variants = run_sdpa_variants(torch, dev, host)
+    sdpa_opt_in = run_sdpa_opt_in(torch, dev, host, kernel_ms)
     gemm = run_gemm(torch, dev, 20)
     gemm["skinny_m"] = run_gemm_skinny(torch, dev)
     flow = None if args.no_flow else run_flow(torch, dev, 3, not args.no_cpu_baseline, args.validate_flow)
@@ -566,6 +606,7 @@ def main():
             "flop_per_launch": sdpa_flop,
         },
         "cpu_baseline": cpu,
+        "sdpa_opt_in_bf16": sdpa_opt_in,
         "sdpa_config2": variants,
         "gemm_config0": gemm,
         "flow": flow,

@@ -65,9 +65,10 @@ def test_flow_block_matches_cpu(oracle, cuda):
 
 
 def test_flow_step_opt_in_bf16(oracle, cuda):
-    """The opt-in bf16-MFMA block Linears: bf16x3 products keep the step
-    within the latent gate against the CPU fp32 path; plain bf16 is reported
-    (it is expected to miss the gate) and must be coarser than bf16x3."""
+    """The opt-in bf16-MFMA products: bf16x3 in the block Linears, and in
+    the block Linears and the SDPA, keeps the step within the latent gate
+    against the CPU fp32 path; plain bf16 is reported (it is expected to
+    miss the gate) and must be coarser than bf16x3."""
     import torch
     from flow_ref import CpuFlow, combined_rmse
     from tsplat.flow import FlowConfig, FlowModel
@@ -78,10 +79,12 @@ def test_flow_step_opt_in_bf16(oracle, cuda):
     zd, cd = torch.from_numpy(z).to(cuda), torch.from_numpy(c).to(cuda)
     strict, _ = model.euler_cfg_step(zd, cd)
     res = {}
-    for p in ("bf16x3", "bf16"):
-        model.set_precision(p)
+    for name, p, include in (("bf16x3", "bf16x3", ("blocks",)), ("bf16", "bf16", ("blocks",)),
+                             ("bf16x3_attn", "bf16x3", ("blocks", "attention"))):
+        model.set_precision(p, include=include)
+        assert model.attention_precision == (p if "attention" in include else "fp32")
         zn, _ = model.euler_cfg_step(zd, cd)
-        res[p] = zn.cpu().numpy()
+        res[name] = zn.cpu().numpy()
     model.set_precision("fp32")
     again, _ = model.euler_cfg_step(zd, cd)
     torch.cuda.synchronize()
@@ -91,6 +94,7 @@ def test_flow_step_opt_in_bf16(oracle, cuda):
     rm["fp32"] = combined_rmse(strict.cpu().numpy(), zn_c)
     print({"latent_rmse_vs_cpu": rm})
     assert np.all(np.isfinite(res["bf16"])) and np.all(np.isfinite(res["bf16x3"]))
-    assert rm["bf16x3"] <= 1e-4
+    assert rm["bf16x3"] <= 1e-4 and rm["bf16x3_attn"] <= 1e-4
     assert not np.array_equal(res["bf16x3"], strict.cpu().numpy())
+    assert not np.array_equal(res["bf16x3_attn"], res["bf16x3"])
     assert rm["bf16"] > 4 * rm["bf16x3"]

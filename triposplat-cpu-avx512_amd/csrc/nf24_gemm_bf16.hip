@@ -68,14 +68,27 @@ __device__ __forceinline__ bf16x8 lds_frag(const __bf16* base, int r, int c) {
   return *reinterpret_cast<const bf16x8*>(base + chunk_offset(r, c));
 }
 
-// hi = bf16(v); lo = bf16(v - hi) (only with three terms).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef unsigned uintx2 __attribute__((ext_vector_type(2)));
+
+// hi = bf16(v); lo = bf16(v - hi) (only with three terms).  Pairs go
+// through one v_cvt_pk_bf16_f32 each; the hi values come back to fp32 by a
+// shift / mask of the packed pair.
 template <int kTerms>
 __device__ __forceinline__ void split4(const floatx4& v, bf16x4& hi, bf16x4& lo) {
+  unsigned h[2], l[2] = {0, 0};
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    hi[e] = (__bf16)v[e];
-    if constexpr (kTerms == 3) lo[e] = (__bf16)(v[e] - (float)hi[e]);
+  for (int p = 0; p < 2; ++p) {
+    const float a = v[2 * p], b = v[2 * p + 1];
+    h[p] = __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{a, b}, bf16x2));
+    if constexpr (kTerms == 3) {
+      const float ha = __uint_as_float(h[p] << 16), hb = __uint_as_float(h[p] & 0xffff0000u);
+      l[p] = __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{a - ha, b - hb}, bf16x2));
+    }
   }
+  hi = __builtin_bit_cast(bf16x4, uintx2{h[0], h[1]});
+  if constexpr (kTerms == 3) lo = __builtin_bit_cast(bf16x4, uintx2{l[0], l[1]});
 }
 
 __device__ __forceinline__ floatx16 mfma_bf16(const bf16x8& a, const bf16x8& b, floatx16 c) {

@@ -113,16 +113,18 @@ class PackedLinear:
 
 
 def set_model_precision(model, precision, include=("blocks",)):
-    """GEMM product precision of a flow model's block Linears ("fp32" strict,
-    or the opt-in "bf16" / "bf16x3"); the timestep / input / output Linears
-    stay fp32 unless include also names "io"."""
+    """Product precision of a flow model ("fp32" strict, or the opt-in
+    "bf16" / "bf16x3"): "blocks" in include sets the block Linears, "io" the
+    timestep / input / output Linears, "attention" the SDPA products (Q K^T
+    and P V); what include does not name stays fp32."""
     precision_id(precision)
     for blk in model.blocks:
         for lin in blk.lin.values():
-            lin.precision = precision
+            lin.precision = precision if "blocks" in include else "fp32"
     for lin in (model.t_fc1, model.t_fc2, model.adaln, model.input_layer, model.out_layer):
         lin.precision = precision if "io" in include else "fp32"
-    model.precision = precision
+    model.precision = precision if "blocks" in include else "fp32"
+    model.attention_precision = precision if "attention" in include else "fp32"
     return model
 
 
@@ -194,6 +196,7 @@ class FlowModel:
         self._freqs = {}
         self.sampler = NativeSamplerBackend()
         self.precision = "fp32"
+        self.attention_precision = "fp32"
 
     def set_precision(self, precision, include=("blocks",)):
         return set_model_precision(self, precision, include)
@@ -230,7 +233,7 @@ class FlowModel:
         h = bo.layer_norm(x, cfg.ln_eps, scale=scale_msa, shift=shift_msa)
         q, k, v = lin["qkv"].qkv_direct(h.view(B * L, C), self.freqs(L), blk.q_gamma, blk.k_gamma,
                                         B, L, H, kv_layout="bhld")
-        a = native_sdpa_f32_ex(q, k, v, out_layout="blhd")
+        a = native_sdpa_f32_ex(q, k, v, out_layout="blhd", precision=self.attention_precision)
         lin["out"].epilogue(a.view(B * L, C), bo.EPILOGUE_GATED, out=x2, gate=gate_msa)
 
         # cross attention to the condition tokens (no RoPE)
@@ -239,7 +242,7 @@ class FlowModel:
         kv = lin["xkv"](cond.reshape(B * Lc, C))  # [B*Lc, 2C] = [k | v]
         xk = bo.head_rmsnorm(kv, blk.xk_gamma, B, Lc, H, token_stride=2 * C)
         xv = bo.head_rmsnorm(kv[:, C:], None, B, Lc, H, token_stride=2 * C, normalize=False)
-        a = native_sdpa_f32_ex(xq, xk, xv, out_layout="blhd")
+        a = native_sdpa_f32_ex(xq, xk, xv, out_layout="blhd", precision=self.attention_precision)
         lin["xout"].epilogue(a.view(B * L, C), bo.EPILOGUE_ADD, out=x2)
 
         # MLP: LN + modulate, fc1 with GELU, fc2 with the gated residual

@@ -86,6 +86,7 @@ class JointFlowModel:
         self.sampler = NativeSamplerBackend()
         self._freqs, self._sel, self._bias = {}, {}, {}
         self.precision = "fp32"
+        self.attention_precision = "fp32"
 
     def set_precision(self, precision, include=("blocks",)):
         return set_model_precision(self, precision, include)
@@ -132,7 +133,8 @@ class JointFlowModel:
         h = bo.layer_norm(x, cfg.ln_eps, scale=cm, shift=sm)
         q, k, v = lin["qkv"].qkv_direct(h.view(Ltot, C), self.freqs(L, Ltot - L), blk.q_gamma,
                                         blk.k_gamma, 1, Ltot, H, kv_layout="bhld")
-        a = native_sdpa_f32_ex(q, k, v, key_bias=key_bias, out_layout="blhd")
+        a = native_sdpa_f32_ex(q, k, v, key_bias=key_bias, out_layout="blhd",
+                               precision=self.attention_precision)
         x2 = x.view(Ltot, C)
         lin["out"].epilogue(a.view(Ltot, C), bo.EPILOGUE_GATED, out=x2, gate=gm)
         h = bo.layer_norm(x, cfg.ln_eps, scale=c2, shift=s2)
@@ -154,7 +156,7 @@ class JointFlowModel:
         qo, pk, pv = q_kv_selected_rope_rmsnorm_pack(q, kv, self.freqs(L, Ltot - L), self.selected(L),
                                                      blk.q_gamma, blk.k_gamma, 1, L, Ltot, H)
         a = native_sdpa_f32_ex(qo, pk, pv, kv_packed=True, key_count=Ltot, key_bias=key_bias,
-                               out_layout="blhd")
+                               out_layout="blhd", precision=self.attention_precision)
         x_lat = x[:, :L].contiguous()
         x2 = x_lat.view(L, C)
         blk.lin["out"].epilogue(a.view(L, C), bo.EPILOGUE_GATED, out=x2, gate=gm)
