@@ -210,3 +210,13 @@ def test_kv_bf16_round_mode_switch(lib):
     finally:
         assert lib.tsplat_set_qkv_bf16_round(0) == 0
     assert kv_bf16_round() is None
+
+
+def test_sdpa_layout_validation(lib):
+    """kv_packed other than 0 / 1, or a packed stride short of Lk / not a
+    multiple of 16, is -2 before any pointer is examined."""
+    P = [0x1000 + 16 * i for i in range(5)]
+    s = lib.tsplat_sdpa_precision_async
+    assert s(*P, 1, 2, 16, 20, 64, 0, 0, 0, 2, 32, 0, 0, None) == -2
+    assert s(*P, 1, 2, 16, 20, 64, 0, 0, 0, 1, 16, 0, 0, None) == -2
+    assert s(*P, 1, 2, 16, 20, 64, 0, 0, 0, 1, 24, 0, 0, None) == -2

@@ -186,3 +186,42 @@ def test_bf16_sdpa_config1_vs_strict(oracle, cuda):
     print("relative RMSE vs strict fp32:", rel, flush=True)
     assert rel["bf16x3"] < 2.0 ** -15, rel
     assert rel["bf16"] < 2.0 ** -6, rel
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16", "bf16x3"])
+@pytest.mark.parametrize("B,H,Lq,Lk,bias", [(1, 2, 70, 77, "shared"), (1, 16, 8192 + 512, 8193, None),
+                                            (2, 3, 40, 300, "per_head")])
+def test_packed_kv_layout_matches(cuda, precision, B, H, Lq, Lk, bias):
+    """Key-contiguous k/v [B,H,64,Lkp] stage the same values into the same
+    LDS positions as [B,H,Lk,64] k/v, so each query row sees the same
+    operations: bit-identical output in every precision (small grid, wide
+    grid with a key-split tail).  The packed bf16x3 wide grid runs 256-query
+    workgroups where [B,H,Lk,64] runs 512, so there the rows of the last
+    head's key-split tail (queries 512.., merged by the combine kernel over
+    a different key partition) agree to rounding and all others bitwise."""
+    import torch
+    from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
+
+    print(f"packed layout {precision} B={B} H={H} Lq={Lq} Lk={Lk}", flush=True)
+    q, k, v = _inputs(Lq + 7 * Lk, B, H, Lq, Lk)
+    b = _bias(bias, H, Lk, 5)
+    kw = {}
+    if b is not None:
+        kw["key_bias_per_head" if bias == "per_head" else "key_bias"] = torch.from_numpy(b).to(cuda)
+    qd, kd, vd = (torch.from_numpy(a).to(cuda) for a in (q, k, v))
+    Lkp = (Lk + 15) // 16 * 16 + 16
+    vp = torch.zeros((B, H, 64, Lkp), device=cuda)
+    vp[..., :Lk] = vd.transpose(2, 3)
+    kp = torch.zeros_like(vp)
+    kp[..., :Lk] = kd.transpose(2, 3)
+    rows = native_sdpa_f32_ex(qd, kd, vd, precision=precision, **kw)
+    packed = native_sdpa_f32_ex(qd, kp, vp, kv_packed=True, key_count=Lk, precision=precision, **kw)
+    torch.cuda.synchronize(cuda)
+    assert bool(torch.isfinite(rows).all())
+    if precision == "bf16x3" and B * H * ((Lq + 511) // 512) >= 256:
+        assert torch.equal(packed[:, :-1], rows[:, :-1])
+        assert torch.equal(packed[:, -1, :512], rows[:, -1, :512])
+        tail = (packed[:, -1, 512:] - rows[:, -1, 512:]).abs().max().item()
+        assert tail <= 1e-5 * float(vd.abs().max()), tail
+    else:
+        assert torch.equal(packed, rows)

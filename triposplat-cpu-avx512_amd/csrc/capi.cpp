@@ -102,6 +102,7 @@ int sdpa_checked(const float* q, const float* k, const float* v, const float* bi
   if (B <= 0 || H <= 0 || Lq <= 0 || Lk <= 0 || D != kHeadDim) return kErrDims;
   if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
     return kErrDims;
+  if (kv_packed != 0 && kv_packed != 1) return kErrDims;
   if (kv_packed && (Lkp < Lk || (Lkp & 15) != 0)) return kErrDims;
   if (has_bias && (bias == nullptr || bias_len != Lk)) return kErrRange;
   if (has_bias && bias_head_stride != 0 && bias_head_stride < Lk) return kErrRange;

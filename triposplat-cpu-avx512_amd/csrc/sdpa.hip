@@ -32,26 +32,30 @@ namespace tsplat {
 namespace sdpa {
 namespace {
 
-// kPacked: k/v are [B, H, 64, Lkp] (key-contiguous rows per dimension), as
-// the reference's packed kernel takes them; otherwise [B, H, Lk, 64].
+// kLayout: 0 = k and v [B, H, Lk, 64]; 1 = both key-contiguous [B, H, 64,
+// Lkp] (as the reference's packed kernel takes them).  Each operand keeps
+// its orientation in LDS.
 // kWaves waves of 32 queries each share every K/V tile of kBKV keys.
 // kSplit: run scores -> softmax -> PV per 32-key block of the tile (16 score
 // registers live instead of kBKV/2), for configurations short of registers.
-template <bool kPacked, bool kBias, int kWaves, int kBKV, bool kSplit>
+template <int kLayout, bool kBias, int kWaves, int kBKV, bool kSplit>
 __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
   constexpr int kThreads = kWaves * 64;
   constexpr int kBQ = kWaves * 32;
   constexpr int kNKB = kBKV / 32;              // 32-key blocks per tile
-  // LDS: unpacked K [key][64 + 4], V [key][64]; packed K and V [d][kBKV + 4].
-  constexpr int kKRows = kPacked ? kD : kBKV;
-  constexpr int kKS = kPacked ? kBKV + 4 : kD + 4;
-  constexpr int kVS = kPacked ? kBKV + 4 : kD;
-  constexpr int kRowUnits = kPacked ? kBKV / 4 : kD / 4;  // float4 per LDS row
-  constexpr int kLoads = kKRows * kRowUnits / kThreads;   // float4 of K (and of V) per thread
-  static_assert(kLoads * kThreads == kKRows * kRowUnits, "tile split");
+  constexpr bool kKP = kLayout == 1;           // k key-contiguous
+  constexpr bool kVP = kLayout != 0;           // v key-contiguous
+  // LDS: K [key][64 + 4] or [d][kBKV + 4]; V [key][64] or [d][kBKV + 4].
+  constexpr int kKS = kKP ? kBKV + 4 : kD + 4;
+  constexpr int kVS = kVP ? kBKV + 4 : kD;
+  constexpr int kKRowUnits = kKP ? kBKV / 4 : kD / 4;  // float4 per LDS row
+  constexpr int kVRowUnits = kVP ? kBKV / 4 : kD / 4;
+  constexpr int kUnits = kBKV * kD / 4;
+  constexpr int kLoads = kUnits / kThreads;    // float4 of K (and of V) per thread
+  static_assert(kLoads * kThreads == kUnits, "tile split");
   static_assert(kThreads >= kBKV, "bias row load");
-  __shared__ __attribute__((aligned(16))) float kbuf[2][kKRows * kKS];
-  __shared__ __attribute__((aligned(16))) float vbuf[2][kKRows * kVS];
+  __shared__ __attribute__((aligned(16))) float kbuf[2][(kKP ? kD : kBKV) * kKS];
+  __shared__ __attribute__((aligned(16))) float vbuf[2][(kVP ? kD : kBKV) * kVS];
   __shared__ __attribute__((aligned(16))) float bbuf[2][kBKV];
 
   const int tid = threadIdx.x;
@@ -85,8 +89,8 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
     }
   }
 
-  const float* kbase = a.k + (int64_t)bh * (kPacked ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
-  const float* vbase = a.v + (int64_t)bh * (kPacked ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
+  const float* kbase = a.k + (int64_t)bh * (kKP ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
+  const float* vbase = a.v + (int64_t)bh * (kVP ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
   const float* brow = kBias ? a.bias + (int64_t)h * a.bias_head_stride : nullptr;
 
   floatx4 kr[kLoads], vr[kLoads];
@@ -95,26 +99,8 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
       const int idx = tid + j * kThreads;
-      const int row = idx / kRowUnits;
-      const int c = idx % kRowUnits;
-      if (!kPacked) {
-        const int key = key0 + row;
-        const bool ok = key < a.Lk;
-        const int64_t off = (int64_t)(ok ? key : 0) * kD + 4 * c;
-        kr[j] = ok ? *reinterpret_cast<const floatx4*>(kbase + off) : floatx4{0, 0, 0, 0};
-        vr[j] = ok ? *reinterpret_cast<const floatx4*>(vbase + off) : floatx4{0, 0, 0, 0};
-      } else {
-        const int key = key0 + 4 * c;  // row = dimension
-        const bool ok = key < a.Lk;
-        const int64_t off = (int64_t)row * a.Lkp + (ok ? key : 0);
-        floatx4 kk = ok ? *reinterpret_cast<const floatx4*>(kbase + off) : floatx4{0, 0, 0, 0};
-        floatx4 vv = ok ? *reinterpret_cast<const floatx4*>(vbase + off) : floatx4{0, 0, 0, 0};
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (key + e >= a.Lk) { kk[e] = 0.0f; vv[e] = 0.0f; }
-        kr[j] = kk;
-        vr[j] = vv;
-      }
+      kr[j] = fetch_unit<kKP, kBKV>(a, kbase, idx, key0);
+      vr[j] = fetch_unit<kVP, kBKV>(a, vbase, idx, key0);
     }
     if (kBias && tid < kBKV) {
       const int key = key0 + tid;
@@ -125,10 +111,8 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
       const int idx = tid + j * kThreads;
-      const int row = idx / kRowUnits;
-      const int c = idx % kRowUnits;
-      *reinterpret_cast<floatx4*>(&kbuf[buf][row * kKS + 4 * c]) = kr[j];
-      *reinterpret_cast<floatx4*>(&vbuf[buf][row * kVS + 4 * c]) = vr[j];
+      *reinterpret_cast<floatx4*>(&kbuf[buf][(idx / kKRowUnits) * kKS + 4 * (idx % kKRowUnits)]) = kr[j];
+      *reinterpret_cast<floatx4*>(&vbuf[buf][(idx / kVRowUnits) * kVS + 4 * (idx % kVRowUnits)]) = vr[j];
     }
     if (kBias && tid < kBKV) bbuf[buf][tid] = br;
   };
@@ -171,7 +155,7 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
 #pragma unroll
         for (int i = 0; i < kGB; ++i) {
           const int kb = kb0 + i;
-          if (!kPacked) {
+          if (!kKP) {
             kf[i] = *reinterpret_cast<const floatx4*>(&kb_[(kb * 32 + l32) * kKS + 8 * hh + 4 * g]);
           } else {
 #pragma unroll
@@ -245,7 +229,7 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
           floatx4 vf[2];
 #pragma unroll
           for (int db = 0; db < 2; ++db) {
-            if (!kPacked) {
+            if (!kVP) {
 #pragma unroll
               for (int e = 0; e < 4; ++e)
                 vf[db][e] = vb_[(kb * 32 + 8 * hh + 4 * g + e) * kVS + db * 32 + l32];
@@ -269,18 +253,19 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
   store_rows<kBQ>(a, o, m_run, l_run, part, b, h, bh, wave, qrow, g, l32);
 }
 
+template <int kLayout, int kWaves, int kBKV, bool kSplit>
+void launch_kernel(dim3 grid, hipStream_t stream, const SdpaArgs& a, bool bias) {
+  const dim3 block(kWaves * 64);
+  if (bias) hipLaunchKernelGGL((sdpa_kernel<kLayout, true, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((sdpa_kernel<kLayout, false, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
+}
+
 template <int kWaves, int kBKV, bool kSplit>
 int launch_shape(const SdpaParams& p, hipStream_t stream, int cus = 0) {
-  const bool packed = p.kv_packed != 0, bias = p.bias != nullptr;
+  const bool bias = p.bias != nullptr;
   return launch_tiles(make_args(p), p, kWaves * 32, kBKV, cus, stream, [&](dim3 grid, const SdpaArgs& a) {
-    const dim3 block(kWaves * 64);
-    if (packed) {
-      if (bias) hipLaunchKernelGGL((sdpa_kernel<true, true, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
-      else hipLaunchKernelGGL((sdpa_kernel<true, false, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
-    } else {
-      if (bias) hipLaunchKernelGGL((sdpa_kernel<false, true, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
-      else hipLaunchKernelGGL((sdpa_kernel<false, false, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
-    }
+    if (p.kv_packed) launch_kernel<1, kWaves, kBKV, kSplit>(grid, stream, a, bias);
+    else launch_kernel<0, kWaves, kBKV, kSplit>(grid, stream, a, bias);
   });
 }
 

@@ -83,10 +83,12 @@ __device__ __forceinline__ void split8(const floatx16& s, int c, bf16x8& hi, bf1
   if constexpr (kLo) lo = __builtin_bit_cast(bf16x8, uintx4{l[0], l[1], l[2], l[3]});
 }
 
-// kPacked: k/v [B, H, 64, Lkp]; otherwise [B, H, Lk, 64].  kWaves waves of
-// 32 queries share each K/V tile of kBKV keys; kGB 32-key blocks per softmax
-// step (1 keeps 16 score registers live).  kTerms: 1 (bf16) or 3 (bf16x3).
-template <bool kPacked, bool kBias, int kWaves, int kBKV, int kGB, int kTerms>
+// kLayout: 0 = k and v [B, H, Lk, 64] (v is transposed on its way into
+// LDS); 1 = both key-contiguous [B, H, 64, Lkp] (k is transposed).  kWaves
+// waves of 32 queries share each K/V tile of kBKV keys; kGB 32-key blocks
+// per softmax step (1 keeps 16 score registers live).  kTerms: 1 (bf16) or
+// 3 (bf16x3).
+template <int kLayout, bool kBias, int kWaves, int kBKV, int kGB, int kTerms>
 __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
   constexpr int kThreads = kWaves * 64;
   constexpr int kBQ = kWaves * 32;
@@ -141,39 +143,20 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
       }
   }
 
-  const float* kbase = a.k + (int64_t)bh * (kPacked ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
-  const float* vbase = a.v + (int64_t)bh * (kPacked ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
+  constexpr bool kKP = kLayout == 1;  // k key-contiguous
+  constexpr bool kVP = kLayout != 0;  // v key-contiguous
+  const float* kbase = a.k + (int64_t)bh * (kKP ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
+  const float* vbase = a.v + (int64_t)bh * (kVP ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
   const float* brow = kBias ? a.bias + (int64_t)h * a.bias_head_stride : nullptr;
 
-  // Unpacked: unit = 4 dims (4c..4c+3) of one key (row); packed: 4 keys
-  // (4c..4c+3) of one dim (row).  Keys past Lk load as zeros.
-  constexpr int kRowUnits = kPacked ? kBKV / 4 : kD / 4;
   floatx4 kr[kLoads], vr[kLoads];
   float br = 0.0f;
   auto load = [&](int key0) {
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
       const int idx = tid + j * kThreads;
-      const int row = idx / kRowUnits;
-      const int c = idx % kRowUnits;
-      if (!kPacked) {
-        const int key = key0 + row;
-        const bool ok = key < a.Lk;
-        const int64_t off = (int64_t)(ok ? key : 0) * kD + 4 * c;
-        kr[j] = ok ? *reinterpret_cast<const floatx4*>(kbase + off) : floatx4{0, 0, 0, 0};
-        vr[j] = ok ? *reinterpret_cast<const floatx4*>(vbase + off) : floatx4{0, 0, 0, 0};
-      } else {
-        const int key = key0 + 4 * c;
-        const bool ok = key < a.Lk;
-        const int64_t off = (int64_t)row * a.Lkp + (ok ? key : 0);
-        floatx4 kk = ok ? *reinterpret_cast<const floatx4*>(kbase + off) : floatx4{0, 0, 0, 0};
-        floatx4 vv = ok ? *reinterpret_cast<const floatx4*>(vbase + off) : floatx4{0, 0, 0, 0};
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (key + e >= a.Lk) { kk[e] = 0.0f; vv[e] = 0.0f; }
-        kr[j] = kk;
-        vr[j] = vv;
-      }
+      kr[j] = fetch_unit<kKP, kBKV>(a, kbase, idx, key0);
+      vr[j] = fetch_unit<kVP, kBKV>(a, vbase, idx, key0);
     }
     if (kBias && tid < kBKV) {
       const int key = key0 + tid;
@@ -184,26 +167,31 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
       const int idx = tid + j * kThreads;
-      const int row = idx / kRowUnits;
-      const int c = idx % kRowUnits;
       bf16x4 kh, kl, vh, vl;
       split4<kLo>(kr[j], kh, kl);
       split4<kLo>(vr[j], vh, vl);
-      if (!kPacked) {  // row = key, dims 4c..4c+3
+      if constexpr (!kKP) {  // key row, dims 4c..4c+3: one 8-byte store per plane
+        const int row = idx / (kD / 4), c = idx % (kD / 4);
         *reinterpret_cast<bf16x4*>(&khi[buf][row * kKS + 4 * c]) = kh;
         if constexpr (kLo) *reinterpret_cast<bf16x4*>(&klo[buf][row * kKS + 4 * c]) = kl;
+      } else {  // dim row, keys 4c..4c+3: transposed element by element
+        const int row = idx / (kBKV / 4), c = idx % (kBKV / 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          khi[buf][(4 * c + e) * kKS + row] = kh[e];
+          if constexpr (kLo) klo[buf][(4 * c + e) * kKS + row] = kl[e];
+        }
+      }
+      if constexpr (!kVP) {  // key row, dims 4c..4c+3: transposed element by element
+        const int row = idx / (kD / 4), c = idx % (kD / 4);
         const int p = vt_pos(row);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           vhi[buf][(4 * c + e) * kVS + p] = vh[e];
           if constexpr (kLo) vlo[buf][(4 * c + e) * kVS + p] = vl[e];
         }
-      } else {  // row = dim, keys 4c..4c+3 (contiguous in V^T: vt_pos keeps bits 0-1)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          khi[buf][(4 * c + e) * kKS + row] = kh[e];
-          if constexpr (kLo) klo[buf][(4 * c + e) * kKS + row] = kl[e];
-        }
+      } else {  // dim row, keys 4c..4c+3 (contiguous in V^T: vt_pos keeps bits 0-1)
+        const int row = idx / (kBKV / 4), c = idx % (kBKV / 4);
         *reinterpret_cast<bf16x4*>(&vhi[buf][row * kVS + vt_pos(4 * c)]) = vh;
         if constexpr (kLo) *reinterpret_cast<bf16x4*>(&vlo[buf][row * kVS + vt_pos(4 * c)]) = vl;
       }
@@ -329,23 +317,25 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
   store_rows<kBQ>(a, o, m_run, l_run, w.part, b, h, bh, wave, qrow, g, l32);
 }
 
+template <int kLayout, int kWaves, int kBKV, int kGB>
+void launch_kernel(dim3 grid, hipStream_t stream, const SdpaArgs& a, bool bias, bool three) {
+  const dim3 block(kWaves * 64);
+  if (bias) {
+    if (three) hipLaunchKernelGGL((sdpa_bf16_kernel<kLayout, true, kWaves, kBKV, kGB, 3>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((sdpa_bf16_kernel<kLayout, true, kWaves, kBKV, kGB, 1>), grid, block, 0, stream, a);
+  } else {
+    if (three) hipLaunchKernelGGL((sdpa_bf16_kernel<kLayout, false, kWaves, kBKV, kGB, 3>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((sdpa_bf16_kernel<kLayout, false, kWaves, kBKV, kGB, 1>), grid, block, 0, stream, a);
+  }
+}
+
 template <int kWaves, int kBKV, int kGB>
 int launch_shape(const SdpaParams& p, hipStream_t stream, int cus) {
-  const bool packed = p.kv_packed != 0, bias = p.bias != nullptr;
+  const bool bias = p.bias != nullptr;
   const bool three = p.precision == kPrecisionBf16x3;
   return launch_tiles(make_args(p), p, kWaves * 32, kBKV, cus, stream, [&](dim3 grid, const SdpaArgs& a) {
-    const dim3 block(kWaves * 64);
-#define TSPLAT_SDPA_BF16_LAUNCH(PK, BI)                                                             \
-  if (three)                                                                                        \
-    hipLaunchKernelGGL((sdpa_bf16_kernel<PK, BI, kWaves, kBKV, kGB, 3>), grid, block, 0, stream, a); \
-  else                                                                                              \
-    hipLaunchKernelGGL((sdpa_bf16_kernel<PK, BI, kWaves, kBKV, kGB, 1>), grid, block, 0, stream, a);
-    if (packed) {
-      if (bias) { TSPLAT_SDPA_BF16_LAUNCH(true, true) } else { TSPLAT_SDPA_BF16_LAUNCH(true, false) }
-    } else {
-      if (bias) { TSPLAT_SDPA_BF16_LAUNCH(false, true) } else { TSPLAT_SDPA_BF16_LAUNCH(false, false) }
-    }
-#undef TSPLAT_SDPA_BF16_LAUNCH
+    if (p.kv_packed) launch_kernel<1, kWaves, kBKV, kGB>(grid, stream, a, bias, three);
+    else launch_kernel<0, kWaves, kBKV, kGB>(grid, stream, a, bias, three);
   });
 }
 
@@ -358,6 +348,9 @@ int launch_sdpa_bf16(const SdpaParams& p, hipStream_t stream) {
   const int cus = device_cus();
   const int64_t wide_tiles = (int64_t)p.B * p.H * ((p.Lq + 511) / 512);
   if (wide_tiles < cus) return launch_shape<4, 64, 1>(p, stream, 0);
+  // bf16x3 with packed k/v spills 168-192 bytes per lane at 16 waves
+  // (6.0 ms at configs[1]); 8 waves have no spills (3.5 ms).
+  if (p.kv_packed && p.precision == kPrecisionBf16x3) return launch_shape<8, 64, 1>(p, stream, cus);
   return launch_shape<16, 64, 1>(p, stream, cus);
 }
 

@@ -19,7 +19,7 @@ struct SdpaArgs {
   const float* v;
   const float* bias;
   float* out;
-  int B, H, Lq, Lk, Lkp;
+  int B, H, Lq, Lk, Lkp;  // Lkp: key stride of a key-contiguous operand
   int64_t bias_head_stride;
   int out_blhd;
   // Tail split: workgroups [0, full_tiles) each own one query tile over all
@@ -48,6 +48,31 @@ __device__ __forceinline__ float pair_max(float x) {
 __device__ __forceinline__ float pair_sum(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// One float4 staging unit of a K or V tile (keys key0 .. key0 + kBKV - 1)
+// of one (b, h), base pointing at that (b, h).  [Lk, 64] operand (kPacked
+// false): unit idx = dims 4c..4c+3 of key row; key-contiguous [64, Lkp]
+// operand: keys 4c..4c+3 of dim row.  Keys past Lk read as zeros.
+template <bool kPacked, int kBKV>
+__device__ __forceinline__ floatx4 fetch_unit(const SdpaArgs& a, const float* base, int idx, int key0) {
+  if constexpr (!kPacked) {
+    const int row = idx / (kD / 4), c = idx % (kD / 4);
+    const int key = key0 + row;
+    const bool ok = key < a.Lk;
+    const int64_t off = (int64_t)(ok ? key : 0) * kD + 4 * c;
+    return ok ? *reinterpret_cast<const floatx4*>(base + off) : floatx4{0, 0, 0, 0};
+  } else {
+    const int row = idx / (kBKV / 4), c = idx % (kBKV / 4);
+    const int key = key0 + 4 * c;
+    const bool ok = key < a.Lk;
+    const int64_t off = (int64_t)row * a.Lkp + (ok ? key : 0);
+    floatx4 x = ok ? *reinterpret_cast<const floatx4*>(base + off) : floatx4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (key + e >= a.Lk) x[e] = 0.0f;
+    return x;
+  }
 }
 
 // Query tile and key range of this workgroup (see SdpaArgs).
