@@ -78,3 +78,31 @@ def test_reduced_step_matches_cpu_full_computation(oracle, cuda):
     print({"latent_rmse": latent_rmse, "velocity_rel_rmse": v_rel})
     assert np.all(np.isfinite(zn_d))
     assert latent_rmse <= 1e-4 and v_rel <= 1e-4
+
+
+def test_reduced_step_opt_in_bf16x3_attention(oracle, cuda):
+    """The single-stream graph with bf16x3 products in its block Linears and
+    in every SDPA (key-bias self attention, the packed selected-rows final
+    block) stays within the latent gate against the CPU fp32 full
+    computation, differs from the strict step, and the strict step is
+    restored bit for bit afterwards."""
+    import torch
+    from flow_ref import CpuJointFlow, combined_rmse
+
+    cfg, model = _model(cuda, hidden=128, heads=2, blocks=2, L=150, Lc=48)
+    z, c = _inputs(cfg)
+    zd, cd = torch.from_numpy(z).to(cuda), torch.from_numpy(c).to(cuda)
+    strict, _ = model.euler_cfg_step(zd, cd, reduce_work=True)
+    model.set_precision("bf16x3", include=("blocks", "attention"))
+    assert model.attention_precision == "bf16x3"
+    zn3, v3 = model.euler_cfg_step(zd, cd, reduce_work=True)
+    model.set_precision("fp32")
+    again, _ = model.euler_cfg_step(zd, cd, reduce_work=True)
+    torch.cuda.synchronize(cuda)
+    assert torch.equal(again, strict)
+    assert not torch.equal(zn3, strict)
+    zn_c, v_c = CpuJointFlow(model.host(), cfg, backend="oracle").joint_euler_cfg_step(z, c)
+    latent_rmse = combined_rmse(zn3.cpu().numpy(), zn_c)
+    print({"bf16x3_latent_rmse": latent_rmse})
+    assert np.all(np.isfinite(zn3.cpu().numpy()))
+    assert latent_rmse <= 1e-4
