@@ -66,11 +66,10 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
 
   const int qblocks = (a.Lq + kBQ - 1) / kBQ;
   const TileWork w = tile_work(a);
-  const int tile = w.tile, part = w.part, k_begin = w.k_begin, k_end = w.k_end;
+  const int tile = w.tile, k_begin = w.k_begin, k_end = w.k_end;
   const int bh = tile / qblocks;
   const int qb = tile % qblocks;
   const int h = bh % a.H;
-  const int b = bh / a.H;
   const int qrow = qb * kBQ + wave * 32 + l32;
   const bool q_ok = qrow < a.Lq;
 
@@ -99,8 +98,12 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
       const int idx = tid + j * kThreads;
-      kr[j] = fetch_unit<kKP, kBKV>(a, kbase, idx, key0);
-      vr[j] = fetch_unit<kVP, kBKV>(a, vbase, idx, key0);
+      if constexpr (!kKP && !kVP) {
+        fetch_units_kv<kBKV>(a, kbase, vbase, idx, key0, kr[j], vr[j]);
+      } else {
+        kr[j] = fetch_unit<kKP, kBKV>(a, kbase, idx, key0);
+        vr[j] = fetch_unit<kVP, kBKV>(a, vbase, idx, key0);
+      }
     }
     if (kBias && tid < kBKV) {
       const int key = key0 + tid;
@@ -249,8 +252,7 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
     __syncthreads();
   }
 
-  if (!q_ok) return;  // lanes l and l ^ 32 share the query: both leave or neither
-  store_rows<kBQ>(a, o, m_run, l_run, part, b, h, bh, wave, qrow, g, l32);
+  store_rows<kBQ>(a, o, m_run, l_run);
 }
 
 template <int kLayout, int kWaves, int kBKV, bool kSplit>

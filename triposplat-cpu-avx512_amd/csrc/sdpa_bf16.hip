@@ -118,7 +118,6 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
   const int bh = w.tile / qblocks;
   const int qb = w.tile % qblocks;
   const int h = bh % a.H;
-  const int b = bh / a.H;
   const int qrow = qb * kBQ + wave * 32 + l32;
   const bool q_ok = qrow < a.Lq;
 
@@ -155,8 +154,12 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
       const int idx = tid + j * kThreads;
-      kr[j] = fetch_unit<kKP, kBKV>(a, kbase, idx, key0);
-      vr[j] = fetch_unit<kVP, kBKV>(a, vbase, idx, key0);
+      if constexpr (!kKP && !kVP) {
+        fetch_units_kv<kBKV>(a, kbase, vbase, idx, key0, kr[j], vr[j]);
+      } else {
+        kr[j] = fetch_unit<kKP, kBKV>(a, kbase, idx, key0);
+        vr[j] = fetch_unit<kVP, kBKV>(a, vbase, idx, key0);
+      }
     }
     if (kBias && tid < kBKV) {
       const int key = key0 + tid;
@@ -313,8 +316,7 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
     __syncthreads();
   }
 
-  if (!q_ok) return;  // lanes l and l ^ 32 share the query: both leave or neither
-  store_rows<kBQ>(a, o, m_run, l_run, w.part, b, h, bh, wave, qrow, g, l32);
+  store_rows<kBQ>(a, o, m_run, l_run);
 }
 
 template <int kLayout, int kWaves, int kBKV, int kGB>

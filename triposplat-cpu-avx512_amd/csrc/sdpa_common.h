@@ -75,6 +75,18 @@ __device__ __forceinline__ floatx4 fetch_unit(const SdpaArgs& a, const float* ba
   }
 }
 
+// Both [Lk, 64] operands' unit idx at once (one shared offset).
+template <int kBKV>
+__device__ __forceinline__ void fetch_units_kv(const SdpaArgs& a, const float* kbase, const float* vbase,
+                                               int idx, int key0, floatx4& kx, floatx4& vx) {
+  const int row = idx / (kD / 4), c = idx % (kD / 4);
+  const int key = key0 + row;
+  const bool ok = key < a.Lk;
+  const int64_t off = (int64_t)(ok ? key : 0) * kD + 4 * c;
+  kx = ok ? *reinterpret_cast<const floatx4*>(kbase + off) : floatx4{0, 0, 0, 0};
+  vx = ok ? *reinterpret_cast<const floatx4*>(vbase + off) : floatx4{0, 0, 0, 0};
+}
+
 // Query tile and key range of this workgroup (see SdpaArgs).
 struct TileWork {
   int tile, part, k_begin, k_end;
@@ -95,11 +107,18 @@ __device__ __forceinline__ TileWork tile_work(const SdpaArgs& a) {
 // Final store of a wave's 32 queries: o[db][r] holds O^T[db*32 + 8*(r/4) +
 // 4*g + r%4][query] (the 32x32 MFMA accumulator layout), m_run / l_run the
 // lane's running max and partial sum.  Split parts write the unnormalised
-// rows and (max, sum) for the combine kernel.
+// rows and (max, sum) for the combine kernel.  The tile indices are
+// recomputed here from the launch state rather than kept live across the
+// key loop (fewer registers held through it).
 template <int kBQ>
 __device__ __forceinline__ void store_rows(const SdpaArgs& a, const floatx16 (&o)[2], float m_run,
-                                           float l_run, int part, int b, int h, int bh, int wave,
-                                           int qrow, int g, int l32) {
+                                           float l_run) {
+  const TileWork w = tile_work(a);
+  const int qblocks = (a.Lq + kBQ - 1) / kBQ;
+  const int bh = w.tile / qblocks, b = bh / a.H, h = bh % a.H, part = w.part;
+  const int wave = threadIdx.x >> 6, g = (threadIdx.x >> 5) & 1, l32 = threadIdx.x & 31;
+  const int qrow = (w.tile % qblocks) * kBQ + wave * 32 + l32;
+  if (qrow >= a.Lq) return;  // lanes l and l ^ 32 share the query: both leave or neither
   const float lsum = pair_sum(l_run);
   if (part >= 0) {
     const int64_t row = (int64_t)part * kBQ + wave * 32 + l32;
