@@ -255,20 +255,24 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
   store_rows<kBQ>(a, o, m_run, l_run);
 }
 
-template <int kLayout, int kWaves, int kBKV, bool kSplit>
-void launch_kernel(dim3 grid, hipStream_t stream, const SdpaArgs& a, bool bias) {
-  const dim3 block(kWaves * 64);
-  if (bias) hipLaunchKernelGGL((sdpa_kernel<kLayout, true, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((sdpa_kernel<kLayout, false, kWaves, kBKV, kSplit>), grid, block, 0, stream, a);
+template <int kLayout, bool kBias, int kWaves, int kBKV, bool kSplit>
+int launch_shape(const SdpaParams& p, hipStream_t stream, int cus) {
+  return launch_tiles(make_args(p), p, kWaves * 32, kBKV, cus, stream, [&](dim3 grid, const SdpaArgs& a) {
+    hipLaunchKernelGGL((sdpa_kernel<kLayout, kBias, kWaves, kBKV, kSplit>), grid, dim3(kWaves * 64), 0,
+                       stream, a);
+  });
 }
 
-template <int kWaves, int kBKV, bool kSplit>
-int launch_shape(const SdpaParams& p, hipStream_t stream, int cus = 0) {
-  const bool bias = p.bias != nullptr;
-  return launch_tiles(make_args(p), p, kWaves * 32, kBKV, cus, stream, [&](dim3 grid, const SdpaArgs& a) {
-    if (p.kv_packed) launch_kernel<1, kWaves, kBKV, kSplit>(grid, stream, a, bias);
-    else launch_kernel<0, kWaves, kBKV, kSplit>(grid, stream, a, bias);
-  });
+// Grids too small to give every CU one 512-query workgroup use 4 waves;
+// larger grids whose tile count is not a multiple of the CU count split the
+// remainder's keys (launch_tiles).  A key bias runs the per-32-key-block
+// softmax (kSplit).
+template <int kLayout, bool kBias>
+int launch_sized(const SdpaParams& p, hipStream_t stream) {
+  const int cus = device_cus();
+  const int64_t wide_tiles = (int64_t)p.B * p.H * ((p.Lq + 511) / 512);
+  if (wide_tiles < cus) return launch_shape<kLayout, kBias, 4, 64, false>(p, stream, 0);
+  return launch_shape<kLayout, kBias, 16, 64, kBias>(p, stream, cus);
 }
 
 }  // namespace
@@ -282,17 +286,12 @@ int launch_shape(const SdpaParams& p, hipStream_t stream, int cus = 0) {
 // that arrives key-major for V (or dim-major for K) transposed in LDS, so all
 // fragments are 128-bit reads, costs 2-4 %: the wider fragments push the
 // 16-wave kernels into spills.
-// Grids too small to give every CU one 512-query workgroup use 4 waves;
-// larger grids whose tile count is not a multiple of the CU count split the
-// remainder's keys (launch_shape).
 int launch_sdpa(const SdpaParams& p, hipStream_t stream) {
   using namespace sdpa;
   if (p.precision != kPrecisionFp32) return launch_sdpa_bf16(p, stream);
-  const int cus = device_cus();
-  const int64_t wide_tiles = (int64_t)p.B * p.H * ((p.Lq + 511) / 512);
-  if (wide_tiles < cus) return launch_shape<4, 64, false>(p, stream);
-  if (p.bias != nullptr) return launch_shape<16, 64, true>(p, stream, cus);
-  return launch_shape<16, 64, false>(p, stream, cus);
+  const bool bias = p.bias != nullptr;
+  if (p.kv_packed) return bias ? launch_sized<1, true>(p, stream) : launch_sized<1, false>(p, stream);
+  return bias ? launch_sized<0, true>(p, stream) : launch_sized<0, false>(p, stream);
 }
 
 }  // namespace tsplat

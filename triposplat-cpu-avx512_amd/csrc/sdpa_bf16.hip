@@ -319,26 +319,30 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
   store_rows<kBQ>(a, o, m_run, l_run);
 }
 
-template <int kLayout, int kWaves, int kBKV, int kGB>
-void launch_kernel(dim3 grid, hipStream_t stream, const SdpaArgs& a, bool bias, bool three) {
-  const dim3 block(kWaves * 64);
-  if (bias) {
-    if (three) hipLaunchKernelGGL((sdpa_bf16_kernel<kLayout, true, kWaves, kBKV, kGB, 3>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((sdpa_bf16_kernel<kLayout, true, kWaves, kBKV, kGB, 1>), grid, block, 0, stream, a);
-  } else {
-    if (three) hipLaunchKernelGGL((sdpa_bf16_kernel<kLayout, false, kWaves, kBKV, kGB, 3>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((sdpa_bf16_kernel<kLayout, false, kWaves, kBKV, kGB, 1>), grid, block, 0, stream, a);
-  }
+template <int kLayout, bool kBias, int kTerms, int kWaves>
+int launch_shape(const SdpaParams& p, hipStream_t stream, int cus) {
+  return launch_tiles(make_args(p), p, kWaves * 32, 64, cus, stream, [&](dim3 grid, const SdpaArgs& a) {
+    hipLaunchKernelGGL((sdpa_bf16_kernel<kLayout, kBias, kWaves, 64, 1, kTerms>), grid, dim3(kWaves * 64), 0,
+                       stream, a);
+  });
 }
 
-template <int kWaves, int kBKV, int kGB>
-int launch_shape(const SdpaParams& p, hipStream_t stream, int cus) {
-  const bool bias = p.bias != nullptr;
-  const bool three = p.precision == kPrecisionBf16x3;
-  return launch_tiles(make_args(p), p, kWaves * 32, kBKV, cus, stream, [&](dim3 grid, const SdpaArgs& a) {
-    if (p.kv_packed) launch_kernel<1, kWaves, kBKV, kGB>(grid, stream, a, bias, three);
-    else launch_kernel<0, kWaves, kBKV, kGB>(grid, stream, a, bias, three);
-  });
+// Small grids: 4 waves.  Wide grids: 16 waves, except bf16x3 with packed
+// k/v, which spills 148-160 bytes per lane at 16 waves (6.0 ms at
+// configs[1]) and none at 8 (3.5 ms).
+template <int kLayout, bool kBias, int kTerms>
+int launch_sized(const SdpaParams& p, hipStream_t stream) {
+  const int cus = device_cus();
+  const int64_t wide_tiles = (int64_t)p.B * p.H * ((p.Lq + 511) / 512);
+  if (wide_tiles < cus) return launch_shape<kLayout, kBias, kTerms, 4>(p, stream, 0);
+  constexpr int kWide = (kLayout == 1 && kTerms == 3) ? 8 : 16;
+  return launch_shape<kLayout, kBias, kTerms, kWide>(p, stream, cus);
+}
+
+template <int kLayout, bool kBias>
+int launch_terms(const SdpaParams& p, hipStream_t stream) {
+  return p.precision == kPrecisionBf16x3 ? launch_sized<kLayout, kBias, 3>(p, stream)
+                                         : launch_sized<kLayout, kBias, 1>(p, stream);
 }
 
 }  // namespace
@@ -347,13 +351,9 @@ int launch_shape(const SdpaParams& p, hipStream_t stream, int cus) {
 int launch_sdpa_bf16(const SdpaParams& p, hipStream_t stream) {
   using namespace sdpa;
   if (p.precision != kPrecisionBf16 && p.precision != kPrecisionBf16x3) return kErrDims;
-  const int cus = device_cus();
-  const int64_t wide_tiles = (int64_t)p.B * p.H * ((p.Lq + 511) / 512);
-  if (wide_tiles < cus) return launch_shape<4, 64, 1>(p, stream, 0);
-  // bf16x3 with packed k/v spills 168-192 bytes per lane at 16 waves
-  // (6.0 ms at configs[1]); 8 waves have no spills (3.5 ms).
-  if (p.kv_packed && p.precision == kPrecisionBf16x3) return launch_shape<8, 64, 1>(p, stream, cus);
-  return launch_shape<16, 64, 1>(p, stream, cus);
+  const bool bias = p.bias != nullptr;
+  if (p.kv_packed) return bias ? launch_terms<1, true>(p, stream) : launch_terms<1, false>(p, stream);
+  return bias ? launch_terms<0, true>(p, stream) : launch_terms<0, false>(p, stream);
 }
 
 }  // namespace tsplat
