@@ -220,3 +220,18 @@ def test_sdpa_layout_validation(lib):
     assert s(*P, 1, 2, 16, 20, 64, 0, 0, 0, 2, 32, 0, 0, None) == -2
     assert s(*P, 1, 2, 16, 20, 64, 0, 0, 0, 1, 16, 0, 0, None) == -2
     assert s(*P, 1, 2, 16, 20, 64, 0, 0, 0, 1, 24, 0, 0, None) == -2
+
+
+def test_block_patches_disabled_and_missing_library():
+    """Disabled patches touch nothing; a missing library is reported at
+    patch time, as the reference's patches report theirs."""
+    import torch
+    from tsplat import native_block_patches as P
+
+    for fn in (P.apply_triposplat_native_gelu_avx512_patch, P.apply_triposplat_native_silu_avx512_patch,
+               P.apply_triposplat_native_norm_rope_avx512_patch,
+               P.apply_triposplat_native_block_elementwise_avx512_patch):
+        assert fn(None) == {"enabled": False}
+    with pytest.raises(FileNotFoundError):
+        P.apply_triposplat_native_silu_avx512_patch(torch.nn.Sequential(torch.nn.SiLU()), enabled=True,
+                                                    library_path="/nonexistent/libtsplat_hip.so")
