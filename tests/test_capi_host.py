@@ -235,3 +235,10 @@ def test_block_patches_disabled_and_missing_library():
     with pytest.raises(FileNotFoundError):
         P.apply_triposplat_native_silu_avx512_patch(torch.nn.Sequential(torch.nn.SiLU()), enabled=True,
                                                     library_path="/nonexistent/libtsplat_hip.so")
+
+
+def test_sampler_backend_reference_name():
+    from tsplat import native_sampler_backend as nsb
+
+    assert nsb.NativeSamplerAVX512Backend is nsb.NativeSamplerBackend
+    assert nsb.create_triposplat_native_sampler_avx512_backend() == (None, {"enabled": False})

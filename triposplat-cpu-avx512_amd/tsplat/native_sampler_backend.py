@@ -124,6 +124,11 @@ class NativeSamplerBackend:
         }
 
 
+# The reference's class name (native_sampler_avx512_backend.py:9), so code
+# that constructs or type-checks against it switches by import alone.
+NativeSamplerAVX512Backend = NativeSamplerBackend
+
+
 def _path(p):
     return library_path(p).as_posix()
 
