@@ -264,10 +264,15 @@ __global__ __launch_bounds__(kWideWaves * 64) void nf24_gemv_wide_kernel(GemvArg
   }
 }
 
-// out[m, c] = bias + sum over splits (in split order) of the partials: a
-// workgroup stages [splits][64 columns] of one row m in LDS with parallel
-// loads, then 64 threads add each column's splits in order.
-constexpr int kMergeCols = 64;
+// out[m, c] = bias + sum over splits (in split order) of the partials, for
+// up to kMergeMaxSplits splits.  A workgroup owns 16 columns of one row m;
+// its 16 threads per column each load every 16th split -- all of a thread's
+// loads are issued before any is used, so the partials arrive in one memory
+// round trip -- and stage them in LDS, where one thread per column adds them
+// in split order.  (16 columns per workgroup gives 4x the workgroups of a
+// 64-column chunk; the merge is latency-bound, not bandwidth-bound.)
+constexpr int kMergeCols = 16;
+constexpr int kMergeLanes = kReduceThreads / kMergeCols;  // threads per column
 constexpr int kMergeMaxSplits = 128;
 __global__ __launch_bounds__(kReduceThreads) void nf24_gemv_merge_kernel(
     const float* partial, const float* bias, float* out, int M, int count, int n_start,
@@ -276,16 +281,43 @@ __global__ __launch_bounds__(kReduceThreads) void nf24_gemv_merge_kernel(
   const int chunks = (count + kMergeCols - 1) / kMergeCols;
   const int m = blockIdx.x / chunks;
   const int c0 = (blockIdx.x % chunks) * kMergeCols;
-  for (int i = threadIdx.x; i < splits * kMergeCols; i += kReduceThreads) {
-    const int s = i / kMergeCols, c = i % kMergeCols;
-    part[s][c] = c0 + c < count ? partial[((int64_t)s * M + m) * count + c0 + c] : 0.0f;
+  const int c = threadIdx.x % kMergeCols, j = threadIdx.x / kMergeCols;
+  const bool ok = c0 + c < count;
+  constexpr int kPer = kMergeMaxSplits / kMergeLanes;
+  float v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int sp = j + kMergeLanes * i;
+    v[i] = (ok && sp < splits) ? partial[((int64_t)sp * M + m) * count + c0 + c] : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int sp = j + kMergeLanes * i;
+    if (sp < splits) part[sp][c] = v[i];
   }
   __syncthreads();
-  const int c = threadIdx.x;
-  if (c >= kMergeCols || c0 + c >= count) return;
-  float v = part[0][c];
-  for (int s = 1; s < splits; ++s) v += part[s][c];
-  out[(int64_t)m * stride_out + c0 + c] = bias[n_start + c0 + c] + v;
+  if (j != 0 || !ok) return;
+  float acc = part[0][c];
+  for (int sp = 1; sp < splits; ++sp) acc += part[sp][c];
+  out[(int64_t)m * stride_out + c0 + c] = bias[n_start + c0 + c] + acc;
+}
+
+// Second kernel of a split call: the merge above, or for more splits than it
+// stages, one thread per output (same order, same result).
+int launch_merge(const float* partial, const float* bias, float* out, int M, int count, int n_start,
+                 int stride_out, int splits, hipStream_t stream) {
+  if (splits <= kMergeMaxSplits) {
+    const int chunks = (count + kMergeCols - 1) / kMergeCols;
+    hipLaunchKernelGGL(nf24_gemv_merge_kernel, dim3((unsigned)(M * chunks)), dim3(kReduceThreads), 0,
+                       stream, partial, bias, out, M, count, n_start, stride_out, splits);
+  } else {
+    const int64_t total = (int64_t)M * count;
+    hipLaunchKernelGGL(nf24_gemv_reduce_kernel,
+                       dim3((unsigned)((total + kReduceThreads - 1) / kReduceThreads)),
+                       dim3(kReduceThreads), 0, stream, partial, bias, out, M, count, n_start,
+                       stride_out, splits);
+  }
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
 template <int MT>
@@ -346,11 +378,8 @@ int launch_nf24_gemv(const GemmParams& p, hipStream_t stream) {
         default: st = launch_wide<8>(a, stream); break;
       }
       if (st != kOk || splits == 1) return st;
-      const int chunks = (p.n_count + kMergeCols - 1) / kMergeCols;
-      hipLaunchKernelGGL(nf24_gemv_merge_kernel, dim3((unsigned)(p.M * chunks)), dim3(kReduceThreads),
-                         0, stream, a.partial, p.bias, p.out, p.M, p.n_count, p.n_start,
-                         p.stride_out, splits);
-      return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+      return launch_merge(a.partial, p.bias, p.out, p.M, p.n_count, p.n_start, p.stride_out, splits,
+                          stream);
     }
   }
   const int mt = p.M <= 1 ? 1 : p.M <= 2 ? 2 : p.M <= 4 ? 4 : p.M <= 8 ? 8 : p.M <= 16 ? 16 : 32;
@@ -389,12 +418,7 @@ int launch_nf24_gemv(const GemmParams& p, hipStream_t stream) {
     default: st = launch_mt<32, 4>(a, cgroups, splits, stream); break;
   }
   if (st != kOk || splits == 1) return st;
-  const int64_t total = (int64_t)p.M * p.n_count;
-  hipLaunchKernelGGL(nf24_gemv_reduce_kernel,
-                     dim3((unsigned)((total + kReduceThreads - 1) / kReduceThreads)),
-                     dim3(kReduceThreads), 0, stream, a.partial, p.bias, p.out, p.M, p.n_count,
-                     p.n_start, p.stride_out, splits);
-  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+  return launch_merge(a.partial, p.bias, p.out, p.M, p.n_count, p.n_start, p.stride_out, splits, stream);
 }
 
 }  // namespace tsplat
