@@ -157,7 +157,7 @@ __global__ __launch_bounds__(kReduceThreads) void nf24_gemv_reduce_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Wide form for M <= 8 with 8-aligned columns: a lane owns 8 adjacent columns
+// Wide form for M <= 16 with 8-aligned columns: a lane owns 8 adjacent columns
 // (one 128-bit code01 and one 64-bit q2 load per row: a wave reads 1 KB + 512 B
 // of one row), a wave owns 16 (or 8) consecutive rows and issues all of
 // their loads before consuming any (one HBM round trip), x comes through the
@@ -171,7 +171,8 @@ constexpr int kWideCols = 512;
 template <int MT, int kRows>
 __global__ __launch_bounds__(kWideWaves * 64) void nf24_gemv_wide_kernel(GemvArgs a) {
   constexpr int rows_per_wave = kRows;
-  __shared__ float red[kWideWaves - 1][MT][kWideCols];
+  constexpr int kRedM = MT < 8 ? MT : 8;  // rows of x reduced per LDS pass
+  __shared__ float red[kWideWaves - 1][kRedM][kWideCols];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -233,33 +234,38 @@ __global__ __launch_bounds__(kWideWaves * 64) void nf24_gemv_wide_kernel(GemvArg
     }
   }
 
-  // Waves 1..3 hand their sums to wave 0, which adds them in wave order.
-  if (wave > 0) {
+  // Waves 1..3 hand their sums to wave 0, which adds them in wave order
+  // (kRedM rows of x per pass through LDS).
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
+  for (int m0 = 0; m0 < MT; m0 += kRedM) {
+    if (m0 > 0) __syncthreads();  // wave 0 has read the previous pass
+    if (wave > 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) red[wave - 1][m][8 * lane + e] = acc[m][e];
-  }
-  __syncthreads();
-  if (wave != 0 || !live) return;
+      for (int m = 0; m < kRedM; ++m)
 #pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    if (m >= a.M) break;
-    float v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      v[e] = acc[m][e];
-#pragma unroll
-      for (int w = 0; w < kWideWaves - 1; ++w) v[e] += red[w][m][8 * lane + e];
+        for (int e = 0; e < 8; ++e) red[wave - 1][m][8 * lane + e] = acc[m0 + m][e];
     }
-    if (a.splits > 1) {
-      float* dst = a.partial + ((int64_t)split * a.M + m) * a.n_count + lc;
-      *reinterpret_cast<floatx4*>(dst) = floatx4{v[0], v[1], v[2], v[3]};
-      *reinterpret_cast<floatx4*>(dst + 4) = floatx4{v[4], v[5], v[6], v[7]};
-    } else {
-      float* dst = a.out + (int64_t)m * a.stride_out + lc;
+    __syncthreads();
+    if (wave != 0 || !live) continue;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dst[e] = a.bias[col + e] + v[e];
+    for (int m = m0; m < m0 + kRedM; ++m) {
+      if (m >= a.M) break;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[e] = acc[m][e];
+#pragma unroll
+        for (int w = 0; w < kWideWaves - 1; ++w) v[e] += red[w][m - m0][8 * lane + e];
+      }
+      if (a.splits > 1) {
+        float* dst = a.partial + ((int64_t)split * a.M + m) * a.n_count + lc;
+        *reinterpret_cast<floatx4*>(dst) = floatx4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<floatx4*>(dst + 4) = floatx4{v[4], v[5], v[6], v[7]};
+      } else {
+        float* dst = a.out + (int64_t)m * a.stride_out + lc;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[e] = a.bias[col + e] + v[e];
+      }
     }
   }
 }
@@ -351,7 +357,7 @@ int launch_mt(GemvArgs a, int cgroups, int splits, hipStream_t stream) {
 // bytes; a split costs a second, small kernel.
 int launch_nf24_gemv(const GemmParams& p, hipStream_t stream) {
   if (p.M < 1 || p.M > 32) return kErrDims;
-  const bool wide = p.M <= 8 && ((p.N | p.n_start | p.n_count) & 7) == 0 &&
+  const bool wide = p.M <= 16 && ((p.N | p.n_start | p.n_count) & 7) == 0 &&
                     (reinterpret_cast<uintptr_t>(p.code01) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(p.q2) & 7) == 0 &&
                     (reinterpret_cast<uintptr_t>(p.scale) & 15) == 0;
@@ -371,11 +377,12 @@ int launch_nf24_gemv(const GemmParams& p, hipStream_t stream) {
         if (a.partial == nullptr) return kErrWorkspace;
       }
       int st;
-      switch (p.M <= 1 ? 1 : p.M <= 2 ? 2 : p.M <= 4 ? 4 : 8) {
+      switch (p.M <= 1 ? 1 : p.M <= 2 ? 2 : p.M <= 4 ? 4 : p.M <= 8 ? 8 : 16) {
         case 1: st = launch_wide<1>(a, stream); break;
         case 2: st = launch_wide<2>(a, stream); break;
         case 4: st = launch_wide<4>(a, stream); break;
-        default: st = launch_wide<8>(a, stream); break;
+        case 8: st = launch_wide<8>(a, stream); break;
+        default: st = launch_wide<16>(a, stream); break;
       }
       if (st != kOk || splits == 1) return st;
       return launch_merge(a.partial, p.bias, p.out, p.M, p.n_count, p.n_start, p.stride_out, splits,
