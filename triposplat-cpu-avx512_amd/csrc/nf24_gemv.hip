@@ -213,24 +213,48 @@ __global__ __launch_bounds__(kWideWaves * 64) void nf24_gemv_wide_kernel(GemvArg
   for (int m = 0; m < MT; ++m)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[m][e] = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kRows; ++i) {
+  // acc[m] += x[m][row] * w[row] over the wave's rows.  Rows of x past M
+  // read row M - 1 (those sums are never stored), so every x load is
+  // unconditional; only rows past the split's range (the last wave of a
+  // ragged split, nr < kRows: uniform) are masked, by x = 0, on a separate
+  // path -- a select on a loaded value is compiled into a branch and a wait
+  // per load, which would serialise the x loads of the common case.
+  auto decode = [&](int i, float (&w)[8]) {
     const uint32_t cw[4] = {c[i].x, c[i].y, c[i].z, c[i].w};
     const uint32_t qw[2] = {q[i].x, q[i].y};
-    float w[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int32_t code = (int32_t)(int16_t)((cw[e >> 1] >> (16 * (e & 1))) & 0xffffu);
       const int32_t res = (int32_t)(int8_t)((qw[e >> 2] >> (8 * (e & 3))) & 0xffu);
       w[e] = (float)(code * 256 + res) * sc[e];
     }
-    const int row = min(r0 + i, a.K - 1);
-    const bool row_ok = i < nr;  // uniform over the wave
+  };
+  const float* xrow = a.x + r0;
+  if (nr == kRows) {
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float xv = (row_ok && m < a.M) ? a.x[(int64_t)m * a.stride_x + row] : 0.0f;
+    for (int i = 0; i < kRows; ++i) {
+      float w[8];
+      decode(i, w);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[m][e] = fmaf(xv, w[e], acc[m][e]);
+      for (int m = 0; m < MT; ++m) {
+        const float xv = xrow[(int64_t)min(m, a.M - 1) * a.stride_x + i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[m][e] = fmaf(xv, w[e], acc[m][e]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      float w[8];
+      decode(i, w);
+      const int row = min(r0 + i, a.K - 1);
+      const bool row_ok = i < nr;  // uniform over the wave
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float xv = row_ok ? a.x[(int64_t)min(m, a.M - 1) * a.stride_x + row] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[m][e] = fmaf(xv, w[e], acc[m][e]);
+      }
     }
   }
 
