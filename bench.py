@@ -78,14 +78,32 @@ def load_traffic(name):
     return None
 
 
-def cpu_baseline_sdpa(q, k, v, budget_s=12.0):
+def parity_stats(got, ref, tol_abs=None):
+    """max-abs / relative error of a device result against the reference's
+    output on the same inputs (float64 arithmetic)."""
+    import numpy as np
+
+    d = got.astype(np.float64) - ref.astype(np.float64)
+    max_abs = float(np.abs(d).max())
+    rms_ref = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    out = {"max_abs": max_abs, "max_rel": max_abs / float(np.abs(ref).max()),
+           "rmse": float(np.sqrt(np.mean(d * d))), "rel_rmse": float(np.sqrt(np.mean(d * d))) / rms_ref}
+    if tol_abs is not None:
+        out.update({"tolerance_max_abs": tol_abs, "within_tolerance": bool(max_abs <= tol_abs)})
+    return out
+
+
+def cpu_baseline_sdpa(q, k, v, budget_s=12.0, gpu_out=None):
     """Time the reference AVX-512 SDPA (or the oracle port) on the host.
 
     The sample is the whole configs[1] call when it fits the budget (it does
     on a 16-core host: ~1.5 s), else the first `rows` query rows of every
     head against all keys.  Median of 3 after one warmup, with all host
     threads; a second figure uses the reference's published SDPA thread
-    count (4)."""
+    count (4).  With `gpu_out` (the device result, [B, L, H, D]) and the
+    reference build present, the sampled rows of the reference's own output
+    are also compared with it (`parity_vs_reference`; the GPU tests' bound
+    is 1e-5 * max|v| max-abs)."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -95,11 +113,13 @@ def cpu_baseline_sdpa(q, k, v, budget_s=12.0):
     kind = "reference" if O.ref_available() else "port"
     B, H, L, D = q.shape
 
+    last = {}
+
     def run(rows, nthreads):
         qs = np.ascontiguousarray(q[:, :, :rows])
         t0 = time.perf_counter()
         if kind == "reference":
-            O.ref_sdpa_q8t512(qs, k, v, None, nthreads)
+            last[rows] = O.ref_sdpa_q8t512(qs, k, v, None, nthreads)
         else:
             O.sdpa_q8t512(qs, k, v)
         return time.perf_counter() - t0
@@ -112,6 +132,11 @@ def cpu_baseline_sdpa(q, k, v, budget_s=12.0):
         return rows, times[1]
 
     rows, t_med = measure(threads)
+    parity = None
+    if gpu_out is not None and rows in last:
+        got = np.ascontiguousarray(gpu_out[:, :rows].transpose(0, 2, 1, 3))
+        parity = parity_stats(got, last[rows], tol_abs=1e-5 * float(np.abs(v).max()))
+        parity["rows"] = f"{rows} of {L} query rows, all heads"
     flop = 4.0 * B * H * rows * L * D
     rows4, t4 = measure(4)
     flop4 = 4.0 * B * H * rows4 * L * D
@@ -125,6 +150,7 @@ def cpu_baseline_sdpa(q, k, v, budget_s=12.0):
         "seconds_per_call": t_med * L / rows,
         "threads4_tflops": flop4 / t4 / 1e12,
         "threads4_seconds_per_call": t4 * L / rows4,
+        "parity_vs_reference": parity,
     }
 
 
@@ -138,8 +164,9 @@ def sdpa_inputs(torch, dev):
     return q_h, k_h, v_h
 
 
-def run_sdpa(torch, dev, steps, warmup, host, precision="fp32"):
-    """one exact SDPA call per step; returns (wall s/step, kernel ms).
+def run_sdpa(torch, dev, steps, warmup, host, precision="fp32", keep_out=False):
+    """one exact SDPA call per step; returns (wall s/step, kernel
+    ms, the output on the host if keep_out else None).
     precision: the product precision (the headline is "fp32"; the opt-in
     modes are timed this way only for `--only sdpa --precision ...` profiles)."""
     from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
@@ -164,7 +191,7 @@ def run_sdpa(torch, dev, steps, warmup, host, precision="fp32"):
     wall = (time.perf_counter() - t0) / steps
     kernel_ms = time_events(torch, step, max(3, steps))
     assert torch.isfinite(out).all().item()
-    return wall, kernel_ms
+    return wall, kernel_ms, (out.cpu().numpy() if keep_out else None)
 
 
 def run_sdpa_opt_in(torch, dev, host, fp32_ms, iters=5):
@@ -238,8 +265,12 @@ def run_sdpa_variants(torch, dev, host, iters=5):
     return res
 
 
-def run_gemm(torch, dev, iters):
-    """NF24 Linear 4096x1024 @ 1024x3072 (+ bias)."""
+def run_gemm(torch, dev, iters, ref_parity=False):
+    """NF24 Linear 4096x1024 @ 1024x3072 (+ bias).  With
+    ref_parity and the reference build present, the device result is also
+    compared with the reference's own AVX-512 NF24 GEMM on the same inputs
+    (`parity_vs_reference`; the GPU tests bound each output by the fp32
+    summation-order bound 2*gamma_(K+1)*sum|terms|)."""
     import numpy as np
     from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
 
@@ -284,6 +315,17 @@ def run_gemm(torch, dev, iters):
             "rel_rmse_vs_fp32": float(d.pow(2).mean().sqrt() / strict.double().pow(2).mean().sqrt()),
             "max_abs_vs_fp32": float(d.abs().max()),
         }
+    parity = None
+    if ref_parity:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+
+        if O.ref_available():
+            ref = O.ref_nf24_gemm(x.cpu().numpy(), codes[0].cpu().numpy(), codes[1].cpu().numpy(),
+                                  scales[0].cpu().numpy(), bias.cpu().numpy(),
+                                  threads=len(os.sched_getaffinity(0)))
+            parity = parity_stats(strict.cpu().numpy(), ref)
+            parity["rows"] = f"all {M} rows"
     return {
         "workload": "configs[0] NF24 Linear X[4096x1024] @ W[1024x3072] + bias, fp32 MFMA accumulate",
         "ms": g_ms,
@@ -292,6 +334,7 @@ def run_gemm(torch, dev, iters):
         "algorithmic_bytes": float(M * K * 4 + K * N * 3 + N * 8 + M * N * 4),
         "traffic": load_traffic("nf24_gemm_config0"),
         "opt_in_bf16": opt_in,
+        "parity_vs_reference": parity,
     }
 
 
@@ -569,7 +612,7 @@ def main():
     host = sdpa_inputs(torch, dev)
     B, H, L, D = host[0].shape
     if args.only == "sdpa":
-        wall, kernel_ms = run_sdpa(torch, dev, args.steps, args.warmup, host, args.precision)
+        wall, kernel_ms, _ = run_sdpa(torch, dev, args.steps, args.warmup, host, args.precision)
         print(json.dumps({"sdpa_ms": kernel_ms, "precision": args.precision,
                           "tflops_equiv": 4.0 * B * H * L * L * D / (kernel_ms * 1e-3) / 1e12}))
         return 0
@@ -577,16 +620,17 @@ def main():
         print("--precision applies to --only sdpa; the full line measures fp32 and reports the "
               "opt-in modes beside it", file=sys.stderr)
         return 2
-    wall, kernel_ms = run_sdpa(torch, dev, args.steps, args.warmup, host)
+    wall, kernel_ms, sdpa_out = run_sdpa(torch, dev, args.steps, args.warmup, host,
+                                         keep_out=not args.no_cpu_baseline)
     sdpa_flop = 4.0 * B * H * L * L * D
     achieved = sdpa_flop / (kernel_ms * 1e-3) / 1e12
 
     variants = run_sdpa_variants(torch, dev, host)
     sdpa_opt_in = run_sdpa_opt_in(torch, dev, host, kernel_ms)
-    gemm = run_gemm(torch, dev, 20)
+    gemm = run_gemm(torch, dev, 20, ref_parity=not args.no_cpu_baseline)
     gemm["skinny_m"] = run_gemm_skinny(torch, dev)
     flow = None if args.no_flow else run_flow(torch, dev, 3, not args.no_cpu_baseline, args.validate_flow)
-    cpu = None if args.no_cpu_baseline else cpu_baseline_sdpa(*host)
+    cpu = None if args.no_cpu_baseline else cpu_baseline_sdpa(*host, gpu_out=sdpa_out)
 
     line = {
         "metric": METRIC,
