@@ -228,10 +228,13 @@ def run_sdpa_opt_in(torch, dev, host, fp32_ms, iters=5):
     return res
 
 
-def run_sdpa_variants(torch, dev, host, iters=5):
+def run_sdpa_variants(torch, dev, host, iters=5, ref_parity=False):
     """key-bias self attention (per-head bias [16, 16384] ~ U(-2, 0),
     and the reference-faithful shared [Lk] bias with log(2048) on one key),
-    and cross attention (16384 queries vs 2048 condition keys, k/v ~ N(0,1))."""
+    and cross attention (16384 queries vs 2048 condition keys, k/v ~ N(0,1)).
+    With ref_parity and the reference build present, each output is compared
+    with the reference's AVX-512 SDPA on the same inputs (its kernel takes a
+    shared [Lk] bias, so the per-head case runs it once per head)."""
     import numpy as np
     from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
 
@@ -248,20 +251,40 @@ def run_sdpa_variants(torch, dev, host, iters=5):
     Lc = 2048
     kc = torch.from_numpy(np.random.default_rng(14).standard_normal((B, H, Lc, D), dtype=np.float32)).to(dev)
     vc = torch.from_numpy(np.random.default_rng(15).standard_normal((B, H, Lc, D), dtype=np.float32)).to(dev)
+    O = None
+    if ref_parity:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+
+        if not O.ref_available():
+            O = None
+    threads = len(os.sched_getaffinity(0))
+
+    def ref_per_head():
+        return np.concatenate([O.ref_sdpa_q8t512(q_h[:, h:h + 1], k_h[:, h:h + 1], v_h[:, h:h + 1], bias_h[h],
+                                                 threads) for h in range(H)], axis=1)
+
     res = {}
-    for name, fn, flop in (
+    for name, fn, flop, ref_fn, v_max in (
         ("keybias_per_head", lambda: native_sdpa_f32_ex(q, k, v, key_bias_per_head=bias, out=out, out_layout="blhd"),
-         4.0 * B * H * L * L * D),
+         4.0 * B * H * L * L * D, ref_per_head, float(np.abs(v_h).max())),
         ("keybias_shared_log2048", lambda: native_sdpa_f32_ex(q, k, v, key_bias=shared, out=out, out_layout="blhd"),
-         4.0 * B * H * L * L * D),
+         4.0 * B * H * L * L * D,
+         lambda: O.ref_sdpa_q8t512(q_h, k_h, v_h, shared.cpu().numpy(), threads), float(np.abs(v_h).max())),
         ("cross_16384x2048", lambda: native_sdpa_f32_ex(q, kc, vc, out=out, out_layout="blhd"),
-         4.0 * B * H * L * Lc * D),
+         4.0 * B * H * L * Lc * D,
+         lambda: O.ref_sdpa_q8t512(q_h, kc.cpu().numpy(), vc.cpu().numpy(), None, threads),
+         float(vc.abs().max())),
     ):
         fn()
         torch.cuda.synchronize()
         ms = sorted(time_events(torch, fn, iters) for _ in range(3))[1]
         tf = flop / (ms * 1e-3) / 1e12
         res[name] = {"ms": ms, "tflops": tf, "frac_fp32_mfma_peak": tf / PEAK_FP32_MFMA}
+        if O is not None:
+            fn()
+            got = np.ascontiguousarray(out.cpu().numpy().transpose(0, 2, 1, 3))
+            res[name]["parity_vs_reference"] = parity_stats(got, ref_fn(), tol_abs=1e-5 * v_max)
     return res
 
 
@@ -625,7 +648,7 @@ def main():
     sdpa_flop = 4.0 * B * H * L * L * D
     achieved = sdpa_flop / (kernel_ms * 1e-3) / 1e12
 
-    variants = run_sdpa_variants(torch, dev, host)
+    variants = run_sdpa_variants(torch, dev, host, ref_parity=not args.no_cpu_baseline)
     sdpa_opt_in = run_sdpa_opt_in(torch, dev, host, kernel_ms)
     gemm = run_gemm(torch, dev, 20, ref_parity=not args.no_cpu_baseline)
     gemm["skinny_m"] = run_gemm_skinny(torch, dev)
