@@ -66,7 +66,9 @@ SHAPES = [(25, 96, 64), (40, 96, 64), (10, 96, 64), (3, 96, 5), (1, 1024, 3072),
           (4, 2048, 640), (16, 1024, 3072), (32, 512, 384), (5, 4096, 1024), (12, 1000, 130),
           (3, 1000, 512), (7, 70, 1032), (1, 8200, 1024), (6, 4096, 8), (2, 1024, 6144),
           # 9-16 rows on the wide kernel (two LDS reduction passes), partial slab
-          (9, 1024, 520), (13, 2048, 1024)]
+          (9, 1024, 520), (13, 2048, 1024),
+          # more K splits than the staged merge holds: the one-thread-per-output merge
+          (1, 40000, 96)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
