@@ -104,7 +104,8 @@ def test_fused_layernorm_modulate_and_head_norm(oracle, cuda):
     assert np.array_equal(v_bhld.cpu().numpy(), kv[:, :, 1].transpose(0, 2, 1, 3))
 
 
-@pytest.mark.parametrize("M,K,N", [(600, 256, 1024), (16384, 1024, 4096), (3000, 4096, 1024), (20, 128, 96)])
+@pytest.mark.parametrize("M,K,N", [(600, 256, 1024), (16384, 1024, 4096), (3000, 4096, 1024), (20, 128, 96),
+                                   (18432, 1024, 1024)])  # whole-round split inside the second gate batch
 def test_gemm_epilogues(oracle, cuda, M, K, N):
     """GELU / gated-residual / add epilogues == NF24 Linear then the separate
     elementwise kernel (bit for bit when both use the same GEMM tile, M > 32);

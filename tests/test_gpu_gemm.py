@@ -131,11 +131,12 @@ def test_gemm_config1_sampled_rows(oracle, cuda, hiplib):
 
 
 @pytest.mark.parametrize("M,K,N", [(16384, 1024, 1024), (32768, 1002, 1024), (2048, 1024, 2048),
-                                   (9000, 998, 1030)])
+                                   (9000, 998, 1030), (18432, 1024, 3072)])
 def test_gemm_large_tiles_sampled_rows(oracle, cuda, hiplib, M, K, N):
     """Shapes that route to each tile configuration (256x256, 256x192,
-    128x128), with the vectorised and the scalar-load paths (K % 4 != 0 or
-    odd N); the oracle checks 32 sampled rows."""
+    128x128, and 18432 rows: 256x256 over 16384 rows plus 128x128 over the
+    rest), with the vectorised and the scalar-load paths (K % 4 != 0 or odd
+    N); the oracle checks 32 sampled rows."""
     import torch
 
     print(f"gemm large M={M} K={K} N={N}", flush=True)

@@ -98,7 +98,8 @@ def test_qkv_direct(oracle, cuda, B, L, H, fb, Lp):
 
 
 @pytest.mark.parametrize("B,L,H,fb", [(1, 16384, 16, 1), (1, 4096, 16, 1), (2, 300, 4, 2), (3, 257, 2, 1),
-                                     (1, 5000, 16, 1), (1, 8194, 16, 1), (1, 3000, 16, 1)])
+                                     (1, 5000, 16, 1), (1, 8194, 16, 1), (1, 3000, 16, 1),
+                                     (1, 18432, 16, 1)])  # split into whole-round row launches
 def test_qkv_fused_matches_unfused(oracle, cuda, B, L, H, fb):
     """Fused epilogue == NF24 GEMM then the postprocess kernel, at shapes that
     route to each tile configuration (256x256: L=16384, 5000, 8194; 256x192:
@@ -127,7 +128,7 @@ def test_qkv_fused_matches_unfused(oracle, cuda, B, L, H, fb):
         assert torch.equal(a_, b_)
 
 
-@pytest.mark.parametrize("B,L,H", [(1, 16384, 16), (2, 300, 4), (3, 257, 2), (1, 5000, 16)])
+@pytest.mark.parametrize("B,L,H", [(1, 16384, 16), (2, 300, 4), (3, 257, 2), (1, 5000, 16), (1, 18432, 16)])
 def test_qkv_direct_bhld_layout(cuda, B, L, H):
     """kv_layout="bhld": the same epilogue arithmetic storing k and v
     [B, H, L, 64] like q -- bit-identical to the packed outputs transposed

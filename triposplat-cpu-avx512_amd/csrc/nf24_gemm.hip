@@ -277,29 +277,54 @@ int compute_units() {
   return cached[dev];
 }
 
+// Modelled time of configuration i (kChoices) over M x n_count outputs.
+double model_time(int i, int M, int n_count) {
+  const int cus = compute_units();
+  const Choice& c = kChoices[i];
+  const int64_t tiles = (int64_t)((M + c.bm - 1) / c.bm) * ((n_count + c.bn - 1) / c.bn);
+  const int64_t slots = (int64_t)cus * c.wgs_per_cu;
+  const int64_t full = tiles / slots;
+  const int64_t rest = tiles - full * slots;
+  const double tile_t = (double)c.bm * c.bn / c.rate;
+  double t = (double)full * c.wgs_per_cu * tile_t;
+  if (rest > 0) {
+    const int64_t k = (rest + cus - 1) / cus;
+    t += (double)k * tile_t * ((k == 1 && c.waves == 4) ? 1.25 : 1.0);
+  }
+  return t;
+}
+
 // Index into kChoices of the configuration with the smallest modelled time.
 int pick_config(int M, int n_count) {
-  const int cus = compute_units();
   int best = 0;
-  double best_t = 0.0;
-  for (int i = 0; i < 3; ++i) {
-    const Choice& c = kChoices[i];
-    const int64_t tiles = (int64_t)((M + c.bm - 1) / c.bm) * ((n_count + c.bn - 1) / c.bn);
-    const int64_t slots = (int64_t)cus * c.wgs_per_cu;
-    const int64_t full = tiles / slots;
-    const int64_t rest = tiles - full * slots;
-    const double tile_t = (double)c.bm * c.bn / c.rate;
-    double t = (double)full * c.wgs_per_cu * tile_t;
-    if (rest > 0) {
-      const int64_t k = (rest + cus - 1) / cus;
-      t += (double)k * tile_t * ((k == 1 && c.waves == 4) ? 1.25 : 1.0);
-    }
-    if (i == 0 || t < best_t) {
-      best = i;
-      best_t = t;
-    }
-  }
+  for (int i = 1; i < 3; ++i)
+    if (model_time(i, M, n_count) < model_time(best, M, n_count)) best = i;
   return best;
+}
+
+// Rows to run as a first launch of 256 x 256 tiles that fill whole rounds
+// of CUs, the rest going to a second launch with its own best shape -- or 0
+// when one launch is modelled as fast (within 3 %).  E.g. the single-stream
+// graph's M = 18432 rows: 16384 rows of 256 x 256 tiles plus 2048 rows of
+// 128 x 128 tiles model 8-9 % faster at N = 3072 / 4096 than any one shape,
+// whose last round would be mostly idle.  Every tile shape sums each output
+// in the same order, so the split changes no result bit.
+int round_split_rows(int M, int n_count) {
+  const int cus = compute_units();
+  const int bands = (n_count + 255) / 256;  // 256 x 256 tiles per 256 rows
+  int g = cus, r = bands;                   // rows of whole rounds: multiples of
+  while (r != 0) {                          // 256 * cus / gcd(cus, bands)
+    const int t = g % r;
+    g = r;
+    r = t;
+  }
+  const int64_t unit = 256LL * (cus / g);
+  const int64_t m1 = (int64_t)M / unit * unit;
+  if (m1 == 0 || m1 == M) return 0;
+  const double one = model_time(pick_config(M, n_count), M, n_count);
+  const int rest = M - (int)m1;
+  const double two = model_time(0, (int)m1, n_count) + model_time(pick_config(rest, n_count), rest, n_count);
+  return two < 0.97 * one ? (int)m1 : 0;
 }
 
 // Rows past the last multiple of 256 that number at most kTailRows would
@@ -339,6 +364,10 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
     const int st = launch_nf24_gemm(rows_slice(p, 0, p.M - rem), stream);
     return st != kOk ? st : launch_cfg<CfgTail>(rows_slice(p, p.M - rem, rem), stream);
   }
+  if (const int m1 = round_split_rows(p.M, p.n_count)) {
+    const int st = launch_nf24_gemm(rows_slice(p, 0, m1), stream);
+    return st != kOk ? st : launch_nf24_gemm(rows_slice(p, m1, p.M - m1), stream);
+  }
   const int best = pick_config(p.M, p.n_count);
   if (best == 0) return launch_cfg<CfgLarge>(p, stream);
   if (best == 1) return launch_cfg<CfgWide>(p, stream);
@@ -358,6 +387,10 @@ int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_
   }
   // Few rows: the 32-row tile (the epilogues live in the MFMA kernels).
   if (p.M <= 32) return launch_cfg<CfgTail, kEpi>(p, stream, q, e, row0);
+  if (const int m1 = round_split_rows(p.M, p.n_count)) {
+    const int st = launch_epi_kind<kEpi>(rows_slice(p, 0, m1), e, stream, q, row0);
+    return st != kOk ? st : launch_epi_kind<kEpi>(rows_slice(p, m1, p.M - m1), e, stream, q, row0 + m1);
+  }
   const int best = pick_config(p.M, p.n_count);
   if (best == 0) return launch_cfg<CfgLarge, kEpi>(p, stream, q, e, row0);
   if (best == 1) return launch_cfg<CfgWide, kEpi>(p, stream, q, e, row0);
