@@ -378,8 +378,26 @@ def quantize_nf24_i16(weight):
 
 # --------------------------------------------------------------------------
 # Reference build (oracle/_ref) loaders, used to pin the oracle.
+# Instruction sets the reference build is compiled for (oracle/Makefile
+# REF_FLAGS); on a host without them its kernels would die on an illegal
+# instruction, so they count as unavailable there.
+REF_CPU_FLAGS = ("avx512f", "avx512dq", "avx512bw", "avx512vl", "fma")
+
+
+def host_supports_ref():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    have = set(line.split(":", 1)[1].split())
+                    return all(flag in have for flag in REF_CPU_FLAGS)
+    except OSError:
+        pass
+    return False
+
+
 def ref_available():
-    return (REF_DIR / "libref_gemm_nf24_i16.so").is_file()
+    return (REF_DIR / "libref_gemm_nf24_i16.so").is_file() and host_supports_ref()
 
 
 def ref_lib(name):
