@@ -21,6 +21,8 @@
 
 #include "nf24_gemm_common.h"
 
+#include <type_traits>
+
 namespace tsplat {
 namespace {
 
@@ -255,7 +257,15 @@ using CfgLarge = GemmCfg<256, 256, 16, 4, 4>;    // 16 waves, 1 workgroup / CU
 using CfgWide = GemmCfg<256, 192, 16, 4, 3>;     // 12 waves, 1 workgroup / CU
 using CfgSmall = GemmCfg<128, 128, 16, 2, 2, 3>; // 4 waves, 3 workgroups / CU
 using CfgSkinny = GemmCfg<32, 128, 32, 1, 4>;
-using CfgTail = GemmCfg<32, 128, 32, 1, 2>;      // <= 32 rows with an epilogue; 64-column waves
+using CfgTail = GemmCfg<32, 128, 32, 1, 2>;      // <= 32 rows, QKV epilogue: 64-column waves (a head)
+// <= 32 rows otherwise: each wave's cost is its chain of K/2 MFMAs per 32
+// columns (one wave per SIMD, nothing to overlap), so 32-column waves -- twice
+// the waves of 64-column ones -- finish in ~0.55x the time (e.g. one row
+// at K = 4096, N = 1024: 148 against 270 us).
+using CfgTailNarrow = GemmCfg<32, 32, 32, 1, 1>;
+
+template <int kEpi>
+using TailCfg = typename std::conditional<kEpi == kEpiQkv, CfgTail, CfgTailNarrow>::type;
 
 struct Choice {
   int bm, bn, wgs_per_cu, waves;
@@ -362,7 +372,7 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
   }
   if (const int rem = tail_rows(p.M)) {
     const int st = launch_nf24_gemm(rows_slice(p, 0, p.M - rem), stream);
-    return st != kOk ? st : launch_cfg<CfgTail>(rows_slice(p, p.M - rem, rem), stream);
+    return st != kOk ? st : launch_cfg<CfgTailNarrow>(rows_slice(p, p.M - rem, rem), stream);
   }
   if (const int m1 = round_split_rows(p.M, p.n_count)) {
     const int st = launch_nf24_gemm(rows_slice(p, 0, m1), stream);
@@ -382,11 +392,11 @@ int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_
   if (const int rem = tail_rows(p.M)) {
     const int st = launch_epi_kind<kEpi>(rows_slice(p, 0, p.M - rem), e, stream, q, row0);
     return st != kOk ? st
-                     : launch_cfg<CfgTail, kEpi>(rows_slice(p, p.M - rem, rem), stream, q, e,
+                     : launch_cfg<TailCfg<kEpi>, kEpi>(rows_slice(p, p.M - rem, rem), stream, q, e,
                                                  row0 + p.M - rem);
   }
   // Few rows: the 32-row tile (the epilogues live in the MFMA kernels).
-  if (p.M <= 32) return launch_cfg<CfgTail, kEpi>(p, stream, q, e, row0);
+  if (p.M <= 32) return launch_cfg<TailCfg<kEpi>, kEpi>(p, stream, q, e, row0);
   if (const int m1 = round_split_rows(p.M, p.n_count)) {
     const int st = launch_epi_kind<kEpi>(rows_slice(p, 0, m1), e, stream, q, row0);
     return st != kOk ? st : launch_epi_kind<kEpi>(rows_slice(p, m1, p.M - m1), e, stream, q, row0 + m1);
