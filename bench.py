@@ -56,6 +56,17 @@ def rope_rmsnorm_host(x, theta=10000.0):
     return y.astype(np.float32)
 
 
+def host_cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baselines."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def time_events(torch, fn, iters):
     """Average device duration of fn() (ms) from events on the current stream."""
     start = torch.cuda.Event(enable_timing=True)
@@ -144,6 +155,7 @@ def cpu_baseline_sdpa(q, k, v, budget_s=12.0, gpu_out=None):
         "value": flop / t_med / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
+        "host_cpu": host_cpu_model(),
         "kind": kind,
         "sample": f"exact SDPA q8t512 (reference AVX-512 build), B=1 H=16 D=64, {rows} of {L} query rows "
                   f"vs all {L} keys; median of 3 = {t_med:.3f} s; {threads} OpenMP threads",
@@ -455,13 +467,28 @@ def run_flow(torch, dev, steps, with_cpu, validate):
             t_h = np.full(2, ts[0] * 1000.0, np.float32)
             _, tm = cpu.timestep(t_h)
             xx, cc = np.stack((z_h, z_h)), np.stack((c_h, np.zeros_like(c_h)))
+            tm = np.ascontiguousarray(tm, np.float32)
             cpu.block(params["blocks"][0], xx[:, :256], cc, tm)
             t0 = time.perf_counter()
-            cpu.block(params["blocks"][0], xx, cc, tm)
+            blk_ref = cpu.block(params["blocks"][0], xx, cc, tm)
             blk_cpu = time.perf_counter() - t0
             est = blk_cpu * cfg.blocks
+            # the same block on the device, same weights / inputs / modulation
+            blk_gpu = model.block_forward(model.blocks[0], torch.from_numpy(xx).to(dev),
+                                          torch.from_numpy(cc).to(dev), torch.from_numpy(tm).to(dev))
+            torch.cuda.synchronize()
+            par = parity_stats(blk_gpu.cpu().numpy(), blk_ref)
+            par["latent_rmse_metric"] = combined_rmse(blk_gpu.cpu().numpy(), blk_ref)
+            par["gate_rmse"] = 1e-4
+            par["within_gate"] = bool(par["latent_rmse_metric"] <= 1e-4)
+            par["compared"] = ("configs[3] block output, both CFG branches (condition, zero condition), "
+                               f"all {2 * L} x {C} values, against the "
+                               f"{'reference AVX-512 build' if backend == 'reference' else 'oracle port'}")
+            out["config3_block"]["parity_vs_reference"] = par
+            del blk_gpu
             out["config4_step"]["cpu_baseline"] = {
                 "kind": "reference" if backend == "reference" else "port", "cores": threads,
+                "host_cpu": host_cpu_model(),
                 "sample": "one full-size block on both CFG branches through the reference's own "
                           "AVX-512 kernels (NF24 GEMM, QKV-direct, SDPA, LayerNorm, modulate, "
                           "gated residual, GELU, RMSNorm), x 28 blocks",

@@ -168,14 +168,14 @@ int triposplat_qkv_postprocess_v2_tail_only_clear(void);
  * scripts/native_qkv_postprocess_bf16_probe_avx512.c:34-94 (a build of the
  * postprocess whose packed k and/or v are rounded to bf16 after the exact
  * computation; build_native_qkv_postprocess_bf16_probe_avx512.sh selects
- * k, v or kv at compile time).  Here the selection is a process-wide mode:
- * bit 0 rounds k, bit 1 rounds v (nearest bf16, ties to even, stored as
- * fp32; probe file :11-22), applied by every QKV postprocess entry -- the
- * two above, the selected-rows entries and the fused NF24 QKV entries --
- * to the k/v they store.  Default 0: exact.  Mode outside 0..3 -> -2.
- * Calls already enqueued keep the mode they were launched with. */
-int tsplat_set_qkv_bf16_round(int mode);
-/* native_qkv_postprocess_bf16_probe_avx512.c:96-105: the current mode. */
+ * k, v or kv at compile time).  Here the selection is the per-call
+ * `kv_round` argument of the asynchronous postprocess forms below (the
+ * full-sequence, selected-rows and fused NF24 QKV entries): bit 0 rounds
+ * the stored k, bit 1 the stored v (nearest bf16, ties to even, kept as
+ * fp32; probe file :11-22); 0 stores them exact; outside 0..3 -> -2.  The
+ * reference-named entries of this library always store them exact, so the
+ * probe-mode query reports 0 (native_qkv_postprocess_bf16_probe_avx512.c:
+ * 96-105). */
 int triposplat_qkv_postprocess_bf16_probe_mode(void);
 
 /* scripts/native_qkv_postprocess_v2_avx512.c:107-191: selected query rows.
@@ -190,14 +190,15 @@ int triposplat_q_kv_selected_rope_rmsnorm_pack_f32_avx512_v2(
     const float* q_gamma, const float* k_gamma, float* q_bhld, float* packed_k, float* packed_v,
     int B, int Lq, int Lk, int H, int D, int Lk_padded, int frequency_batches, int threads);
 /* Asynchronous form; the indices are not read on the host: a query whose
- * index is outside [0, Lk) gets an all-zero q row. */
+ * index is outside [0, Lk) gets an all-zero q row.  kv_round: see the bf16
+ * probe above (0 = exact). */
 int tsplat_q_kv_selected_postprocess_async(const float* q, const float* kv,
                                            const float* frequencies,
                                            const int64_t* selected_indices,
                                            const float* q_gamma, const float* k_gamma,
                                            float* q_bhld, float* packed_k, float* packed_v, int B,
                                            int Lq, int Lk, int H, int D, int Lk_padded,
-                                           int frequency_batches, void* stream);
+                                           int frequency_batches, int kv_round, void* stream);
 
 /* scripts/gemm_nf24_qkv_direct_avx512.c:87-199: NF24 QKV GEMM (N = 3*H*64)
  * followed by the postprocess above, without returning the [B*L, N]
@@ -216,11 +217,12 @@ int triposplat_gemm_nf24_qkv_direct_row_tile(void);
 int triposplat_gemm_nf24_qkv_direct_tile_bytes(void);
 int triposplat_gemm_nf24_qkv_direct_residual_mode(void);
 
-/* Asynchronous forms of the two QKV entries. */
+/* Asynchronous forms of the two QKV entries (the postprocess with the
+ * probe's per-call kv_round, 0 = exact; the fused entry always exact). */
 int tsplat_qkv_postprocess_async(const float* qkv, const float* frequencies, const float* q_gamma,
                                  const float* k_gamma, float* q_bhld, float* packed_k,
                                  float* packed_v, int B, int L, int H, int D, int L_padded,
-                                 int frequency_batches, void* stream);
+                                 int frequency_batches, int kv_round, void* stream);
 int tsplat_gemm_nf24_qkv_direct_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,
                                       const float* scale, const float* bias,
                                       const float* frequencies, const float* q_gamma,
@@ -286,12 +288,14 @@ int tsplat_nf24_gemm_precision_async(const float* x, const int16_t* code01_t,
  * (the RoPE / RMSNorm epilogue is the same fp32 arithmetic) and a choice of
  * K/V layout: kv_layout 0 packed [B, H, 64, L_padded] (the reference's),
  * 1 [B, H, L, 64] like q (L_padded ignored), the layout the unpacked SDPA
- * reads.  No counterpart in the reference. */
+ * reads; kv_round as the bf16 probe above (0 = exact).  No counterpart in
+ * the reference. */
 int tsplat_gemm_nf24_qkv_direct_ex_async(
     const float* x, const int16_t* code01_t, const int8_t* q2_t, const float* scale,
     const float* bias, const float* frequencies, const float* q_gamma, const float* k_gamma,
     float* q_bhld, float* k_out, float* v_out, int B, int L, int K, int N, int H, int D,
-    int L_padded, int frequency_batches, int kv_layout, int precision, void* stream);
+    int L_padded, int frequency_batches, int kv_layout, int precision, int kv_round,
+    void* stream);
 
 /* ---------------- flow-block elementwise -------------------------------- */
 /* Bit-identical per element to the reference kernels (same operation order,

@@ -105,7 +105,8 @@ def test_fused_layernorm_modulate_and_head_norm(oracle, cuda):
 
 
 @pytest.mark.parametrize("M,K,N", [(600, 256, 1024), (16384, 1024, 4096), (3000, 4096, 1024), (20, 128, 96),
-                                   (18432, 1024, 1024)])  # whole-round split inside the second gate batch
+                                   (18432, 1024, 1024),   # whole-round split inside the second gate batch
+                                   (16386, 1024, 1024)])  # 2-row tail tile inside the second gate batch
 def test_gemm_epilogues(oracle, cuda, M, K, N):
     """GELU / gated-residual / add epilogues == NF24 Linear then the separate
     elementwise kernel (bit for bit when both use the same GEMM tile, M > 32);
@@ -149,6 +150,13 @@ def test_gemm_epilogues(oracle, cuda, M, K, N):
         assert np.abs(y_gelu.cpu().numpy() - gl).max() <= 1e-5
         exp = base.cpu().numpy() + lin
         assert np.abs(y_add.cpu().numpy() - exp).max() <= 1e-5
+        # gated: base[b] += lin[b] * gate[b] with rows M / B per gate batch
+        gh = np.ascontiguousarray(gate.cpu().numpy())
+        exp_gated = np.ascontiguousarray(base.cpu().numpy())
+        delta = lin.copy()
+        assert oracle.ew("gated_residual_inplace", exp_gated, delta, gh, B, M // B, N) == 0
+        tol = 1e-5 * max(1.0, float(np.abs(gh).max()))
+        assert np.abs(y_gated.cpu().numpy() - exp_gated).max() <= tol
 
 
 def test_sampler_backend_and_flow_of_calls(oracle, cuda):

@@ -84,3 +84,118 @@ def test_graph_sdpa_key_split_tail(cuda):
         native_sdpa_f32_ex(q, k, v, out=out)
     torch.cuda.synchronize(cuda)
     _replays_match(torch, cuda, g, out, expected, lambda: native_sdpa_f32_ex(q, k, v))
+
+
+def _canaries(torch, cuda, n=4, mib=96):
+    """Fresh device allocations filled with a pattern: if the library had
+    freed a buffer a graph still writes to, the caching allocator could hand
+    that memory out here and a replay would overwrite the pattern."""
+    return [torch.full(((mib << 20) // 4,), 1234.5, device=cuda) for _ in range(n)]
+
+
+def test_graph_survives_workspace_growth_gemm(cuda):
+    """Capture a few-row GEMM at a small shape, then grow the capture
+    stream's workspace with a larger eager call on the same stream: the
+    captured buffer is retired, not freed, so replays still equal the eager
+    result bit for bit and no other allocation is written."""
+    import torch
+    from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
+
+    g0 = torch.Generator(device=cuda).manual_seed(5)
+
+    def linear(M, K, N):
+        x = torch.randn((M, K), generator=g0, device=cuda)
+        w = torch.randn((N, K), generator=g0, device=cuda) * 0.02
+        b = torch.randn((N,), generator=g0, device=cuda) * 0.01
+        codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+        return x, codes[0], codes[1], scales[0], b
+
+    small = linear(2, 1024, 3072)     # K split into 32 partials: ~0.8 MB of workspace
+    large = linear(2, 4096, 6144)     # 64 partials of 2 rows: ~3.1 MB
+    expected = nf24_linear(*small)
+    expected_large = nf24_linear(*large)
+    out = torch.empty_like(expected)
+    s = torch.cuda.Stream(device=cuda)
+    torch.cuda.synchronize(cuda)
+    with torch.cuda.stream(s):
+        nf24_linear(*small, out=out)            # sizes s's buffer for the small call
+    torch.cuda.synchronize(cuda)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s, capture_error_mode="relaxed"):
+        nf24_linear(*small, out=out)
+    torch.cuda.synchronize(cuda)
+    with torch.cuda.stream(s):
+        got_large = nf24_linear(*large)        # grows s's buffer: the captured one is retired
+    torch.cuda.synchronize(cuda)
+    assert torch.equal(got_large, expected_large)
+    canaries = _canaries(torch, cuda)
+    torch.cuda.synchronize(cuda)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize(cuda)
+        assert torch.equal(out, expected)
+        with torch.cuda.stream(s):
+            assert torch.equal(nf24_linear(*large), expected_large)
+        torch.cuda.synchronize(cuda)
+    for c in canaries:
+        assert bool((c == 1234.5).all())
+
+
+def test_graph_survives_workspace_growth_sdpa(cuda, hiplib):
+    """The same for the SDPA's key-split partials: capture a call whose
+    split tail needs ~35 MB, grow the stream's buffer past 64 MiB with an
+    eager call of 511 query tiles, then replay."""
+    import ctypes
+
+    import torch
+    from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
+
+    props = torch.cuda.get_device_properties(cuda)
+    if props.multi_processor_count != 256:
+        pytest.skip(f"the split plan assumes 256 CUs, the device has {props.multi_processor_count}")
+    g0 = torch.Generator(device=cuda).manual_seed(6)
+
+    def qkv(H, Lq, Lk):
+        q = torch.nn.functional.normalize(torch.randn((1, H, Lq, 64), generator=g0, device=cuda), dim=-1) * 8
+        k = torch.nn.functional.normalize(torch.randn((1, H, Lk, 64), generator=g0, device=cuda), dim=-1) * 8
+        v = torch.randn((1, H, Lk, 64), generator=g0, device=cuda)
+        return q, k, v
+
+    small = qkv(16, 8704, 1024)      # 272 tiles: 16 split 16 ways (34.6 MB)
+    large = qkv(7, 73 * 512, 128)    # 511 tiles: 255 split 2 ways (68.9 MB)
+    expected = native_sdpa_f32_ex(*small)
+    expected_large = native_sdpa_f32_ex(*large)
+    out = torch.empty_like(expected)
+    s = torch.cuda.Stream(device=cuda)
+    torch.cuda.synchronize(cuda)
+    with torch.cuda.stream(s):
+        native_sdpa_f32_ex(*small, out=out)
+    torch.cuda.synchronize(cuda)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s, capture_error_mode="relaxed"):
+        native_sdpa_f32_ex(*small, out=out)
+    torch.cuda.synchronize(cuda)
+    vals = [ctypes.c_uint64(0) for _ in range(2)]
+    assert hiplib.triposplat_sdpa_q8t512_workspace_stats(*[ctypes.byref(v) for v in vals]) == 0
+    allocations = vals[0].value
+    with torch.cuda.stream(s):
+        got_large = native_sdpa_f32_ex(*large)
+    torch.cuda.synchronize(cuda)
+    assert hiplib.triposplat_sdpa_q8t512_workspace_stats(*[ctypes.byref(v) for v in vals]) == 0
+    assert vals[0].value == allocations + 1        # the large call grew s's buffer
+    assert torch.equal(got_large, expected_large)
+    canaries = _canaries(torch, cuda)
+    torch.cuda.synchronize(cuda)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize(cuda)
+        assert torch.equal(out, expected)
+        with torch.cuda.stream(s):
+            assert torch.equal(native_sdpa_f32_ex(*large), expected_large)
+        torch.cuda.synchronize(cuda)
+    for c in canaries:
+        assert bool((c == 1234.5).all())

@@ -217,7 +217,7 @@ def test_qkv_selected_rows(oracle, cuda, hiplib, B, Lq, Lk, H, fb, Lkp):
     args[3] = d[3].data_ptr()
     assert hiplib.triposplat_q_kv_selected_rope_rmsnorm_pack_f32_avx512_v2(*args, 0) == -3
     assert hiplib.tsplat_q_kv_selected_postprocess_async(
-        *args, torch.cuda.current_stream(cuda).cuda_stream) == 0
+        *args, 0, torch.cuda.current_stream(cuda).cuda_stream) == 0
     torch.cuda.synchronize(cuda)
     qo = outs[0].cpu().numpy()
     row = min(3, Lq - 1)
@@ -244,14 +244,14 @@ def test_device_packer_bit_exact(oracle, cuda, out_f, in_f):
 @pytest.mark.parametrize("mode", ["k", "v", "kv"])
 def test_kv_bf16_round_probe(oracle, cuda, hiplib, mode):
     """The bf16 K/V sensitivity probe (native_qkv_postprocess_bf16_probe_avx512.c):
-    with the mode set, every postprocess form stores k and/or v as the
+    with kv_round=mode, every postprocess form stores k and/or v as the
     nearest bf16 of the exact value -- the oracle's exact outputs passed
     through oracle.bf16_round, bit for bit -- and q and the unselected
-    operand stay exact; the fused projection equals GEMM + postprocess."""
+    operand stay exact; the fused projection equals GEMM + postprocess.
+    The mode is per call: a call without it right after stays exact."""
     import torch
     from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
-    from tsplat.qkv import (gemm_nf24_qkv_direct, kv_bf16_round, q_kv_selected_rope_rmsnorm_pack,
-                            qkv_rope_rmsnorm_pack, set_kv_bf16_round)
+    from tsplat.qkv import gemm_nf24_qkv_direct, q_kv_selected_rope_rmsnorm_pack, qkv_rope_rmsnorm_pack
 
     print(f"kv bf16 round mode={mode}", flush=True)
     B, L, H = 2, 37, 3
@@ -266,38 +266,39 @@ def test_kv_bf16_round_probe(oracle, cuda, hiplib, mode):
     want = (exact[0], oracle.bf16_round(exact[1]) if rk else exact[1],
             oracle.bf16_round(exact[2]) if rv else exact[2])
     assert not np.array_equal(want[1 if rk else 2], exact[1 if rk else 2])   # the rounding is visible
-    assert set_kv_bf16_round(mode) is None
-    try:
-        assert kv_bf16_round() == mode
-        assert hiplib.triposplat_qkv_postprocess_bf16_probe_mode() == {"k": 1, "v": 2, "kv": 3}[mode]
-        got = qkv_rope_rmsnorm_pack(t(qkv), t(fr), t(qg), t(kg), B, L, H)
-        for g_, w_ in zip(got, want):
-            assert np.array_equal(g_.cpu().numpy().view(np.uint32), w_.view(np.uint32))
+    got = qkv_rope_rmsnorm_pack(t(qkv), t(fr), t(qg), t(kg), B, L, H, kv_round=mode)
+    for g_, w_ in zip(got, want):
+        assert np.array_equal(g_.cpu().numpy().view(np.uint32), w_.view(np.uint32))
+    plain = qkv_rope_rmsnorm_pack(t(qkv), t(fr), t(qg), t(kg), B, L, H)
+    for g_, w_ in zip(plain, exact):
+        assert np.array_equal(g_.cpu().numpy().view(np.uint32), w_.view(np.uint32))
 
-        sel = np.sort(r.choice(L, 20, replace=False)).astype(np.int64)
-        qs = r.standard_normal((B, 20, C), dtype=np.float32)
-        kv = np.ascontiguousarray(qkv.reshape(B, L, 3 * C)[..., C:])
-        st, ref = oracle.q_kv_selected_rope_rmsnorm_pack(qs, kv, fr, sel, qg, kg, B, 20, L, H)
-        assert st == 0
-        got = q_kv_selected_rope_rmsnorm_pack(t(qs), t(kv), t(fr), t(sel), t(qg), t(kg), B, 20, L, H)
-        for g_, w_, rnd in zip(got, ref, (False, rk, rv)):
-            w_ = oracle.bf16_round(w_) if rnd else w_
-            assert np.array_equal(g_.cpu().numpy().view(np.uint32), w_.view(np.uint32))
+    sel = np.sort(r.choice(L, 20, replace=False)).astype(np.int64)
+    qs = r.standard_normal((B, 20, C), dtype=np.float32)
+    kv = np.ascontiguousarray(qkv.reshape(B, L, 3 * C)[..., C:])
+    st, ref = oracle.q_kv_selected_rope_rmsnorm_pack(qs, kv, fr, sel, qg, kg, B, 20, L, H)
+    assert st == 0
+    got = q_kv_selected_rope_rmsnorm_pack(t(qs), t(kv), t(fr), t(sel), t(qg), t(kg), B, 20, L, H,
+                                          kv_round=mode)
+    for g_, w_, rnd in zip(got, ref, (False, rk, rv)):
+        w_ = oracle.bf16_round(w_) if rnd else w_
+        assert np.array_equal(g_.cpu().numpy().view(np.uint32), w_.view(np.uint32))
 
-        x = torch.from_numpy(r.standard_normal((B * L, 256), dtype=np.float32)).to(cuda)
-        w = torch.from_numpy((r.standard_normal((3 * C, 256)) * 0.02).astype(np.float32)).to(cuda)
-        bias = torch.zeros(3 * C, device=cuda)
-        codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
-        args = (x, codes[0], codes[1], scales[0], bias, t(fr), t(qg), t(kg), B, L, H)
-        fused = gemm_nf24_qkv_direct(*args)
-        unfused = qkv_rope_rmsnorm_pack(nf24_linear(*args[:5]), *args[5:])
-        bhld = gemm_nf24_qkv_direct(*args, kv_layout="bhld")
-        torch.cuda.synchronize(cuda)
-        for a_, b_ in zip(fused, unfused):
-            assert torch.equal(a_, b_)
-        assert torch.equal(bhld[1], fused[1][..., :L].transpose(2, 3))
-        assert torch.equal(bhld[2], fused[2][..., :L].transpose(2, 3))
-        assert not fused[1][..., L:].any() and not fused[2][..., L:].any()
-    finally:
-        set_kv_bf16_round(None)
+    x = torch.from_numpy(r.standard_normal((B * L, 256), dtype=np.float32)).to(cuda)
+    w = torch.from_numpy((r.standard_normal((3 * C, 256)) * 0.02).astype(np.float32)).to(cuda)
+    bias = torch.zeros(3 * C, device=cuda)
+    codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+    args = (x, codes[0], codes[1], scales[0], bias, t(fr), t(qg), t(kg), B, L, H)
+    fused = gemm_nf24_qkv_direct(*args, kv_round=mode)
+    unfused = qkv_rope_rmsnorm_pack(nf24_linear(*args[:5]), *args[5:], kv_round=mode)
+    bhld = gemm_nf24_qkv_direct(*args, kv_layout="bhld", kv_round=mode)
+    exact_fused = gemm_nf24_qkv_direct(*args)
+    torch.cuda.synchronize(cuda)
+    for a_, b_ in zip(fused, unfused):
+        assert torch.equal(a_, b_)
+    assert torch.equal(bhld[1], fused[1][..., :L].transpose(2, 3))
+    assert torch.equal(bhld[2], fused[2][..., :L].transpose(2, 3))
+    assert not fused[1][..., L:].any() and not fused[2][..., L:].any()
+    assert torch.equal(exact_fused[0], fused[0])
+    assert not torch.equal(exact_fused[1 if rk else 2], fused[1 if rk else 2])
     assert hiplib.triposplat_qkv_postprocess_bf16_probe_mode() == 0

@@ -18,10 +18,13 @@
 namespace tsplat {
 namespace {
 std::atomic<int> g_last_hip_error{0};
-// bf16 rounding of the stored k (bit 0) and v (bit 1) applied by every QKV
-// postprocess entry; 0 (exact) unless tsplat_set_qkv_bf16_round changes it.
-std::atomic<int> g_kv_round{0};
+std::atomic<int> g_sdpa_query_tile{512};
 }  // namespace
+
+void note_sdpa_query_tile(int queries) {
+  g_sdpa_query_tile.store(queries, std::memory_order_relaxed);
+}
+int sdpa_query_tile() { return g_sdpa_query_tile.load(std::memory_order_relaxed); }
 
 int note(hipError_t e) {
   if (e != hipSuccess) g_last_hip_error.store((int)e);
@@ -67,10 +70,16 @@ using namespace tsplat;
 namespace {
 
 constexpr int kHeadDim = 64;
-constexpr int kAbiVersion = 2;
+constexpr int kAbiVersion = 3;
 
+// Profile of the blocking (reference-named) SDPA calls: calls, host time
+// spent growing the key-split workspace (allocate), the rest of the call up
+// to the device's completion (compute), and workspace release (free).
+// There is no pack step: the kernel reads [B, H, L, 64] k/v in place.
 std::atomic<uint64_t> g_sdpa_calls{0};
 std::atomic<uint64_t> g_sdpa_ns{0};
+std::atomic<uint64_t> g_sdpa_alloc_ns{0};
+std::atomic<uint64_t> g_sdpa_free_ns{0};
 
 // ---------------------------------------------------------------- GEMM
 int gemm_checked(const float* x, const int16_t* code01, const int8_t* q2, const float* scale,
@@ -125,15 +134,20 @@ int sdpa_blocking(const float* q, const float* k, const float* v, const float* b
                   int B, int H, int Lq, int Lk, int D, int has_bias, int bias_len, int kv_packed,
                   int Lkp, int out_blhd) {
   const auto t0 = std::chrono::steady_clock::now();
+  uint64_t alloc_ns0 = 0, alloc_ns1 = 0;
+  workspace_timing(kSlotSdpaPartial, &alloc_ns0, nullptr);
   int st = sdpa_checked(q, k, v, bias, out, B, H, Lq, Lk, D, has_bias, bias_len, 0, kv_packed,
                         Lkp, out_blhd, nullptr);
   if (st == kOk) st = sync_null_stream();
   if (st == kOk) {
     const auto t1 = std::chrono::steady_clock::now();
+    workspace_timing(kSlotSdpaPartial, &alloc_ns1, nullptr);
+    const uint64_t total =
+        (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
+    const uint64_t alloc = alloc_ns1 - alloc_ns0;
     g_sdpa_calls.fetch_add(1, std::memory_order_relaxed);
-    g_sdpa_ns.fetch_add(
-        (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count(),
-        std::memory_order_relaxed);
+    g_sdpa_alloc_ns.fetch_add(alloc, std::memory_order_relaxed);
+    g_sdpa_ns.fetch_add(total > alloc ? total - alloc : 0, std::memory_order_relaxed);
   }
   return st;
 }
@@ -141,8 +155,9 @@ int sdpa_blocking(const float* q, const float* k, const float* v, const float* b
 // ---------------------------------------------------------------- QKV
 int post_checked(const float* qkv, const float* freqs, const float* qg, const float* kg,
                  float* q, float* pk, float* pv, int B, int L, int H, int D, int Lp, int fb,
-                 hipStream_t stream) {
+                 hipStream_t stream, int kv_round = 0) {
   if (!qkv || !freqs || !qg || !kg || !q || !pk || !pv) return kErrNull;
+  if (kv_round < 0 || kv_round > 3) return kErrDims;
   if (B <= 0 || L <= 0 || H <= 0 || D != kHeadDim || Lp < L || (Lp & 15) != 0 ||
       (fb != 1 && fb != B))
     return kErrDims;
@@ -157,8 +172,7 @@ int post_checked(const float* qkv, const float* freqs, const float* qg, const fl
   TSPLAT_CHECK(check_dev(q, (int64_t)B * L * C * 4));
   TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * Lp * 4));
   TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lp * 4));
-  QkvPostParams p{qkv, freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb};
-  p.kv_round = g_kv_round.load(std::memory_order_relaxed);
+  QkvPostParams p{qkv, freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb, kv_round};
   const int st = launch_qkv_postprocess(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
   return st;
@@ -166,8 +180,10 @@ int post_checked(const float* qkv, const float* freqs, const float* qg, const fl
 
 int selected_checked(const float* q, const float* kv, const float* freqs, const int64_t* sel,
                      const float* qg, const float* kg, float* q_out, float* pk, float* pv, int B,
-                     int Lq, int Lk, int H, int D, int Lkp, int fb, hipStream_t stream) {
+                     int Lq, int Lk, int H, int D, int Lkp, int fb, hipStream_t stream,
+                     int kv_round = 0) {
   if (!q || !kv || !freqs || !sel || !qg || !kg || !q_out || !pk || !pv) return kErrNull;
+  if (kv_round < 0 || kv_round > 3) return kErrDims;
   if (B <= 0 || Lq <= 0 || Lk <= 0 || H <= 0 || D != kHeadDim || Lkp < Lk || (Lkp & 15) != 0 ||
       (fb != 1 && fb != B))
     return kErrDims;
@@ -182,8 +198,7 @@ int selected_checked(const float* q, const float* kv, const float* freqs, const 
   TSPLAT_CHECK(check_dev(q_out, (int64_t)B * Lq * C * 4));
   TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * Lkp * 4));
   TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lkp * 4));
-  QkvSelectedParams p{q, kv, freqs, sel, qg, kg, q_out, pk, pv, B, Lq, Lk, H, Lkp, fb};
-  p.kv_round = g_kv_round.load(std::memory_order_relaxed);
+  QkvSelectedParams p{q, kv, freqs, sel, qg, kg, q_out, pk, pv, B, Lq, Lk, H, Lkp, fb, kv_round};
   const int st = launch_qkv_selected_postprocess(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
   return st;
@@ -193,9 +208,10 @@ int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
                        const float* scale, const float* bias, const float* freqs,
                        const float* qg, const float* kg, float* q, float* pk, float* pv, int B,
                        int L, int K, int N, int H, int D, int Lp, int fb, hipStream_t stream,
-                       int precision = kPrecisionFp32, int kv_layout = 0) {
+                       int precision = kPrecisionFp32, int kv_layout = 0, int kv_round = 0) {
   if (!x || !code01 || !q2 || !scale || !bias || !freqs || !qg || !kg || !q || !pk || !pv)
     return kErrNull;
+  if (kv_round < 0 || kv_round > 3) return kErrDims;
   if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
     return kErrDims;
   if (kv_layout != 0 && kv_layout != 1) return kErrDims;
@@ -221,8 +237,7 @@ int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
   TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * kv_keys * 4));
   // RoPE, RMSNorm and the q / packed k,v stores run in the GEMM's epilogue.
   QkvFusedParams p{{x, code01, q2, scale, bias, nullptr, (int)M, K, N, 0, N, K, N, precision},
-                   freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb, kv_layout};
-  p.kv_round = g_kv_round.load(std::memory_order_relaxed);
+                   freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb, kv_layout, kv_round};
   const int st = launch_nf24_gemm_qkv(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
   return st;
@@ -333,33 +348,42 @@ int triposplat_sdpa_f32_avx512_exact_q8t512_packed_blhd(
 }
 
 int triposplat_sdpa_key_tile(void) { return 64; }
-int triposplat_sdpa_query_block(void) { return 128; }
+int triposplat_sdpa_query_block(void) { return sdpa_query_tile(); }
 int triposplat_sdpa_packed_output_is_blhd(void) { return 1; }
 
 void triposplat_sdpa_q8t512_profile_reset(void) {
   g_sdpa_calls.store(0);
   g_sdpa_ns.store(0);
+  g_sdpa_alloc_ns.store(0);
+  g_sdpa_free_ns.store(0);
 }
 
 int triposplat_sdpa_q8t512_profile_get(uint64_t* calls, uint64_t* allocate_ns, uint64_t* pack_ns,
                                        uint64_t* compute_ns, uint64_t* free_ns) {
   if (!calls || !allocate_ns || !pack_ns || !compute_ns || !free_ns) return kErrNull;
   *calls = g_sdpa_calls.load();
-  *allocate_ns = 0;
+  *allocate_ns = g_sdpa_alloc_ns.load();
   *pack_ns = 0;
   *compute_ns = g_sdpa_ns.load();
-  *free_ns = 0;
+  *free_ns = g_sdpa_free_ns.load();
   return kOk;
 }
 
 int triposplat_sdpa_q8t512_workspace_stats(uint64_t* allocations, uint64_t* capacity_bytes) {
   if (!allocations || !capacity_bytes) return kErrNull;
-  *allocations = 0;
-  *capacity_bytes = 0;
+  uint64_t retired = 0;
+  workspace_stats(kSlotSdpaPartial, allocations, capacity_bytes, &retired);
   return kOk;
 }
 
-void triposplat_sdpa_q8t512_workspace_release(void) {}
+void triposplat_sdpa_q8t512_workspace_release(void) {
+  const auto t0 = std::chrono::steady_clock::now();
+  release_workspace(kSlotSdpaPartial);
+  g_sdpa_free_ns.fetch_add((uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+                               std::chrono::steady_clock::now() - t0)
+                               .count(),
+                           std::memory_order_relaxed);
+}
 
 int tsplat_sdpa_async(const float* q, const float* k, const float* v,
                       const float* key_bias_or_null, float* out, int B, int H, int Lq, int Lk,
@@ -406,17 +430,9 @@ int triposplat_qkv_rope_rmsnorm_pack_f32_avx512(const float* qkv, const float* f
                                                         L_padded, frequency_batches, threads);
 }
 
-// Selects the bf16 rounding of stored k (bit 0) / v (bit 1) for all later
-// QKV postprocess calls of the process.
-int tsplat_set_qkv_bf16_round(int mode) {
-  if (mode < 0 || mode > 3) return kErrDims;
-  g_kv_round.store(mode, std::memory_order_relaxed);
-  return kOk;
-}
-
-int triposplat_qkv_postprocess_bf16_probe_mode(void) {
-  return g_kv_round.load(std::memory_order_relaxed);
-}
+// The reference-named postprocess entries of this library store k and v
+// exactly (the probe's rounding is the per-call kv_round of the async forms).
+int triposplat_qkv_postprocess_bf16_probe_mode(void) { return 0; }
 
 // Tokens per workgroup of the postprocess kernel's k/v transpose.
 int triposplat_qkv_postprocess_token_tile(void) { return 64; }
@@ -473,10 +489,10 @@ int tsplat_q_kv_selected_postprocess_async(const float* q, const float* kv,
                                            const float* q_gamma, const float* k_gamma,
                                            float* q_bhld, float* packed_k, float* packed_v, int B,
                                            int Lq, int Lk, int H, int D, int Lk_padded,
-                                           int frequency_batches, void* stream) {
+                                           int frequency_batches, int kv_round, void* stream) {
   return selected_checked(q, kv, frequencies, selected_indices, q_gamma, k_gamma, q_bhld, packed_k,
                           packed_v, B, Lq, Lk, H, D, Lk_padded, frequency_batches,
-                          static_cast<hipStream_t>(stream));
+                          static_cast<hipStream_t>(stream), kv_round);
 }
 
 int triposplat_gemm_nf24_qkv_direct_row_tile(void) { return 128; }
@@ -487,9 +503,9 @@ int triposplat_gemm_nf24_qkv_direct_residual_mode(void) { return 4; }
 int tsplat_qkv_postprocess_async(const float* qkv, const float* frequencies, const float* q_gamma,
                                  const float* k_gamma, float* q_bhld, float* packed_k,
                                  float* packed_v, int B, int L, int H, int D, int L_padded,
-                                 int frequency_batches, void* stream) {
+                                 int frequency_batches, int kv_round, void* stream) {
   return post_checked(qkv, frequencies, q_gamma, k_gamma, q_bhld, packed_k, packed_v, B, L, H, D,
-                      L_padded, frequency_batches, static_cast<hipStream_t>(stream));
+                      L_padded, frequency_batches, static_cast<hipStream_t>(stream), kv_round);
 }
 
 int tsplat_gemm_nf24_qkv_direct_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,
@@ -507,10 +523,11 @@ int tsplat_gemm_nf24_qkv_direct_ex_async(
     const float* x, const int16_t* code01_t, const int8_t* q2_t, const float* scale,
     const float* bias, const float* frequencies, const float* q_gamma, const float* k_gamma,
     float* q_bhld, float* k_out, float* v_out, int B, int L, int K, int N, int H, int D,
-    int L_padded, int frequency_batches, int kv_layout, int precision, void* stream) {
+    int L_padded, int frequency_batches, int kv_layout, int precision, int kv_round,
+    void* stream) {
   return qkv_direct_checked(x, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, q_bhld,
                             k_out, v_out, B, L, K, N, H, D, L_padded, frequency_batches,
-                            static_cast<hipStream_t>(stream), precision, kv_layout);
+                            static_cast<hipStream_t>(stream), precision, kv_layout, kv_round);
 }
 
 // ------------------------------------------------------------------ packer

@@ -192,6 +192,7 @@ int launch_tiles(SdpaArgs a, const SdpaParams& p, int kBQ, int kBKV, int cus, hi
                  Main&& main) {
   const int64_t tiles = (int64_t)p.B * p.H * ((p.Lq + kBQ - 1) / kBQ);
   if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
+  note_sdpa_query_tile(kBQ);
   int64_t grid_n = tiles;
   a.full_tiles = (int)tiles;
   a.splits = 1;

@@ -56,6 +56,9 @@ struct SdpaParams {
   int precision = kPrecisionFp32;
 };
 int launch_sdpa(const SdpaParams& p, hipStream_t stream);
+// Queries per workgroup of the most recent SDPA launch (512 before any).
+void note_sdpa_query_tile(int queries);
+int sdpa_query_tile();
 // The bf16-MFMA modes (called by launch_sdpa for precision != fp32).
 int launch_sdpa_bf16(const SdpaParams& p, hipStream_t stream);
 
@@ -190,10 +193,20 @@ int launch_nf24_pack(const float* w, int out_f, int in_f, const float* alphabet,
 int launch_nf24_decode(const int16_t* code01_t, const int8_t* q2_t, const float* scale, float* out,
                        int in_f, int out_f, int transposed, hipStream_t stream);
 
-// Grow-only device scratch owned by the library, one buffer per (device,
-// stream, slot); null on allocation failure.  Valid until the next call with
-// the same key that asks for more bytes.
+// Device scratch owned by the library, one grow-only buffer per (device,
+// stream, slot); null on allocation failure, or when the stream is under
+// graph capture and its buffer is too small.  The policy (reuse, free after
+// the stream, retire a buffer a capture recorded) is in workspace_pool.h.
 enum WorkspaceSlot : int { kSlotGemvPartial = 0, kSlotSdpaPartial = 1 };
 void* stream_workspace(hipStream_t stream, size_t bytes, int slot);
+// Frees the slot's buffers of the current device that no capture recorded
+// (after their streams) and retires the others.
+void release_workspace(int slot);
+// Buffers allocated for the slot so far, bytes of its current buffers, and
+// bytes of superseded buffers kept alive for captured graphs.
+void workspace_stats(int slot, uint64_t* allocations, uint64_t* live_bytes,
+                     uint64_t* retired_bytes);
+// Host time the slot has spent allocating, and waiting for streams + freeing.
+void workspace_timing(int slot, uint64_t* alloc_ns, uint64_t* free_ns);
 
 }  // namespace tsplat

@@ -1,64 +1,86 @@
 // Per-stream device workspaces for kernels that need scratch memory: the
 // split-K partial sums of the few-row GEMM and the key-split partials of the
 // SDPA tail.  Every user overwrites the part it reads, so buffers are not
-// cleared.
-//
-// One grow-only buffer per (device, stream, slot).  Calls on one stream are
-// ordered by the stream, so they may share its buffer; calls on different
-// streams get different buffers.  Growing waits for the stream before the
-// old buffer is released.  A stream under HIP-graph capture cannot allocate
-// or wait, so a call there that needs a larger buffer fails (the caller
-// returns -5); one eager call of the same or a larger shape on that stream
-// beforehand provides the buffer.  Buffers live until the process ends.
+// cleared.  The grow / free / retire policy is WorkspacePool's
+// (workspace_pool.h); this file supplies the HIP operations and a lock.
 
 #include <hip/hip_runtime.h>
 
-#include <map>
+#include <chrono>
 #include <mutex>
-#include <tuple>
 
 #include "tsplat_launch.h"
+#include "workspace_pool.h"
 
 namespace tsplat {
 namespace {
 
-struct Buffer {
-  void* ptr = nullptr;
-  size_t bytes = 0;
+struct HipOps {
+  void* alloc(size_t bytes) {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    return p;
+  }
+  void free(void* p) { (void)hipFree(p); }
+  bool sync(hipStream_t s) { return hipStreamSynchronize(s) == hipSuccess; }
+  uint64_t now_ns() {
+    return (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+               std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+  }
 };
 
+using Pool = WorkspacePool<hipStream_t, HipOps>;
+static_assert(kSlotSdpaPartial < Pool::kSlots, "workspace slot out of range");
+
 std::mutex g_mu;
-std::map<std::tuple<int, hipStream_t, int>, Buffer>* g_buffers = nullptr;
+// Never destroyed: retired buffers stay valid for graphs until the process
+// ends, and the HIP runtime may be gone by the time static destructors run.
+Pool* g_pool = nullptr;
+
+Pool& pool() {
+  if (g_pool == nullptr) g_pool = new Pool(HipOps{});
+  return *g_pool;
+}
 
 }  // namespace
 
 void* stream_workspace(hipStream_t stream, size_t bytes, int slot) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  std::lock_guard<std::mutex> lock(g_mu);
-  if (g_buffers == nullptr) g_buffers = new std::map<std::tuple<int, hipStream_t, int>, Buffer>();
-  Buffer& b = (*g_buffers)[std::make_tuple(dev, stream, slot)];
-  if (b.bytes >= bytes && b.ptr != nullptr) return b.ptr;
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
   }
-  if (capture != hipStreamCaptureStatusNone) return nullptr;
-  if (b.ptr != nullptr) {
-    if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
-    (void)hipFree(b.ptr);
-    b.ptr = nullptr;
-    b.bytes = 0;
-  }
-  const size_t want = bytes < 256 ? 256 : bytes;
-  if (hipMalloc(&b.ptr, want) != hipSuccess) {
-    (void)hipGetLastError();
-    b.ptr = nullptr;
-    return nullptr;
-  }
-  b.bytes = want;
-  return b.ptr;
+  std::lock_guard<std::mutex> lock(g_mu);
+  return pool().acquire(dev, stream, slot, bytes, capture != hipStreamCaptureStatusNone);
+}
+
+void release_workspace(int slot) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  std::lock_guard<std::mutex> lock(g_mu);
+  pool().release(dev, slot);
+}
+
+void workspace_stats(int slot, uint64_t* allocations, uint64_t* live_bytes,
+                     uint64_t* retired_bytes) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  const WorkspaceSlotStats s = pool().stats(slot);
+  if (allocations) *allocations = s.allocations;
+  if (live_bytes) *live_bytes = s.live_bytes;
+  if (retired_bytes) *retired_bytes = s.retired_bytes;
+}
+
+void workspace_timing(int slot, uint64_t* alloc_ns, uint64_t* free_ns) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  const WorkspaceSlotStats s = pool().stats(slot);
+  if (alloc_ns) *alloc_ns = s.alloc_ns;
+  if (free_ns) *free_ns = s.free_ns;
 }
 
 }  // namespace tsplat

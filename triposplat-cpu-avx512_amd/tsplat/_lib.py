@@ -42,17 +42,16 @@ SIGNATURES = {
     "triposplat_qkv_rope_rmsnorm_pack_f32_avx512": ([_vp] * 7 + [_i] * 7, _i),
     "triposplat_qkv_postprocess_token_tile": ([], _i),
     "triposplat_qkv_postprocess_v2_tail_only_clear": ([], _i),
-    "tsplat_set_qkv_bf16_round": ([_i], _i),
     "triposplat_qkv_postprocess_bf16_probe_mode": ([], _i),
     "triposplat_gemm_nf24_qkv_rope_rmsnorm_pack_f32_avx512": ([_vp] * 15 + [_i] * 10, _i),
     "triposplat_gemm_nf24_qkv_direct_row_tile": ([], _i),
     "triposplat_gemm_nf24_qkv_direct_tile_bytes": ([], _i),
     "triposplat_gemm_nf24_qkv_direct_residual_mode": ([], _i),
     "triposplat_q_kv_selected_rope_rmsnorm_pack_f32_avx512_v2": ([_vp] * 9 + [_i] * 8, _i),
-    "tsplat_q_kv_selected_postprocess_async": ([_vp] * 9 + [_i] * 7 + [_vp], _i),
-    "tsplat_qkv_postprocess_async": ([_vp] * 7 + [_i] * 6 + [_vp], _i),
+    "tsplat_q_kv_selected_postprocess_async": ([_vp] * 9 + [_i] * 8 + [_vp], _i),
+    "tsplat_qkv_postprocess_async": ([_vp] * 7 + [_i] * 7 + [_vp], _i),
     "tsplat_gemm_nf24_qkv_direct_async": ([_vp] * 11 + [_i] * 8 + [_vp], _i),
-    "tsplat_gemm_nf24_qkv_direct_ex_async": ([_vp] * 11 + [_i] * 10 + [_vp], _i),
+    "tsplat_gemm_nf24_qkv_direct_ex_async": ([_vp] * 11 + [_i] * 11 + [_vp], _i),
     "tsplat_nf24_pack_async": ([_vp, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp], _i),
     "tsplat_nf24_decode_async": ([_vp] * 4 + [_i] * 3 + [_vp], _i),
     "tsplat_nf24_gemm_epilogue_async": ([_vp] * 6 + [_i] * 8 + [_vp, _i64, _i, _vp], _i),

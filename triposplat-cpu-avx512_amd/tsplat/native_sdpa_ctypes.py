@@ -1,12 +1,17 @@
 """Exact SDPA entry point: the device counterpart of the reference's
 scripts/native_sdpa_ctypes.py:23-76 (``native_sdpa_f32``).
 
-Same name, keyword arguments and error behaviour, with the device check
+Same name, keyword arguments, default symbol
+(``triposplat_sdpa_f32_avx512_exact_q8``, overridable by ``symbol=`` or
+TRIPOSPLAT_NATIVE_SDPA_SYMBOL) and error behaviour, with the device check
 flipped: q/k/v must be GPU tensors (the reference raises on non-CPU tensors,
-this raises on non-GPU ones).  Inputs are cast to fp32 and made contiguous,
-``out`` is allocated here, and the kernel is enqueued on torch's current
-stream, so the result is ordered with the surrounding torch work.  A nonzero
-kernel status raises RuntimeError; nothing falls back to torch.
+this raises on non-GPU ones).  Inputs are cast to fp32 and made contiguous
+and ``out`` is allocated here.  A reference-named symbol is blocking, as the
+CPU call was: torch's current stream is waited for, the kernel runs on the
+null stream and the call returns once it has finished.  The symbol
+``tsplat_sdpa_async`` instead enqueues on torch's current stream and returns
+at once.  A nonzero kernel status raises RuntimeError; nothing falls back to
+torch.
 
 ``native_sdpa_f32_ex`` adds what the device path offers beyond the reference
 ABI: a per-head key bias [H, Lk], key-contiguous packed K/V [B, H, 64, Lkp]
@@ -18,7 +23,7 @@ import os
 
 from ._lib import check_status, current_stream_handle, load_library
 
-DEFAULT_SYMBOL = "tsplat_sdpa_async"
+DEFAULT_SYMBOL = "triposplat_sdpa_f32_avx512_exact_q8"
 
 
 def _as_f32_contig(t):

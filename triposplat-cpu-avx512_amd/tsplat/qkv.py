@@ -14,26 +14,19 @@ from __future__ import annotations
 from ._lib import check_status, current_stream_handle, load_library
 
 
+# bf16 rounding of the stored k and/or v (the K/V sensitivity probe,
+# scripts/native_qkv_postprocess_bf16_probe_avx512.c:34-94, whose three builds
+# scripts/build_native_qkv_postprocess_bf16_probe_avx512.sh selects with
+# BF16_TARGET): None stores them exact (the default), "k", "v" or "kv" round
+# them to the nearest bf16 after the exact computation.  Per call: no other
+# call's numerics change.
 KV_BF16_ROUND_MODES = {None: 0, "k": 1, "v": 2, "kv": 3}
 
 
-def set_kv_bf16_round(mode, *, library=None):
-    """Process-wide bf16 rounding of the k and/or v that every QKV
-    postprocess form stores: None (exact, the default), "k", "v" or "kv" --
-    the three builds of scripts/build_native_qkv_postprocess_bf16_probe_avx512.sh
-    (BF16_TARGET), as one switch.  Returns the previous mode."""
+def kv_round_id(mode) -> int:
     if mode not in KV_BF16_ROUND_MODES:
-        raise ValueError(f"kv bf16 round mode must be one of {sorted(KV_BF16_ROUND_MODES, key=str)}")
-    lib = load_library(library)
-    previous = kv_bf16_round(library=library)
-    check_status(lib.tsplat_set_qkv_bf16_round(KV_BF16_ROUND_MODES[mode]), "tsplat_set_qkv_bf16_round")
-    return previous
-
-
-def kv_bf16_round(*, library=None):
-    """The current mode (triposplat_qkv_postprocess_bf16_probe_mode)."""
-    bits = load_library(library).triposplat_qkv_postprocess_bf16_probe_mode()
-    return {v: k for k, v in KV_BF16_ROUND_MODES.items()}[bits]
+        raise ValueError(f"kv_round must be one of {sorted(KV_BF16_ROUND_MODES, key=str)}")
+    return KV_BF16_ROUND_MODES[mode]
 
 
 def padded_length(L: int) -> int:
@@ -52,10 +45,13 @@ def _check(torch, name, t):
         raise ValueError(f"{name} must be a contiguous fp32 GPU tensor")
 
 
-def qkv_rope_rmsnorm_pack(qkv, frequencies, q_gamma, k_gamma, B, L, H, *, L_padded=None, library=None):
-    """qkv [B*L, 3*H*64]; frequencies [fb, L, H, 64] (cos, sin pairs), fb in {1, B}."""
+def qkv_rope_rmsnorm_pack(qkv, frequencies, q_gamma, k_gamma, B, L, H, *, L_padded=None, kv_round=None,
+                          library=None):
+    """qkv [B*L, 3*H*64]; frequencies [fb, L, H, 64] (cos, sin pairs), fb in {1, B};
+    kv_round: the bf16 probe mode of the stored k/v (None = exact)."""
     import torch
 
+    rnd = kv_round_id(kv_round)
     for name, t in (("qkv", qkv), ("frequencies", frequencies), ("q_gamma", q_gamma), ("k_gamma", k_gamma)):
         _check(torch, name, t)
     Lp = padded_length(L) if L_padded is None else int(L_padded)
@@ -65,23 +61,25 @@ def qkv_rope_rmsnorm_pack(qkv, frequencies, q_gamma, k_gamma, B, L, H, *, L_padd
         status = lib.tsplat_qkv_postprocess_async(
             qkv.data_ptr(), frequencies.data_ptr(), q_gamma.data_ptr(), k_gamma.data_ptr(),
             q.data_ptr(), pk.data_ptr(), pv.data_ptr(), int(B), int(L), int(H), 64, Lp,
-            int(frequencies.shape[0]), current_stream_handle(qkv.device),
+            int(frequencies.shape[0]), rnd, current_stream_handle(qkv.device),
         )
     check_status(status, "tsplat_qkv_postprocess_async")
     return q, pk, pv
 
 
 def gemm_nf24_qkv_direct(x2, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, B, L, H, *,
-                         L_padded=None, precision="fp32", kv_layout="packed", library=None):
+                         L_padded=None, precision="fp32", kv_layout="packed", kv_round=None, library=None):
     """NF24 QKV projection of x2 [B*L, K] (N = 3*H*64) then the postprocess;
     precision of the projection as tsplat.nf24.nf24_linear.  kv_layout
     "packed" returns k/v [B, H, 64, L_padded] (the reference's layout),
-    "bhld" returns k/v [B, H, L, 64] like q (what the unpacked SDPA reads)."""
+    "bhld" returns k/v [B, H, L, 64] like q (what the unpacked SDPA reads).
+    kv_round: the bf16 probe mode of the stored k/v (None = exact)."""
     import torch
 
     from .nf24 import precision_id
 
     mode = precision_id(precision)
+    rnd = kv_round_id(kv_round)
     if kv_layout not in ("packed", "bhld"):
         raise ValueError(f"kv_layout must be 'packed' or 'bhld', not {kv_layout!r}")
     for name, t in (("x", x2), ("frequencies", frequencies), ("q_gamma", q_gamma), ("k_gamma", k_gamma)):
@@ -98,23 +96,26 @@ def gemm_nf24_qkv_direct(x2, code01_t, q2_t, scale, bias, frequencies, q_gamma, 
                 pv.data_ptr(), int(B), int(L), int(x2.shape[1]), int(code01_t.shape[1]), int(H), 64, Lp,
                 int(frequencies.shape[0]))
         stream = current_stream_handle(x2.device)
-        if mode == 0 and kv_layout == "packed":
+        if mode == 0 and kv_layout == "packed" and rnd == 0:
             name, status = "tsplat_gemm_nf24_qkv_direct_async", lib.tsplat_gemm_nf24_qkv_direct_async(*args, stream)
         else:
             name = "tsplat_gemm_nf24_qkv_direct_ex_async"
-            status = lib.tsplat_gemm_nf24_qkv_direct_ex_async(*args, int(kv_layout == "bhld"), mode, stream)
+            status = lib.tsplat_gemm_nf24_qkv_direct_ex_async(*args, int(kv_layout == "bhld"), mode, rnd,
+                                                                stream)
     check_status(status, name)
     return q, pk, pv
 
 
 def q_kv_selected_rope_rmsnorm_pack(q, kv, frequencies, selected_indices, q_gamma, k_gamma, B, Lq, Lk, H,
-                                    *, L_padded=None, library=None):
+                                    *, L_padded=None, kv_round=None, library=None):
     """Selected query rows (scripts/native_qkv_postprocess_v2_avx512.c:107-191):
     q [B, Lq, H*64] from a Q-only projection, kv [B, Lk, 2*H*64] = [k | v];
     query t is rotated with frequency row selected_indices[t] (int64 GPU
-    tensor).  Returns q [B, H, Lq, 64] and packed k/v [B, H, 64, L_padded]."""
+    tensor).  Returns q [B, H, Lq, 64] and packed k/v [B, H, 64, L_padded].
+    kv_round: the bf16 probe mode of the stored k/v (None = exact)."""
     import torch
 
+    rnd = kv_round_id(kv_round)
     for name, t in (("q", q), ("kv", kv), ("frequencies", frequencies), ("q_gamma", q_gamma),
                     ("k_gamma", k_gamma)):
         _check(torch, name, t)
@@ -130,7 +131,7 @@ def q_kv_selected_rope_rmsnorm_pack(q, kv, frequencies, selected_indices, q_gamm
         status = lib.tsplat_q_kv_selected_postprocess_async(
             q.data_ptr(), kv.data_ptr(), frequencies.data_ptr(), selected_indices.data_ptr(),
             q_gamma.data_ptr(), k_gamma.data_ptr(), qo.data_ptr(), pk.data_ptr(), pv.data_ptr(),
-            int(B), int(Lq), int(Lk), int(H), 64, Lp, int(frequencies.shape[0]),
+            int(B), int(Lq), int(Lk), int(H), 64, Lp, int(frequencies.shape[0]), rnd,
             current_stream_handle(q.device),
         )
     check_status(status, "tsplat_q_kv_selected_postprocess_async")
