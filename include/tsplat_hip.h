@@ -18,7 +18,8 @@
  * -3 range, stride or key-bias length mismatch; -4 range not 16-aligned (or a
  * pointer not 16-byte aligned where float4 access is required); -5 device
  * workspace allocation failed; -6 not device memory / allocation too small /
- * other device; -7 HIP launch or runtime error (tsplat_last_hip_error()).
+ * other device; -7 HIP launch or runtime error (tsplat_last_hip_error());
+ * -8 the no-allocation SDPA entry's static scratch is too small for the call.
  *
  * Weight format NF24 (residual mode 4): w[k][n] = fp32((int32)code01[k][n] *
  * 256 + q2[k][n]) * scale[n], code01 int16 [K][N], q2 int8 [K][N], scale fp32
@@ -136,6 +137,22 @@ int tsplat_sdpa_precision_async(const float* q, const float* k, const float* v,
                                 int Lk, int D, int has_key_bias, int key_bias_len,
                                 int64_t bias_head_stride, int kv_packed, int Lkp, int out_blhd,
                                 int precision, void* stream);
+
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  tsplat_sdpa_precision_async, same arguments and
+ * result, calling no hipMalloc / hipFree: the key-split partials of a
+ * partial last round of query tiles go to a static 66 MiB device array
+ * instead of the library's per-stream workspace.  That holds every launch
+ * plan of a 256-CU device; a call that would need more returns -8 before any
+ * launch.  The array is per GPU and shared by all calls on it, whatever the
+ * stream: calls that overlap in time on one GPU race and must be ordered by
+ * the caller. */
+int tsplat_sdpa_noalloc_async(const float* q, const float* k, const float* v,
+                              const float* key_bias_or_null, float* out, int B, int H, int Lq,
+                              int Lk, int D, int has_key_bias, int key_bias_len,
+                              int64_t bias_head_stride, int kv_packed, int Lkp, int out_blhd,
+                              int precision, void* stream);
 
 /* ---------------- QKV RoPE -> RMSNorm -> pack -------------------------- */
 

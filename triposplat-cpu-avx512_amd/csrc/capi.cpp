@@ -17,6 +17,7 @@
 
 namespace tsplat {
 namespace {
+constexpr int kSdpaHeadDim = 64;
 std::atomic<int> g_last_hip_error{0};
 std::atomic<int> g_sdpa_query_tile{512};
 }  // namespace
@@ -63,6 +64,33 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 int sync_null_stream() { return note(hipStreamSynchronize(nullptr)); }
 
+int sdpa_checked(const float* q, const float* k, const float* v, const float* bias, float* out,
+                 int B, int H, int Lq, int Lk, int D, int has_bias, int bias_len,
+                 int64_t bias_head_stride, int kv_packed, int Lkp, int out_blhd,
+                 hipStream_t stream, int precision, float* scratch, size_t scratch_bytes) {
+  if (!q || !k || !v || !out) return kErrNull;
+  if (B <= 0 || H <= 0 || Lq <= 0 || Lk <= 0 || D != kSdpaHeadDim) return kErrDims;
+  if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
+    return kErrDims;
+  if (kv_packed != 0 && kv_packed != 1) return kErrDims;
+  if (kv_packed && (Lkp < Lk || (Lkp & 15) != 0)) return kErrDims;
+  if (has_bias && (bias == nullptr || bias_len != Lk)) return kErrRange;
+  if (has_bias && bias_head_stride != 0 && bias_head_stride < Lk) return kErrRange;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return kErrAlign;
+  const int64_t bh = (int64_t)B * H;
+  TSPLAT_CHECK(check_dev(q, bh * Lq * kSdpaHeadDim * 4));
+  const int64_t kv_elems = kv_packed ? bh * kSdpaHeadDim * Lkp : bh * Lk * kSdpaHeadDim;
+  TSPLAT_CHECK(check_dev(k, kv_elems * 4));
+  TSPLAT_CHECK(check_dev(v, kv_elems * 4));
+  TSPLAT_CHECK(check_dev(out, bh * Lq * kSdpaHeadDim * 4));
+  if (has_bias) TSPLAT_CHECK(check_dev(bias, ((int64_t)(H - 1) * bias_head_stride + Lk) * 4));
+  SdpaParams p{q, k, v, has_bias ? bias : nullptr, out, B, H, Lq, Lk, kv_packed, Lkp,
+               bias_head_stride, out_blhd, precision, scratch, scratch_bytes};
+  const int st = launch_sdpa(p, stream);
+  if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
+  return st;
+}
+
 }  // namespace tsplat
 
 using namespace tsplat;
@@ -102,34 +130,6 @@ bool ref_gemm_ptrs_ok(const void* a, const void* b, const void* c, const void* d
   return a && b && c && d && e && f && g && h && i && j;
 }
 
-// ---------------------------------------------------------------- SDPA
-int sdpa_checked(const float* q, const float* k, const float* v, const float* bias, float* out,
-                 int B, int H, int Lq, int Lk, int D, int has_bias, int bias_len,
-                 int64_t bias_head_stride, int kv_packed, int Lkp, int out_blhd,
-                 hipStream_t stream, int precision = kPrecisionFp32) {
-  if (!q || !k || !v || !out) return kErrNull;
-  if (B <= 0 || H <= 0 || Lq <= 0 || Lk <= 0 || D != kHeadDim) return kErrDims;
-  if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
-    return kErrDims;
-  if (kv_packed != 0 && kv_packed != 1) return kErrDims;
-  if (kv_packed && (Lkp < Lk || (Lkp & 15) != 0)) return kErrDims;
-  if (has_bias && (bias == nullptr || bias_len != Lk)) return kErrRange;
-  if (has_bias && bias_head_stride != 0 && bias_head_stride < Lk) return kErrRange;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return kErrAlign;
-  const int64_t bh = (int64_t)B * H;
-  TSPLAT_CHECK(check_dev(q, bh * Lq * kHeadDim * 4));
-  const int64_t kv_elems = kv_packed ? bh * kHeadDim * Lkp : bh * Lk * kHeadDim;
-  TSPLAT_CHECK(check_dev(k, kv_elems * 4));
-  TSPLAT_CHECK(check_dev(v, kv_elems * 4));
-  TSPLAT_CHECK(check_dev(out, bh * Lq * kHeadDim * 4));
-  if (has_bias) TSPLAT_CHECK(check_dev(bias, ((int64_t)(H - 1) * bias_head_stride + Lk) * 4));
-  SdpaParams p{q, k, v, has_bias ? bias : nullptr, out, B, H, Lq, Lk, kv_packed, Lkp,
-               bias_head_stride, out_blhd, precision};
-  const int st = launch_sdpa(p, stream);
-  if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
-  return st;
-}
-
 int sdpa_blocking(const float* q, const float* k, const float* v, const float* bias, float* out,
                   int B, int H, int Lq, int Lk, int D, int has_bias, int bias_len, int kv_packed,
                   int Lkp, int out_blhd) {
@@ -137,7 +137,7 @@ int sdpa_blocking(const float* q, const float* k, const float* v, const float* b
   uint64_t alloc_ns0 = 0, alloc_ns1 = 0;
   workspace_timing(kSlotSdpaPartial, &alloc_ns0, nullptr);
   int st = sdpa_checked(q, k, v, bias, out, B, H, Lq, Lk, D, has_bias, bias_len, 0, kv_packed,
-                        Lkp, out_blhd, nullptr);
+                        Lkp, out_blhd, nullptr, kPrecisionFp32, nullptr, 0);
   if (st == kOk) st = sync_null_stream();
   if (st == kOk) {
     const auto t1 = std::chrono::steady_clock::now();
@@ -391,7 +391,7 @@ int tsplat_sdpa_async(const float* q, const float* k, const float* v,
                       int kv_packed, int Lkp, int out_blhd, void* stream) {
   return sdpa_checked(q, k, v, key_bias_or_null, out, B, H, Lq, Lk, D, has_key_bias,
                       key_bias_len, bias_head_stride, kv_packed, Lkp, out_blhd,
-                      static_cast<hipStream_t>(stream));
+                      static_cast<hipStream_t>(stream), kPrecisionFp32, nullptr, 0);
 }
 
 int tsplat_sdpa_precision_async(const float* q, const float* k, const float* v,
@@ -401,7 +401,7 @@ int tsplat_sdpa_precision_async(const float* q, const float* k, const float* v,
                                 int precision, void* stream) {
   return sdpa_checked(q, k, v, key_bias_or_null, out, B, H, Lq, Lk, D, has_key_bias,
                       key_bias_len, bias_head_stride, kv_packed, Lkp, out_blhd,
-                      static_cast<hipStream_t>(stream), precision);
+                      static_cast<hipStream_t>(stream), precision, nullptr, 0);
 }
 
 // ------------------------------------------------------------------ QKV

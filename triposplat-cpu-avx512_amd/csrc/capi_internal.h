@@ -14,6 +14,12 @@ int check_dev(const void* p, int64_t bytes);
 bool aligned16(const void* p);
 // Waits for the null stream (the blocking reference-named entry points).
 int sync_null_stream();
+// Argument checks of the SDPA entry points, then launch_sdpa on `stream`;
+// scratch / scratch_bytes as SdpaParams (null: the stream's workspace).
+int sdpa_checked(const float* q, const float* k, const float* v, const float* bias, float* out,
+                 int B, int H, int Lq, int Lk, int D, int has_bias, int bias_len,
+                 int64_t bias_head_stride, int kv_packed, int Lkp, int out_blhd,
+                 hipStream_t stream, int precision, float* scratch, size_t scratch_bytes);
 
 }  // namespace tsplat
 

@@ -205,8 +205,15 @@ int launch_tiles(SdpaArgs a, const SdpaParams& p, int kBQ, int kBKV, int cus, hi
     splits = (p.Lk + kps - 1) / kps;
     if (splits >= 2) {
       const size_t items = (size_t)rest * splits * kBQ;
-      float* ws = static_cast<float*>(stream_workspace(stream, items * (kD + 2) * 4, kSlotSdpaPartial));
-      if (ws == nullptr) return kErrWorkspace;
+      const size_t need = items * (kD + 2) * 4;
+      float* ws;
+      if (p.scratch != nullptr) {
+        if (need > p.scratch_bytes) return kErrScratch;
+        ws = p.scratch;
+      } else {
+        ws = static_cast<float*>(stream_workspace(stream, need, kSlotSdpaPartial));
+        if (ws == nullptr) return kErrWorkspace;
+      }
       a.full_tiles = (int)(tiles - rest);
       a.splits = splits;
       a.keys_per_split = kps;

@@ -8,7 +8,8 @@ namespace tsplat {
 
 // Status codes.  -1..-5 keep the meaning the reference kernels give them
 // (scripts/gemm_nf24_i16_avx512.c:171-175, native_sdpa_avx512_exact_q8t512.c:151-166);
-// -6 and -7 are the device-side failures a CPU kernel cannot have.
+// -6 and -7 are the device-side failures a CPU kernel cannot have; -8 is the
+// limit of the no-allocation SDPA entry point.
 enum Status : int {
   kOk = 0,
   kErrNull = -1,        // a required pointer is null
@@ -18,6 +19,7 @@ enum Status : int {
   kErrWorkspace = -5,   // device workspace could not be allocated
   kErrPointer = -6,     // pointer is not device memory, or its allocation is too small
   kErrLaunch = -7,      // HIP launch / runtime error
+  kErrScratch = -8,     // the call needs more scratch than the static no-allocation buffer
 };
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));

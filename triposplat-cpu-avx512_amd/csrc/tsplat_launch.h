@@ -54,6 +54,12 @@ struct SdpaParams {
   // operands into bf16 terms as the NF24 GEMM's modes do (q scaled first,
   // p = the unnormalised exponentials); softmax arithmetic stays fp32.
   int precision = kPrecisionFp32;
+  // Scratch for the key-split partials of a partial last round of query
+  // tiles: null takes the stream's library-owned workspace (which may
+  // allocate); non-null uses [scratch, scratch + scratch_bytes) and fails
+  // with kErrScratch when the launch plan needs more.
+  float* scratch = nullptr;
+  size_t scratch_bytes = 0;
 };
 int launch_sdpa(const SdpaParams& p, hipStream_t stream);
 // Queries per workgroup of the most recent SDPA launch (512 before any).

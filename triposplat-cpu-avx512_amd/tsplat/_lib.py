@@ -38,6 +38,7 @@ SIGNATURES = {
     "triposplat_sdpa_q8t512_workspace_release": ([], None),
     "tsplat_sdpa_async": ([_vp] * 5 + [_i] * 7 + [_i64] + [_i] * 3 + [_vp], _i),
     "tsplat_sdpa_precision_async": ([_vp] * 5 + [_i] * 7 + [_i64] + [_i] * 4 + [_vp], _i),
+    "tsplat_sdpa_noalloc_async": ([_vp] * 5 + [_i] * 7 + [_i64] + [_i] * 4 + [_vp], _i),
     "triposplat_qkv_rope_rmsnorm_pack_f32_avx512_v2": ([_vp] * 7 + [_i] * 7, _i),
     "triposplat_qkv_rope_rmsnorm_pack_f32_avx512": ([_vp] * 7 + [_i] * 7, _i),
     "triposplat_qkv_postprocess_token_tile": ([], _i),
@@ -92,6 +93,7 @@ STATUS_TEXT = {
     -5: "device workspace allocation failed",
     -6: "not device memory of the current device, or allocation too small",
     -7: "HIP launch / runtime error",
+    -8: "needs more scratch than the no-allocation entry point's static buffer",
 }
 
 _CACHE: dict[str, ctypes.CDLL] = {}
