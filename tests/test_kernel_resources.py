@@ -33,8 +33,8 @@ BUDGET = {
 # kernels that must exist (a rename must update this test, not skip it)
 REQUIRED = [
     ("sdpa", "sdpa_kernelILi0ELb0ELi16ELi64ELb0E"),          # configs[1] headline
-    ("nf24_gemm", "GemmCfgILi256ELi192ELi16ELi4ELi3ELi1EEELb1ELi0E"),  # configs[0]
-    ("nf24_gemm", "GemmCfgILi256ELi256ELi16ELi4ELi4ELi1EEELb1ELi1E"),  # fused QKV, L = 16384
+    ("nf24_gemm", "GemmCfgILi256ELi192ELi32ELi4ELi3ELi1ELi0ELb1EEELb1ELi0E"),  # configs[0]
+    ("nf24_gemm", "GemmCfgILi256ELi256ELi16ELi4ELi4ELi1ELi0ELb0EEELb1ELi1E"),  # fused QKV, L = 16384
 ]
 
 

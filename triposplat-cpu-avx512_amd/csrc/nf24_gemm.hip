@@ -28,77 +28,82 @@ namespace {
 
 using namespace nf24;
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int kMinWaves_ = 1>
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int kMinWaves_ = 1, int kProducers_ = 0,
+          bool kDefer_ = false>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  // kDefer: the last k-slice of each K step is read into registers before the
+  // step's barrier and multiplied after it, overlapping the next step's first
+  // LDS reads (same per-accumulator order, so the same result).
+  static constexpr bool kDefer = kDefer_;
   static constexpr int kMinWaves = kMinWaves_;  // waves per SIMD the register budget must allow
-  static constexpr int kThreads = WM * WN * 64;
+  // kProducers > 0: that many extra waves only stage tiles (load, decode,
+  // store to LDS) while the WM x WN waves only run MFMAs; 0: every wave does both.
+  static constexpr int kProducers = kProducers_;
+  static constexpr int kComputeWaves = WM * WN;
+  static constexpr int kThreads = (kComputeWaves + kProducers) * 64;
+  static constexpr int kLoadThreads = kProducers > 0 ? kProducers * 64 : kThreads;
   static constexpr int kTM = BM / WM, kTN = BN / WN;
   static constexpr int kMB = kTM / 32, kNB = kTN / 32;
   static constexpr int kS = BK + 4;  // LDS row stride in floats (bank spread)
   // X tile: BM x BK as float4 units; W tile: (column pair, kWK consecutive k)
-  // units, kWK = 4 unless that leaves threads idle.
+  // units, kWK = 4 unless that leaves loading threads idle.
   static constexpr int kXUnits = BM * BK / 4;
-  static constexpr int kWK = ((BN / 2) * (BK / 4) >= kThreads) ? 4 : 2;
+  static constexpr int kWK = ((BN / 2) * (BK / 4) >= kLoadThreads) ? 4 : 2;
   static constexpr int kWUnits = (BN / 2) * (BK / kWK);
-  static constexpr int kXIter = (kXUnits + kThreads - 1) / kThreads;
-  static constexpr int kWIter = (kWUnits + kThreads - 1) / kThreads;
+  static constexpr int kXIter = (kXUnits + kLoadThreads - 1) / kLoadThreads;
+  static constexpr int kWIter = (kWUnits + kLoadThreads - 1) / kLoadThreads;
   static_assert(kTM % 32 == 0 && kTN % 32 == 0, "wave tile must be 32-aligned");
   static_assert(BK % 8 == 0 && BN % 2 == 0, "BK must be a multiple of 8, BN even");
+  static_assert(kThreads <= 1024, "at most 1024 threads per workgroup");
 };
 
-// kVec: x rows 16-byte aligned with K % 4 == 0, and N, n_start, n_count even
-// (so a column pair is loaded with one 32-bit / 16-bit access).
-template <class C, bool kVec, int kEpi>
-__global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::kMinWaves)))
-void nf24_gemm_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) float xs[2][C::BM * C::kS];
-  __shared__ __attribute__((aligned(16))) float ws[2][C::BN * C::kS];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / C::WN, wn = wave % C::WN;
-  const int g = lane >> 5;
-  const int l32 = lane & 31;
-
-  const int tiles_n = (a.n_count + C::BN - 1) / C::BN;
-  const int tile = xcd_tile_index(blockIdx.x, gridDim.x);
-  const int m0 = (tile / tiles_n) * C::BM;
-  const int c0 = (tile % tiles_n) * C::BN;
-
-  // W units owned by this thread: column pair (lc, lc+1), k = kWK*kq .. +kWK-1
-  // inside each K step.  The pair and its scales are fixed for the whole K loop.
+// Moves one K step of the X tile (fp32) and the W tile (packed codes, decoded
+// to fp32) from global memory through registers into LDS, both stored
+// k-contiguous ([row][k], [col][k], row stride kS).  Thread t of the
+// C::kLoadThreads loading threads owns fixed X float4 units and W units
+// (column pair, kWK consecutive k).  kVec: x rows 16-byte aligned with
+// K % 4 == 0, and N, n_start, n_count even (a column pair is one 32-bit /
+// 16-bit access).
+template <class C, bool kVec>
+struct TileLoader {
+  int t;
+  int m0;
   int w_pair[C::kWIter], w_kq[C::kWIter], w_nabs[C::kWIter];
   bool w_ok0[C::kWIter], w_ok1[C::kWIter], w_live[C::kWIter];
   float w_sc0[C::kWIter], w_sc1[C::kWIter];
-#pragma unroll
-  for (int j = 0; j < C::kWIter; ++j) {
-    const int u = tid + j * C::kThreads;
-    w_live[j] = u < C::kWUnits;
-    w_pair[j] = u % (C::BN / 2);
-    w_kq[j] = u / (C::BN / 2);
-    const int lc = c0 + 2 * w_pair[j];
-    w_ok0[j] = w_live[j] && lc < a.n_count;
-    w_ok1[j] = w_live[j] && lc + 1 < a.n_count;
-    w_nabs[j] = a.n_start + lc;
-    w_sc0[j] = w_ok0[j] ? a.scale[w_nabs[j]] : 0.0f;
-    w_sc1[j] = w_ok1[j] ? a.scale[w_nabs[j] + 1] : 0.0f;
-  }
-
   floatx4 xr[C::kXIter];
   uint32_t cr[C::kWIter][C::kWK];  // two int16 codes (columns lc, lc+1)
   uint32_t qr[C::kWIter][C::kWK];  // two int8 codes in the low 16 bits
 
-  auto load_tile = [&](int k0) {
+  // The column pairs and their scales are fixed for the whole K loop.
+  __device__ __forceinline__ void init(const GemmArgs& a, int t_, int m0_, int c0) {
+    t = t_;
+    m0 = m0_;
+#pragma unroll
+    for (int j = 0; j < C::kWIter; ++j) {
+      const int u = t + j * C::kLoadThreads;
+      w_live[j] = u < C::kWUnits;
+      w_pair[j] = u % (C::BN / 2);
+      w_kq[j] = u / (C::BN / 2);
+      const int lc = c0 + 2 * w_pair[j];
+      w_ok0[j] = w_live[j] && lc < a.n_count;
+      w_ok1[j] = w_live[j] && lc + 1 < a.n_count;
+      w_nabs[j] = a.n_start + lc;
+      w_sc0[j] = w_ok0[j] ? a.scale[w_nabs[j]] : 0.0f;
+      w_sc1[j] = w_ok1[j] ? a.scale[w_nabs[j] + 1] : 0.0f;
+    }
+  }
+
+  __device__ __forceinline__ void load(const GemmArgs& a, int k0) {
 #pragma unroll
     for (int j = 0; j < C::kXIter; ++j) {
-      const int idx = tid + j * C::kThreads;
+      const int idx = t + j * C::kLoadThreads;
       const int row = idx / (C::BK / 4);
       const int kc = idx % (C::BK / 4);
       const int gm = m0 + row;
       const int gk = k0 + 4 * kc;
-      const bool live = (C::kXUnits % C::kThreads == 0) || idx < C::kXUnits;
+      const bool live = (C::kXUnits % C::kLoadThreads == 0) || idx < C::kXUnits;
       const float* src = a.x + (int64_t)gm * a.stride_x + gk;
       if (kVec) {
         xr[j] = (live && gm < a.M && gk < a.K) ? *reinterpret_cast<const floatx4*>(src)
@@ -129,20 +134,22 @@ void nf24_gemm_kernel(GemmArgs a) {
         }
       }
     }
-  };
+  }
 
-  auto store_tile = [&](int buf) {
+  // Decodes w = fp32((int32)q01 * 256 + q2) * scale (the reference's
+  // decode16, one rounding) and stores both tiles.
+  __device__ __forceinline__ void store(float* xs, float* ws) {
 #pragma unroll
     for (int j = 0; j < C::kXIter; ++j) {
-      const int idx = tid + j * C::kThreads;
-      if ((C::kXUnits % C::kThreads) != 0 && idx >= C::kXUnits) continue;
+      const int idx = t + j * C::kLoadThreads;
+      if ((C::kXUnits % C::kLoadThreads) != 0 && idx >= C::kXUnits) continue;
       const int row = idx / (C::BK / 4);
       const int kc = idx % (C::BK / 4);
-      *reinterpret_cast<floatx4*>(&xs[buf][row * C::kS + 4 * kc]) = xr[j];
+      *reinterpret_cast<floatx4*>(&xs[row * C::kS + 4 * kc]) = xr[j];
     }
 #pragma unroll
     for (int j = 0; j < C::kWIter; ++j) {
-      if ((C::kWUnits % C::kThreads) != 0 && !w_live[j]) continue;
+      if ((C::kWUnits % C::kLoadThreads) != 0 && !w_live[j]) continue;
       typedef float wvec __attribute__((ext_vector_type(C::kWK)));
       wvec w0, w1;
 #pragma unroll
@@ -154,11 +161,106 @@ void nf24_gemm_kernel(GemmArgs a) {
         w0[e] = (float)qa * w_sc0[j];
         w1[e] = (float)qb * w_sc1[j];
       }
-      *reinterpret_cast<wvec*>(&ws[buf][(2 * w_pair[j]) * C::kS + C::kWK * w_kq[j]]) = w0;
-      *reinterpret_cast<wvec*>(&ws[buf][(2 * w_pair[j] + 1) * C::kS + C::kWK * w_kq[j]]) = w1;
+      *reinterpret_cast<wvec*>(&ws[(2 * w_pair[j]) * C::kS + C::kWK * w_kq[j]]) = w0;
+      *reinterpret_cast<wvec*>(&ws[(2 * w_pair[j] + 1) * C::kS + C::kWK * w_kq[j]]) = w1;
     }
-  };
+  }
+};
 
+// One K step of MFMAs of a wave over the staged tiles xb / wb.  The K index
+// inside each 8-slice is permuted identically for A and B (step t reads
+// k = 8kk + 4*(lane/32) + t), so every lane fetches 4 consecutive k with one
+// ds_read_b128 and the dot product is unchanged.
+template <class C>
+__device__ __forceinline__ void mfma_step(const float* xb, const float* wb, int wm, int wn, int g,
+                                          int l32, floatx16 (&acc)[C::kMB][C::kNB]) {
+#pragma unroll
+  for (int kk = 0; kk < C::BK / 8; ++kk) {
+    floatx4 af[C::kMB], bf[C::kNB];
+#pragma unroll
+    for (int mb = 0; mb < C::kMB; ++mb)
+      af[mb] = *reinterpret_cast<const floatx4*>(
+          &xb[(wm * C::kTM + mb * 32 + l32) * C::kS + 8 * kk + 4 * g]);
+#pragma unroll
+    for (int nb = 0; nb < C::kNB; ++nb)
+      bf[nb] = *reinterpret_cast<const floatx4*>(
+          &wb[(wn * C::kTN + nb * 32 + l32) * C::kS + 8 * kk + 4 * g]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int mb = 0; mb < C::kMB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < C::kNB; ++nb)
+          acc[mb][nb] = mfma32x32x2(af[mb][t], bf[nb][t], acc[mb][nb]);
+  }
+}
+
+// Fragments of k-slice kk of a staged step, and their 16 MFMA k-steps.
+template <class C>
+struct Frags {
+  floatx4 af[C::kMB], bf[C::kNB];
+};
+template <class C>
+__device__ __forceinline__ void read_slice(const float* xb, const float* wb, int kk, int wm, int wn,
+                                           int g, int l32, Frags<C>& f) {
+#pragma unroll
+  for (int mb = 0; mb < C::kMB; ++mb)
+    f.af[mb] = *reinterpret_cast<const floatx4*>(
+        &xb[(wm * C::kTM + mb * 32 + l32) * C::kS + 8 * kk + 4 * g]);
+#pragma unroll
+  for (int nb = 0; nb < C::kNB; ++nb)
+    f.bf[nb] = *reinterpret_cast<const floatx4*>(
+        &wb[(wn * C::kTN + nb * 32 + l32) * C::kS + 8 * kk + 4 * g]);
+}
+template <class C>
+__device__ __forceinline__ void mfma_slice(const Frags<C>& f, floatx16 (&acc)[C::kMB][C::kNB]) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int mb = 0; mb < C::kMB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < C::kNB; ++nb)
+        acc[mb][nb] = mfma32x32x2(f.af[mb][t], f.bf[nb][t], acc[mb][nb]);
+}
+
+template <class C, bool kVec, int kEpi>
+__global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::kMinWaves)))
+void nf24_gemm_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) float xs[2][C::BM * C::kS];
+  __shared__ __attribute__((aligned(16))) float ws[2][C::BN * C::kS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 5;
+  const int l32 = lane & 31;
+
+  const int tiles_n = (a.n_count + C::BN - 1) / C::BN;
+  int tm, tn;
+  xcd_grid(blockIdx.x, gridDim.x / tiles_n, tiles_n, a.xcd_pm, a.xcd_pn, tm, tn);
+  const int m0 = tm * C::BM;
+  const int c0 = tn * C::BN;
+  const int nk = (a.K + C::BK - 1) / C::BK;
+
+  if (C::kProducers > 0 && wave >= C::kComputeWaves) {
+    // Producer waves: stage K step kt + 1 into the other buffer while the
+    // MFMA waves consume step kt; one barrier per step, as the consumers.
+    TileLoader<C, kVec> ld;
+    ld.init(a, tid - C::kComputeWaves * 64, m0, c0);
+    ld.load(a, 0);
+    ld.store(xs[0], ws[0]);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + 1 < nk) {
+        ld.load(a, (kt + 1) * C::BK);
+        ld.store(xs[(kt & 1) ^ 1], ws[(kt & 1) ^ 1]);
+      }
+      __syncthreads();
+    }
+    return;
+  }
+
+  const int wm = wave / C::WN, wn = wave % C::WN;
   // Accumulators start at the bias, as the reference's chain does.
   floatx16 acc[C::kMB][C::kNB];
 #pragma unroll
@@ -171,37 +273,53 @@ void nf24_gemm_kernel(GemmArgs a) {
       for (int r = 0; r < 16; ++r) acc[mb][nb][r] = bv;
   }
 
-  const int nk = (a.K + C::BK - 1) / C::BK;
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load_tile((kt + 1) * C::BK);
-    const float* xb = xs[buf];
-    const float* wb = ws[buf];
-#pragma unroll
-    for (int kk = 0; kk < C::BK / 8; ++kk) {
-      floatx4 af[C::kMB], bf[C::kNB];
-#pragma unroll
-      for (int mb = 0; mb < C::kMB; ++mb)
-        af[mb] = *reinterpret_cast<const floatx4*>(
-            &xb[(wm * C::kTM + mb * 32 + l32) * C::kS + 8 * kk + 4 * g]);
-#pragma unroll
-      for (int nb = 0; nb < C::kNB; ++nb)
-        bf[nb] = *reinterpret_cast<const floatx4*>(
-            &wb[(wn * C::kTN + nb * 32 + l32) * C::kS + 8 * kk + 4 * g]);
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int mb = 0; mb < C::kMB; ++mb)
-#pragma unroll
-          for (int nb = 0; nb < C::kNB; ++nb)
-            acc[mb][nb] = mfma32x32x2(af[mb][t], bf[nb][t], acc[mb][nb]);
-    }
-    if (kt + 1 < nk) store_tile(buf ^ 1);
+  if constexpr (C::kProducers > 0) {
     __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      mfma_step<C>(xs[kt & 1], ws[kt & 1], wm, wn, g, l32, acc);
+      __syncthreads();
+    }
+  } else if constexpr (C::kDefer) {
+    TileLoader<C, kVec> ld;
+    ld.init(a, tid, m0, c0);
+    ld.load(a, 0);
+    ld.store(xs[0], ws[0]);
+    __syncthreads();
+    Frags<C> last;
+    for (int kt = 0; kt < nk; ++kt) {
+      const int buf = kt & 1;
+      Frags<C> f0;
+      read_slice<C>(xs[buf], ws[buf], 0, wm, wn, g, l32, f0);
+      if (kt > 0) mfma_slice<C>(last, acc);  // the previous step's deferred slice
+      if (kt + 1 < nk) ld.load(a, (kt + 1) * C::BK);
+      mfma_slice<C>(f0, acc);
+#pragma unroll
+      for (int kk = 1; kk + 1 < C::BK / 8; ++kk) {
+        Frags<C> f;
+        read_slice<C>(xs[buf], ws[buf], kk, wm, wn, g, l32, f);
+        mfma_slice<C>(f, acc);
+      }
+      read_slice<C>(xs[buf], ws[buf], C::BK / 8 - 1, wm, wn, g, l32, last);
+      if (kt + 1 < nk) ld.store(xs[buf ^ 1], ws[buf ^ 1]);
+      __syncthreads();
+    }
+    mfma_slice<C>(last, acc);
+  } else {
+    // Every wave stages: the next K step's codes and X are fetched into
+    // registers while the MFMAs of the current step run (double-buffered
+    // LDS, one barrier per step).
+    TileLoader<C, kVec> ld;
+    ld.init(a, tid, m0, c0);
+    ld.load(a, 0);
+    ld.store(xs[0], ws[0]);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int buf = kt & 1;
+      if (kt + 1 < nk) ld.load(a, (kt + 1) * C::BK);
+      mfma_step<C>(xs[buf], ws[buf], wm, wn, g, l32, acc);
+      if (kt + 1 < nk) ld.store(xs[buf ^ 1], ws[buf ^ 1]);
+      __syncthreads();
+    }
   }
 
   if constexpr (kEpi == kEpiQkv) {
@@ -211,15 +329,43 @@ void nf24_gemm_kernel(GemmArgs a) {
   store_result<C::kMB, C::kNB, kEpi>(a, acc, m0 + wm * C::kTM, c0 + wn * C::kTN, g, l32);
 }
 
+// The XCD rectangles (xcd_grid) that minimise the bytes of x rows and
+// codes each XCD's L2 must fetch for its tiles, or pm = pn = 0 when the grid
+// does not divide into 8 equal rectangles or the contiguous runs of
+// xcd_tile_index fetch as little.
+inline bool g_xcd_blocking = true;
+void xcd_blocking(int tiles_m, int tiles_n, int bm, int bn, int K, int& pm, int& pn) {
+  pm = pn = 0;
+  if (!g_xcd_blocking || (tiles_m * tiles_n) % 8 != 0) return;
+  auto bytes = [&](double rows, double cols) { return rows * bm * K * 4.0 + cols * bn * K * 3.0; };
+  // contiguous runs: tiles/8 consecutive tiles, row-major
+  const int run = tiles_m * tiles_n / 8;
+  const int run_rows = (run + tiles_n - 1) / tiles_n + (run % tiles_n != 0 ? 1 : 0);
+  const int run_cols = run >= tiles_n ? tiles_n : run;
+  double best = bytes(run_rows, run_cols);
+  for (int m = 1; m <= 8; m *= 2) {
+    const int n = 8 / m;
+    if (tiles_m % m != 0 || tiles_n % n != 0) continue;
+    const double b = bytes((double)tiles_m / m, (double)tiles_n / n);
+    if (b < best) {
+      best = b;
+      pm = m;
+      pn = n;
+    }
+  }
+}
+
 template <class C, int kEpi = kEpiStore>
 int launch_cfg(const GemmParams& p, hipStream_t stream, const QkvArgs& e = QkvArgs{},
                const GemmEpilogueParams& ep = GemmEpilogueParams{kEpilogueStore, nullptr, 0, 1},
                int row0 = 0) {
   GemmArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out,
              p.M, p.K, p.N, p.n_start, p.n_count, p.stride_x, p.stride_out, e,
-             ep.gate, ep.gate_stride, ep.rows_per_batch, row0};
-  const int64_t tiles = (int64_t)((p.M + C::BM - 1) / C::BM) * ((p.n_count + C::BN - 1) / C::BN);
+             ep.gate, ep.gate_stride, ep.rows_per_batch, row0, 0, 0};
+  const int tiles_m = (p.M + C::BM - 1) / C::BM, tiles_n = (p.n_count + C::BN - 1) / C::BN;
+  const int64_t tiles = (int64_t)tiles_m * tiles_n;
   if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
+  xcd_blocking(tiles_m, tiles_n, C::BM, C::BN, p.K, a.xcd_pm, a.xcd_pn);
   const bool vec = (reinterpret_cast<uintptr_t>(p.x) % 16 == 0) && (p.stride_x % 4 == 0) &&
                    (p.K % 4 == 0) && (p.N % 2 == 0) && (p.n_start % 2 == 0) &&
                    (p.n_count % 2 == 0) && (reinterpret_cast<uintptr_t>(p.code01) % 4 == 0) &&
@@ -254,7 +400,10 @@ __global__ __launch_bounds__(kTailThreads) void packed_tail_zero_kernel(float* p
 // Against measurement (M = 2048..32768, N = 1024..4096) the model picks the
 // fastest configuration or one within 3 % of it.
 using CfgLarge = GemmCfg<256, 256, 16, 4, 4>;    // 16 waves, 1 workgroup / CU
-using CfgWide = GemmCfg<256, 192, 16, 4, 3>;     // 12 waves, 1 workgroup / CU
+// 12 waves, 1 workgroup / CU, K steps of 32, the last k-slice of each step
+// multiplied after its barrier (measured at configs[0]: BK 16 -> 32 -5 %,
+// deferral a further -3 %; with deferral the 256 x 256 tile is 4 % slower)
+using CfgWide = GemmCfg<256, 192, 32, 4, 3, 1, 0, true>;
 using CfgSmall = GemmCfg<128, 128, 16, 2, 2, 3>; // 4 waves, 3 workgroups / CU
 using CfgSkinny = GemmCfg<32, 128, 32, 1, 4>;
 using CfgTail = GemmCfg<32, 128, 32, 1, 2>;      // <= 32 rows, QKV epilogue: 64-column waves (a head)
@@ -272,7 +421,7 @@ struct Choice {
   double rate;
 };
 constexpr Choice kChoices[] = {
-    {256, 256, 1, 16, 126.0}, {256, 192, 1, 12, 122.0}, {128, 128, 3, 4, 111.0}};
+    {256, 256, 1, 16, 126.0}, {256, 192, 1, 12, 125.0}, {128, 128, 3, 4, 111.0}};
 
 int compute_units() {
   static int cached[64] = {0};

@@ -52,7 +52,30 @@ struct GemmArgs {
   int64_t gate_stride;
   int rows_per_batch;
   int row0;  // global index of row 0 of x / out (the epilogues' token mapping)
+  // XCD blocking of the tile grid (xcd_grid): 0, or pm x pn = 8 rectangles
+  int xcd_pm, xcd_pn;
 };
+
+// Tile (row band, column band) of workgroup `id` in a grid of tiles_m x
+// tiles_n tiles.  Workgroup i runs on XCD i % 8.  With pm x pn = 8 the grid
+// is cut into pm x pn rectangles, one per XCD, so that each XCD's L2 holds
+// the x rows of tiles_m / pm bands and the codes of tiles_n / pn bands
+// instead of every band of one operand; within a rectangle the XCD's
+// workgroups take tiles row by row in dispatch order.  Otherwise each XCD
+// gets a contiguous run of tile indices (xcd_tile_index).
+__device__ __forceinline__ void xcd_grid(int id, int tiles_m, int tiles_n, int pm, int pn,
+                                         int& tm, int& tn) {
+  if (pm > 0) {
+    const int xcd = id & 7, j = id >> 3;
+    const int rw = tiles_n / pn, rh = tiles_m / pm;
+    tm = (xcd / pn) * rh + j / rw;
+    tn = (xcd % pn) * rw + j % rw;
+    return;
+  }
+  const int tile = xcd_tile_index(id, tiles_m * tiles_n);
+  tm = tile / tiles_n;
+  tn = tile % tiles_n;
+}
 
 // kEpilogue* of tsplat_launch.h, plus the fused QKV epilogue.
 enum Epilogue : int { kEpiStore = kEpilogueStore, kEpiQkv = 1 };
