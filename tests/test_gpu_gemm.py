@@ -68,7 +68,12 @@ SHAPES = [(25, 96, 64), (40, 96, 64), (10, 96, 64), (3, 96, 5), (1, 1024, 3072),
           # 9-16 rows on the wide kernel (two LDS reduction passes), partial slab
           (9, 1024, 520), (13, 2048, 1024),
           # more K splits than the staged merge holds: the one-thread-per-output merge
-          (1, 40000, 96)]
+          (1, 40000, 96),
+          # the MFMA few-row form (6..16 rows, >= 96 slabs of 32 columns): every row count
+          # at its edges, ragged K (a partial last chunk and a partial last wave), a K
+          # that only two waves reach, the wide N
+          (6, 1024, 3072), (8, 1000, 3072), (11, 2048, 6144), (16, 40, 3072), (13, 4100, 3104),
+          (5, 1024, 3072), (16, 1024, 3040)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
@@ -95,6 +100,22 @@ def test_gemm_reference_smoke_tolerance(oracle, cuda, hiplib):
         ref = torch.nn.functional.linear(torch.from_numpy(x), torch.from_numpy(w_hat.T.copy()),
                                          torch.from_numpy(b))
         torch.testing.assert_close(torch.from_numpy(got), ref, rtol=2e-5, atol=2e-5)
+
+
+def test_few_row_mfma_range_and_strides(oracle, cuda, hiplib):
+    """The MFMA few-row form on an output range with row strides (x padded,
+    out wider than the range), equal to the same columns of the full call."""
+    import torch
+
+    M, K, N = 12, 1024, 3200
+    start, count = 64, 3072
+    x, w, b = seeded_linear(71, M, K, N)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    got = _run_async(torch, hiplib, cuda, x, c01, q2, s, b, start, count, stride_x=K + 12,
+                     stride_out=count + 32)[:, :count]
+    _check(oracle, x, c01, q2, s, b, got, start)
+    full = _run_async(torch, hiplib, cuda, x, c01, q2, s, b)
+    assert np.array_equal(got, full[:, start:start + count])
 
 
 @pytest.mark.parametrize("start,count", [(0, 16), (16, 32), (48, 80), (5, 7), (100, 28)])

@@ -294,6 +294,143 @@ __global__ __launch_bounds__(kWideWaves * 64) void nf24_gemv_wide_kernel(GemvArg
   }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA form for M <= 16 (columns, column offset and N multiples of kCols,
+// 16-byte aligned codes, scales and x rows): one workgroup owns kCols
+// columns over the whole K range, so no partial sums leave the chip and no
+// second kernel runs.  Each wave takes consecutive 32-row chunks of K
+// (kWaves equal ranges); per chunk every lane loads 8 columns of one row
+// (a 128-bit code01 and a 64-bit q2 load: a wave instruction covers whole
+// rows of the slab) and 8 values of one x row, decodes the weights exactly
+// as decode16 and stores them transposed into the wave's own LDS tile
+// ([col][k], [row][k]); v_mfma_f32_16x16x4_f32 then accumulates x rows
+// 0..15 against 16-column blocks, the k inside each 16-slice permuted
+// identically for both operands so every lane reads 4 consecutive k with one
+// ds_read_b128.  The loads of kPass chunks are issued before any is used.
+// (Rows a wave does not own are multiplied by x = 0.)
+// The wave sums are added in wave order through LDS.  Rows of x past M read
+// row M - 1; their sums are never stored.
+constexpr int kMfmaRows = 32;            // K rows per chunk
+constexpr int kMfmaS = kMfmaRows + 4;    // LDS row stride in floats
+
+template <int kCols, int kWaves, int kPass>
+__global__ __launch_bounds__(kWaves * 64) void nf24_gemv_mfma_kernel(GemvArgs a) {
+  constexpr int kLanesPerRow = kCols / 8;              // 8 columns per lane
+  constexpr int kRowsPerLoad = 64 / kLanesPerRow;      // rows per wave instruction
+  constexpr int kLoads = kMfmaRows / kRowsPerLoad;     // instructions per chunk
+  constexpr int kBlocks = kCols / 16;
+  __shared__ __attribute__((aligned(16))) float ws[kWaves][kCols * kMfmaS];
+  __shared__ __attribute__((aligned(16))) float xs[kWaves][16 * kMfmaS];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int c0 = blockIdx.x * kCols;                 // first local column of the slab
+  const int cg = lane % kLanesPerRow, lr = lane / kLanesPerRow;
+  const int64_t ncol = a.n_start + c0 + 8 * cg;      // this lane's first column
+  const int kw0 = wave * a.k_per_split;              // k_per_split: rows per wave
+  const int kw1 = min(a.K, kw0 + a.k_per_split);
+  const int xm = min(lane >> 2, a.M - 1);            // x row this lane stages
+  const int xk = 8 * (lane & 3);                     // its 8 k within a chunk
+
+  float sc[8];
+  {
+    const floatx4 s0 = *reinterpret_cast<const floatx4*>(a.scale + ncol);
+    const floatx4 s1 = *reinterpret_cast<const floatx4*>(a.scale + ncol + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sc[e] = s0[e];
+      sc[4 + e] = s1[e];
+    }
+  }
+  floatx4 acc[kBlocks];
+#pragma unroll
+  for (int b = 0; b < kBlocks; ++b) acc[b] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  float* wsw = ws[wave];
+  float* xsw = xs[wave];
+
+  for (int kb = kw0; kb < kw1; kb += kPass * kMfmaRows) {
+    uint4 c[kPass][kLoads];
+    uint2 q[kPass][kLoads];
+    floatx4 xv[kPass][2];
+#pragma unroll
+    for (int p = 0; p < kPass; ++p) {
+      const int kc = kb + p * kMfmaRows;
+      // Code loads are unconditional (rows past K re-read row K - 1) so that
+      // all of them are in flight at once; rows outside the wave's range
+      // meet x = 0 below, and every decoded weight is finite.
+#pragma unroll
+      for (int i = 0; i < kLoads; ++i) {
+        const int kr = min(kc + i * kRowsPerLoad + lr, a.K - 1);
+        const int64_t off = (int64_t)kr * a.N + ncol;
+        c[p][i] = *reinterpret_cast<const uint4*>(a.code01 + off);
+        q[p][i] = *reinterpret_cast<const uint2*>(a.q2 + off);
+      }
+      const float* xr = a.x + (int64_t)xm * a.stride_x + kc + xk;
+      if (kc + kMfmaRows <= kw1) {  // uniform over the wave
+        xv[p][0] = *reinterpret_cast<const floatx4*>(xr);
+        xv[p][1] = *reinterpret_cast<const floatx4*>(xr + 4);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[p][e >> 2][e & 3] = (kc + xk + e < kw1) ? xr[e] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < kPass; ++p) {
+#pragma unroll
+      for (int i = 0; i < kLoads; ++i) {
+        const uint32_t cw[4] = {c[p][i].x, c[p][i].y, c[p][i].z, c[p][i].w};
+        const uint32_t qw[2] = {q[p][i].x, q[p][i].y};
+        const int kl = i * kRowsPerLoad + lr;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int32_t code = (int32_t)(int16_t)((cw[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+          const int32_t res = (int32_t)(int8_t)((qw[e >> 2] >> (8 * (e & 3))) & 0xffu);
+          wsw[(8 * cg + e) * kMfmaS + kl] = (float)(code * 256 + res) * sc[e];
+        }
+      }
+      *reinterpret_cast<floatx4*>(&xsw[(lane >> 2) * kMfmaS + xk]) = xv[p][0];
+      *reinterpret_cast<floatx4*>(&xsw[(lane >> 2) * kMfmaS + xk + 4]) = xv[p][1];
+      // The tile is this wave's alone: LDS runs one wave's instructions in
+      // order, so a wave-scope fence (which keeps the compiler from moving
+      // the reads above the stores) is all the ordering needed.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int kk = 0; kk < kMfmaRows / 16; ++kk) {
+        const int koff = 16 * kk + 4 * (lane >> 4);
+        const floatx4 af = *reinterpret_cast<const floatx4*>(&xsw[(lane & 15) * kMfmaS + koff]);
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+          const floatx4 bf =
+              *reinterpret_cast<const floatx4*>(&wsw[(16 * b + (lane & 15)) * kMfmaS + koff]);
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[t], bf[t], acc[b], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+
+  // Wave sums in wave order.  Lane l of block b holds rows 4*(l/16) + i,
+  // column 16 b + l % 16.
+  __syncthreads();
+  float* red = &ws[0][0];  // [kWaves][kBlocks][64 lanes][4]
+#pragma unroll
+  for (int b = 0; b < kBlocks; ++b)
+    *reinterpret_cast<floatx4*>(&red[((wave * kBlocks + b) * 64 + lane) * 4]) = acc[b];
+  __syncthreads();
+  for (int i = tid; i < kBlocks * 64 * 4; i += kWaves * 64) {
+    float v = red[i];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) v += red[w * kBlocks * 256 + i];
+    const int b = i / 256, l = (i / 4) % 64, r = i % 4;
+    const int row = 4 * (l >> 4) + r, col = c0 + 16 * b + (l & 15);
+    if (row < a.M) a.out[(int64_t)row * a.stride_out + col] = a.bias[a.n_start + col] + v;
+  }
+}
+
 // out[m, c] = bias + sum over splits (in split order) of the partials, for
 // up to kMergeMaxSplits splits.  A workgroup owns 16 columns of one row m;
 // its 16 threads per column each load every 16th split -- all of a thread's
@@ -379,8 +516,40 @@ int launch_mt(GemvArgs a, int cgroups, int splits, hipStream_t stream) {
 // workgroups stream the weights, at most until each wave keeps 16 rows and
 // the partial sums (splits * M * count * 8 bytes) stay under half the weight
 // bytes; a split costs a second, small kernel.
+namespace {
+// The MFMA form: 32-column slabs, 8 waves, all loads of 4 chunks in flight.
+// Measured against the K-split wide kernel (cold weights, HIP-graph replay,
+// per call): at N = 3072 / 6144, K = 1024 it is 10.1 / 11.6 us for every M
+// <= 16, where the split kernel takes 7.2 / 9.4 us at M = 1 and 16.3 / 22.0
+// us at M = 16 (the crossing is near M = 6); with fewer than 96 slabs
+// (N = 1024, K = 4096: 27-29 us against 9-19 us) too few CUs stream.
+// 64-column slabs and 4 or 16 waves measured slower.
+constexpr int kMfmaCols = 32;
+constexpr int kMfmaWaves = 8;
+constexpr int kMfmaMinRows = 6;
+constexpr int kMfmaMinSlabs = 96;
+
+int launch_mfma_form(const GemmParams& p, hipStream_t stream) {
+  const int per_wave =
+      ((p.K + kMfmaWaves * kMfmaRows - 1) / (kMfmaWaves * kMfmaRows)) * kMfmaRows;
+  GemvArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out, nullptr, p.M, p.K, p.N,
+             p.n_start, p.n_count, p.stride_x, p.stride_out, per_wave, 1};
+  hipLaunchKernelGGL((nf24_gemv_mfma_kernel<kMfmaCols, kMfmaWaves, 4>),
+                     dim3((unsigned)(p.n_count / kMfmaCols)), dim3(kMfmaWaves * 64), 0, stream, a);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+}  // namespace
+
 int launch_nf24_gemv(const GemmParams& p, hipStream_t stream) {
   if (p.M < 1 || p.M > 32) return kErrDims;
+  const bool mfma_ok = p.M >= kMfmaMinRows && p.M <= 16 &&
+                       ((p.N | p.n_start | p.n_count) % kMfmaCols) == 0 &&
+                       p.n_count / kMfmaCols >= kMfmaMinSlabs && (p.stride_x & 3) == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.x) & 15) == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.code01) & 15) == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.q2) & 15) == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.scale) & 15) == 0;
+  if (mfma_ok) return launch_mfma_form(p, stream);
   const bool wide = p.M <= 16 && ((p.N | p.n_start | p.n_count) & 7) == 0 &&
                     (reinterpret_cast<uintptr_t>(p.code01) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(p.q2) & 7) == 0 &&
