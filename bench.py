@@ -373,6 +373,171 @@ def run_gemm(torch, dev, iters, ref_parity=False):
     }
 
 
+def time_interleaved(torch, fns, iters, rounds=5):
+    """Median per-call device time (ms) of each callable, timed in
+    interleaved rounds (clocks drift between rounds on these boxes)."""
+    for _ in range(3):
+        for f in fns.values():
+            f()
+    torch.cuda.synchronize()
+    ts = {k: [] for k in fns}
+    for _ in range(rounds):
+        for k, f in fns.items():
+            ts[k].append(time_events(torch, f, iters))
+    return {k: sorted(v)[len(v) // 2] for k, v in ts.items()}
+
+
+def packed_linear(torch, dev, K, N, seed):
+    """A seeded NF24 Linear (W ~ N(0, 0.02), bias ~ N(0, 0.01)), packed on the device."""
+    import numpy as np
+    from tsplat.nf24 import quantize_nf24_i16_per_output_channel
+
+    w = torch.from_numpy((np.random.default_rng(seed).standard_normal((N, K), dtype=np.float32)
+                          * np.float32(0.02)).astype(np.float32)).to(dev)
+    b = torch.from_numpy((np.random.default_rng(seed + 1).standard_normal(N, dtype=np.float32)
+                          * np.float32(0.01)).astype(np.float32)).to(dev)
+    codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+    return codes[0], codes[1], scales[0], b
+
+
+GEMM_L16384 = (("qkv", 1024, 3072), ("mlp_fc1", 1024, 4096), ("mlp_fc2", 4096, 1024), ("attn_out", 1024, 1024))
+
+
+def run_gemm_l16384(torch, dev, iters=8):
+    """The flow block's four NF24 Linear shapes at the metric's L = 16384 rows
+    (strict fp32 MFMA, plain store), TFLOP/s and fraction of the fp32 peak."""
+    import numpy as np
+    from tsplat.nf24 import nf24_linear
+
+    M = 16384
+    res = {}
+    fns, meta = {}, {}
+    for i, (name, K, N) in enumerate(GEMM_L16384):
+        x = torch.from_numpy(np.random.default_rng(40 + i).standard_normal((M, K), dtype=np.float32)).to(dev)
+        c01, q2, sc, b = packed_linear(torch, dev, K, N, 50 + 2 * i)
+        out = torch.empty((M, N), dtype=torch.float32, device=dev)
+        fns[name] = (lambda x=x, c01=c01, q2=q2, sc=sc, b=b, out=out: nf24_linear(x, c01, q2, sc, b, out=out))
+        meta[name] = (K, N)
+    ms = time_interleaved(torch, fns, iters)
+    for name, (K, N) in meta.items():
+        tf = 2.0 * M * N * K / (ms[name] * 1e-3) / 1e12
+        res[name] = {"M": M, "K": K, "N": N, "ms": ms[name], "tflops": tf, "frac_fp32_mfma_peak": tf / PEAK_FP32_MFMA}
+    return res
+
+
+# The reference's own published timings of this path (AMD EPYC 9654, 4 CPUs;
+# seconds per call, GCC 9 build / GCC 13 -march=znver4 build):
+# docs/triposplat_cpu_p0_p1_validation_20260722_ja.md:43-46 (SDPA),
+# :99-104 (GEMM, GCC 9) and docs/triposplat_high_memory_native_f32_audit_20260723_ja.md:66-71
+# (GEMM, GCC 13).
+PUBLISHED_S = {
+    "sdpa_L12294_dense": (2.597, 2.006),
+    "sdpa_L8194_keybias_log4101": (0.993, 0.841),
+    "gemm_12294x1024x3072_qkv": (0.302, 0.332),
+    "gemm_12294x1024x4096_fc1": (0.498, 0.371),
+    "gemm_12294x4096x1024_fc2": (0.539, 0.418),
+    "gemm_12294x1024x1024_out": (0.121, 0.075),
+}
+
+
+def run_reference_shapes(torch, dev, with_cpu, iters=5):
+    """The reference's real TripoSplat sequence shapes on the device, with the
+    reference's AVX-512 build timed beside them on the host at its published
+    thread count (4), and each device output compared with the reference's
+    on the rows the CPU computed:
+      * SDPA L = 12294 dense (the positive CFG branch, attention_patch:5357-5363);
+      * SDPA L = 8194 with the compressed negative branch's key bias (log 4101
+        on the single condition key, attention_patch:5468-5475, 5618-5628);
+      * SDPA 8193 selected latent queries x 12294 keys (the final block);
+      * the block's four NF24 GEMMs at M = 12294.
+    The CPU SDPA runs on the first 2048 query rows of every head (rows are
+    independent) and is scaled to the whole call; the CPU GEMMs run in full."""
+    import numpy as np
+    from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
+    from tsplat.nf24 import nf24_linear
+
+    O = None
+    if with_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+
+        if not O.ref_available():
+            O = None
+    threads = 4
+    H, D = 16, 64
+    res = {}
+    for name, Lq, Lk, logm in (("sdpa_L12294_dense", 12294, 12294, False),
+                               ("sdpa_L8194_keybias_log4101", 8194, 8194, True),
+                               ("sdpa_selected_8193x12294", 8193, 12294, False)):
+        q_h = rope_rmsnorm_host(np.random.default_rng(30).standard_normal((1, H, Lq, D), dtype=np.float32))
+        k_h = rope_rmsnorm_host(np.random.default_rng(31).standard_normal((1, H, Lk, D), dtype=np.float32))
+        v_h = np.random.default_rng(32).standard_normal((1, H, Lk, D), dtype=np.float32)
+        bias_h = None
+        if logm:
+            bias_h = np.zeros(Lk, np.float32)
+            bias_h[Lk - 1] = np.float32(math.log(4101.0))
+        q, k, v = (torch.from_numpy(a).to(dev) for a in (q_h, k_h, v_h))
+        bias = None if bias_h is None else torch.from_numpy(bias_h).to(dev)
+        out = torch.empty((1, H, Lq, D), dtype=torch.float32, device=dev)
+        fn = lambda: native_sdpa_f32_ex(q, k, v, key_bias=bias, out=out)
+        ms = time_interleaved(torch, {"x": fn}, iters)["x"]
+        flop = 4.0 * H * Lq * Lk * D
+        row = {"Lq": Lq, "Lk": Lk, "key_bias": "log(4101) on key Lk-1" if logm else None, "ms": ms,
+               "tflops": flop / (ms * 1e-3) / 1e12, "frac_fp32_mfma_peak": flop / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA}
+        if name in PUBLISHED_S:
+            row["published_cpu_s_4cpu_gcc9_gcc13"] = PUBLISHED_S[name]
+            row["speedup_vs_published_gcc13"] = PUBLISHED_S[name][1] / (ms * 1e-3)
+        if O is not None:
+            rows = 2048
+            qs = np.ascontiguousarray(q_h[:, :, :rows])
+            O.ref_sdpa_q8t512(qs[:, :, :256], k_h, v_h, bias_h, threads)
+            times, ref = [], None
+            for _ in range(3):
+                t0 = time.perf_counter()
+                ref = O.ref_sdpa_q8t512(qs, k_h, v_h, bias_h, threads)
+                times.append(time.perf_counter() - t0)
+            cpu_s = sorted(times)[1] * Lq / rows
+            row["cpu_reference"] = {"threads": threads, "s_per_call": cpu_s, "sample": f"{rows} of {Lq} query rows, all heads",
+                                    "speedup_gpu_vs_cpu": cpu_s / (ms * 1e-3)}
+            fn()
+            torch.cuda.synchronize()
+            row["parity_vs_reference"] = parity_stats(out[:, :, :rows].cpu().numpy(), ref,
+                                                      tol_abs=1e-5 * float(np.abs(v_h).max()))
+        res[name] = row
+        del q, k, v, out
+    M = 12294
+    for i, (tag, K, N) in enumerate((("qkv", 1024, 3072), ("fc1", 1024, 4096), ("fc2", 4096, 1024), ("out", 1024, 1024))):
+        name = f"gemm_{M}x{K}x{N}_{tag}"
+        x_h = np.random.default_rng(60 + i).standard_normal((M, K), dtype=np.float32)
+        x = torch.from_numpy(x_h).to(dev)
+        c01, q2, sc, b = packed_linear(torch, dev, K, N, 70 + 2 * i)
+        out = torch.empty((M, N), dtype=torch.float32, device=dev)
+        fn = lambda: nf24_linear(x, c01, q2, sc, b, out=out)
+        ms = time_interleaved(torch, {"x": fn}, iters)["x"]
+        flop = 2.0 * M * N * K
+        row = {"M": M, "K": K, "N": N, "ms": ms, "tflops": flop / (ms * 1e-3) / 1e12,
+               "frac_fp32_mfma_peak": flop / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA,
+               "published_cpu_s_4cpu_gcc9_gcc13": PUBLISHED_S[name],
+               "speedup_vs_published_gcc13": PUBLISHED_S[name][1] / (ms * 1e-3)}
+        if O is not None:
+            ch, qh, sh, bh = (t.cpu().numpy() for t in (c01, q2, sc, b))
+            O.ref_nf24_gemm(x_h[:256], ch, qh, sh, bh, threads)
+            times, ref = [], None
+            for _ in range(3):
+                t0 = time.perf_counter()
+                ref = O.ref_nf24_gemm(x_h, ch, qh, sh, bh, threads)
+                times.append(time.perf_counter() - t0)
+            cpu_s = sorted(times)[1]
+            row["cpu_reference"] = {"threads": threads, "s_per_call": cpu_s, "sample": "the whole call",
+                                    "speedup_gpu_vs_cpu": cpu_s / (ms * 1e-3)}
+            fn()
+            torch.cuda.synchronize()
+            row["parity_vs_reference"] = parity_stats(out.cpu().numpy(), ref)
+        res[name] = row
+        del x, out
+    return res
+
+
 def flow_inputs(cfg):
     import numpy as np
 
@@ -623,7 +788,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=("sdpa", "gemm", "copy", "flow", "skinny"), default=None,
+    ap.add_argument("--only", choices=("sdpa", "gemm", "copy", "flow", "skinny", "gemm16k", "refshapes"),
+                    default=None,
                     help="run one workload alone (for profiler runs) and print its figures")
     ap.add_argument("--no-flow", action="store_true", help="skip configs[3]/[4] (flow block / step)")
     ap.add_argument("--precision", choices=("fp32", "bf16", "bf16x3"), default="fp32",
@@ -655,6 +821,12 @@ def main():
     if args.only == "skinny":
         print(json.dumps(run_gemm_skinny(torch, dev)))
         return 0
+    if args.only == "gemm16k":
+        print(json.dumps(run_gemm_l16384(torch, dev)))
+        return 0
+    if args.only == "refshapes":
+        print(json.dumps(run_reference_shapes(torch, dev, not args.no_cpu_baseline)))
+        return 0
     if args.only == "flow":
         print(json.dumps(run_flow(torch, dev, 3, not args.no_cpu_baseline, args.validate_flow)))
         return 0
@@ -679,6 +851,8 @@ def main():
     sdpa_opt_in = run_sdpa_opt_in(torch, dev, host, kernel_ms)
     gemm = run_gemm(torch, dev, 20, ref_parity=not args.no_cpu_baseline)
     gemm["skinny_m"] = run_gemm_skinny(torch, dev)
+    gemm["l16384"] = run_gemm_l16384(torch, dev)
+    refshapes = run_reference_shapes(torch, dev, not args.no_cpu_baseline)
     flow = None if args.no_flow else run_flow(torch, dev, 3, not args.no_cpu_baseline, args.validate_flow)
     cpu = None if args.no_cpu_baseline else cpu_baseline_sdpa(*host, gpu_out=sdpa_out)
 
@@ -713,6 +887,7 @@ def main():
         "sdpa_opt_in_bf16": sdpa_opt_in,
         "sdpa_config2": variants,
         "gemm_config0": gemm,
+        "reference_shapes": refshapes,
         "flow": flow,
     }
     print(json.dumps(line))
