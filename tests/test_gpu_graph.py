@@ -145,8 +145,8 @@ def test_graph_survives_workspace_growth_gemm(cuda):
 
 def test_graph_survives_workspace_growth_sdpa(cuda, hiplib):
     """The same for the SDPA's key-split partials: capture a call whose
-    split tail needs ~35 MB, grow the stream's buffer past 64 MiB with an
-    eager call of 511 query tiles, then replay."""
+    split tail needs ~17 MB (a 32 MiB buffer), grow the stream's buffer with
+    an eager call that needs ~35 MB, then replay."""
     import ctypes
 
     import torch
@@ -163,8 +163,8 @@ def test_graph_survives_workspace_growth_sdpa(cuda, hiplib):
         v = torch.randn((1, H, Lk, 64), generator=g0, device=cuda)
         return q, k, v
 
-    small = qkv(16, 8704, 1024)      # 272 tiles: 16 split 16 ways (34.6 MB)
-    large = qkv(7, 73 * 512, 128)    # 511 tiles: 255 split 2 ways (68.9 MB)
+    small = qkv(16, 8292, 512)       # 272 tiles: 16 split 8 ways (17.3 MB)
+    large = qkv(16, 8704, 1024)      # 272 tiles: 16 split 16 ways (34.6 MB)
     expected = native_sdpa_f32_ex(*small)
     expected_large = native_sdpa_f32_ex(*large)
     out = torch.empty_like(expected)

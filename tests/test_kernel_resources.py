@@ -24,7 +24,7 @@ BUDGET = {
     # opt-in bf16x3 / bf16 SDPA at 16 waves ([B,H,L,64] k/v): 8 waves spill
     # nothing but run 6 % slower
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb0ELi16ELi64ELi1ELi3E"): 40,
-    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3E"): 84,
+    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3E"): 88,
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi1E"): 32,
     # opt-in bf16 GEMM, 256x256 tile with the fused QKV epilogue
     ("nf24_gemm_bf16", "Bf16CfgILi256ELi256ELi2ELi4EEELi1ELb1ELi1E"): 8,

@@ -64,14 +64,15 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
   const int g = lane >> 5;
   const int l32 = lane & 31;
 
-  const int qblocks = (a.Lq + kBQ - 1) / kBQ;
   const TileWork w = tile_work(a);
-  const int tile = w.tile, k_begin = w.k_begin, k_end = w.k_end;
-  const int bh = tile / qblocks;
-  const int qb = tile % qblocks;
+  const int k_begin = w.k_begin, k_end = w.k_end;
+  int bh, qb;
+  tile_coords(a, w.tile, kBQ, bh, qb);
   const int h = bh % a.H;
   const int qrow = qb * kBQ + wave * 32 + l32;
   const bool q_ok = qrow < a.Lq;
+  // A wave whose 32 queries all lie past Lq only helps stage K/V.
+  const bool wave_live = qb * kBQ + wave * 32 < a.Lq;
 
   // Q fragment for this lane's query, pre-scaled into log2 units:
   // qf[hh][t] = q[8*hh + 4*g + t] * 0.125 * log2(e), so the MFMA yields the
@@ -145,6 +146,7 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
     constexpr int kGB = kSplit ? 1 : kNKB;
     constexpr int kGroupUnroll = kSplit ? 1 : kNKB;
     const bool tail = key0 + kBKV > a.Lk;
+    if (wave_live) {
 #pragma unroll kGroupUnroll
     for (int kb0 = 0; kb0 < kNKB; kb0 += kGB) {
       floatx16 s[kGB];
@@ -247,6 +249,7 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_kernel(SdpaArgs a) {
             for (int db = 0; db < 2; ++db) o[db] = mfma32x32x2(vf[db][e], s[i][4 * hh + e], o[db]);
         }
     }
+    }  // wave_live
 
     if (t + 1 < ntiles) store(buf ^ 1);
     __syncthreads();

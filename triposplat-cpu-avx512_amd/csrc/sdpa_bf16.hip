@@ -113,10 +113,11 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
   const int g = lane >> 5;
   const int l32 = lane & 31;
 
-  const int qblocks = (a.Lq + kBQ - 1) / kBQ;
   const TileWork w = tile_work(a);
-  const int bh = w.tile / qblocks;
-  const int qb = w.tile % qblocks;
+  int bh, qb;
+  tile_coords(a, w.tile, kBQ, bh, qb);
+  // A wave whose 32 queries all lie past Lq only helps stage K/V.
+  const bool wave_live = qb * kBQ + wave * 32 < a.Lq;
   const int h = bh % a.H;
   const int qrow = qb * kBQ + wave * 32 + l32;
   const bool q_ok = qrow < a.Lq;
@@ -225,6 +226,7 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
     const __bf16* vl_ = vlo[buf];
     const bool tail = key0 + kBKV > a.Lk;
 
+    if (wave_live) {
 #pragma unroll
     for (int kb0 = 0; kb0 < kNKB; kb0 += kGB) {
       floatx16 s[kGB];
@@ -311,6 +313,7 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
           }
         }
     }
+    }  // wave_live
 
     if (t + 1 < ntiles) store(buf ^ 1);
     __syncthreads();

@@ -87,6 +87,28 @@ __device__ __forceinline__ void fetch_units_kv(const SdpaArgs& a, const float* k
   vx = ok ? *reinterpret_cast<const floatx4*>(vbase + off) : floatx4{0, 0, 0, 0};
 }
 
+// (b*H + h, query block) of query tile `tile`.  When Lq is not a multiple of
+// kBQ, each head's last, partial tile is numbered after all the full tiles:
+// its waves past Lq skip the arithmetic, so partial tiles are cheap, and this
+// order puts them in the launch's last (key-split) round instead of among the
+// full tiles of the first rounds.
+__device__ __forceinline__ void tile_coords(const SdpaArgs& a, int tile, int kBQ, int& bh, int& qb) {
+  const int qblocks = (a.Lq + kBQ - 1) / kBQ;
+  if (a.Lq % kBQ == 0) {
+    bh = tile / qblocks;
+    qb = tile % qblocks;
+    return;
+  }
+  const int full = a.B * a.H * (qblocks - 1);
+  if (tile < full) {
+    bh = tile / (qblocks - 1);
+    qb = tile % (qblocks - 1);
+  } else {
+    bh = tile - full;
+    qb = qblocks - 1;
+  }
+}
+
 // Query tile and key range of this workgroup (see SdpaArgs).
 struct TileWork {
   int tile, part, k_begin, k_end;
@@ -114,10 +136,11 @@ template <int kBQ>
 __device__ __forceinline__ void store_rows(const SdpaArgs& a, const floatx16 (&o)[2], float m_run,
                                            float l_run) {
   const TileWork w = tile_work(a);
-  const int qblocks = (a.Lq + kBQ - 1) / kBQ;
-  const int bh = w.tile / qblocks, b = bh / a.H, h = bh % a.H, part = w.part;
+  int bh, qb;
+  tile_coords(a, w.tile, kBQ, bh, qb);
+  const int b = bh / a.H, h = bh % a.H, part = w.part;
   const int wave = threadIdx.x >> 6, g = (threadIdx.x >> 5) & 1, l32 = threadIdx.x & 31;
-  const int qrow = (w.tile % qblocks) * kBQ + wave * 32 + l32;
+  const int qrow = qb * kBQ + wave * 32 + l32;
   if (qrow >= a.Lq) return;  // lanes l and l ^ 32 share the query: both leave or neither
   const float lsum = pair_sum(l_run);
   if (part >= 0) {
@@ -163,8 +186,9 @@ __global__ __launch_bounds__(kCombineThreads) void sdpa_combine_kernel(SdpaArgs 
   const int64_t r = i / kD;  // (tail tile, query in tile)
   const int ptile = (int)(r / q_per_tile), qi = (int)(r % q_per_tile);
   const int tile = a.full_tiles + ptile;
-  const int qblocks = (a.Lq + q_per_tile - 1) / q_per_tile;
-  const int bh = tile / qblocks, qrow = (tile % qblocks) * q_per_tile + qi;
+  int bh, qb;
+  tile_coords(a, tile, q_per_tile, bh, qb);
+  const int qrow = qb * q_per_tile + qi;
   if (qrow >= a.Lq) return;
   const int64_t base = (int64_t)ptile * a.splits * q_per_tile + qi;
   float m = -INFINITY;
@@ -180,6 +204,32 @@ __global__ __launch_bounds__(kCombineThreads) void sdpa_combine_kernel(SdpaArgs 
   float* dst = a.out_blhd ? a.out + (((int64_t)b * a.Lq + qrow) * a.H + h) * kD
                           : a.out + ((int64_t)bh * a.Lq + qrow) * kD;
   dst[d] = o * (1.0f / l);
+}
+
+// Key ranges for each of the `rest` tiles of a partial last round.  Modelled
+// in units of one full tile over all keys: with s ranges the rest's full
+// tiles make ceil(full * s / cus) rounds of 1/s each, plus a fixed cost per
+// piece (its prologue, Q load and partial store) of 2 % of a tile; partial
+// tiles (numbered last, see tile_coords) cost little and are not counted.
+// rest * s stays within 2 * cus, so the partials need at most
+// (2 * cus - 1) * kBQ rows of workspace; s <= 16.
+inline int choose_splits(const SdpaParams& p, int kBQ, int64_t rest, int cus) {
+  const int64_t partial = (p.Lq % kBQ != 0) ? (int64_t)p.B * p.H : 0;
+  const int64_t full = rest > partial ? rest - partial : 0;
+  if (full == 0) {  // only partial tiles: spread them over the CUs
+    const int64_t s = (cus + rest - 1) / rest;
+    return (int)(s < 16 ? s : 16);
+  }
+  int best = 1;
+  double best_t = 1e30;
+  for (int s = 1; s <= 16 && rest * s <= 2 * (int64_t)cus; ++s) {
+    const double t = (double)((full * s + cus - 1) / cus) * (1.0 / s + 0.02);
+    if (t < best_t - 1e-9) {
+      best_t = t;
+      best = s;
+    }
+  }
+  return best;
 }
 
 // Launches `main(grid, args)` over the query tiles of kBQ queries.  A last
@@ -199,10 +249,9 @@ int launch_tiles(SdpaArgs a, const SdpaParams& p, int kBQ, int kBKV, int cus, hi
   a.keys_per_split = p.Lk;
   const int64_t rest = cus > 0 ? tiles % cus : 0;
   if (cus > 0 && tiles >= cus && rest != 0) {
-    int splits = (int)((cus + rest - 1) / rest);
-    if (splits > 16) splits = 16;
-    const int kps = ((p.Lk + splits - 1) / splits + kBKV - 1) / kBKV * kBKV;
-    splits = (p.Lk + kps - 1) / kps;
+    const int splits0 = choose_splits(p, kBQ, rest, cus);
+    const int kps = ((p.Lk + splits0 - 1) / splits0 + kBKV - 1) / kBKV * kBKV;
+    const int splits = (p.Lk + kps - 1) / kps;
     if (splits >= 2) {
       const size_t items = (size_t)rest * splits * kBQ;
       const size_t need = items * (kD + 2) * 4;
