@@ -151,3 +151,59 @@ def test_materialize_decodes_exactly(oracle, cuda, tmp_path):
     assert y.shape == (9, 17) and bool(torch.isfinite(y).all())
     assert torch.allclose(yr, yf[:, 16:48], rtol=1e-5, atol=1e-6)
     assert meta["runtime"]["range_calls"] == 1
+
+
+def test_reference_written_directory_interchange(oracle, cuda, tmp_path):
+    """The directory the reference's own writer produced
+    (tests/golden/prepacked_toy, see make_prepacked_golden.py) against this
+    package: (1) packing the same source checkpoint here gives the same
+    manifest (the float quantization statistics to 1e-5 relative, everything
+    else equal) and byte-identical shard files (same sha256); (2) the
+    reference-written directory loads through load_nf24_i16_prepacked_model
+    with checksum verification and runs the toy model on the device, matching
+    the oracle GEMM chain on the decoded weights."""
+    from pathlib import Path
+
+    import torch
+    from safetensors.numpy import load_file as load_np
+    from tsplat import nf24_prepacked as P
+    from tsplat.native_linear_rnf8_patch import apply_triposplat_native_rnf8_avx512_patch
+
+    golden = Path(__file__).resolve().parent / "golden"
+    ref_dir = golden / "prepacked_toy"
+    ref_manifest = json.loads((ref_dir / "manifest.json").read_text())
+    src = tmp_path / "prepacked_toy_source.safetensors"   # same name: the manifest records it
+    shutil.copy(golden / "prepacked_toy_source.safetensors", src)
+    ours = P.pack_nf24_i16_checkpoint(src, tmp_path / "ours", expected_linear_count=2)
+
+    def strip(m):
+        m = json.loads(json.dumps(m))
+        stats = {}
+        for name, e in m["linears"].items():
+            stats[name] = e.pop("quantization")
+        return m, stats
+
+    a, sa = strip(ours)
+    b, sb = strip(ref_manifest)
+    assert a == b                                         # names, files, sha256, sizes, shapes, source
+    for name in sa:
+        qa, qb = sa[name], sb[name]
+        assert sorted(qa) == sorted(qb)
+        assert qa["nf8_derived_alphabet_size"] == qb["nf8_derived_alphabet_size"] == 163
+        for st_a, st_b in zip(qa["stages"], qb["stages"]):
+            assert st_a["saturated_values"] == st_b["saturated_values"]
+            assert st_a["quantizer"] == st_b["quantizer"]
+            for key in ("residual_max_abs", "residual_rmse"):
+                assert abs(st_a[key] - st_b[key]) <= 1e-5 * abs(st_b[key]) + 1e-12, (name, key)
+
+    ToyModel = _toy()
+    model = P.load_nf24_i16_prepacked_model(ref_dir, ToyModel, verify_checksums=True).eval()
+    meta = apply_triposplat_native_rnf8_avx512_patch(
+        model, enabled=True, include_regex=r".*", threads=2, strict=True, stages=3, residual_mode="nf24_i16")
+    assert meta["selected_count"] == 2 and meta["prepacked_load"]["checksums_verified"] is True
+    x = np.random.default_rng(8).standard_normal((25, 96)).astype(np.float32)
+    with torch.inference_mode():
+        h1 = model.fc1(torch.from_numpy(x).to(cuda)).cpu().numpy()
+    shard = load_np((ref_dir / ref_manifest["linears"]["fc1"]["file"]).as_posix())
+    want = oracle.nf24_gemm(x, shard["code01_t"], shard["q2_t"], shard["scale"], shard["bias"])
+    assert np.abs(h1 - want).max() <= 2e-5

@@ -76,20 +76,51 @@ def quantize_nf24_i16_per_output_channel(weight, codebook=None):
             code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), current_stream_handle(device),
         )
     check_status(status, "tsplat_nf24_pack_async")
-    decoded = decode_nf24_i16_weight(code01_t, q2_t, scale)
-    diff = decoded - w
-    weight_rms = float(torch.sqrt(torch.mean(w * w)).item())
-    rmse = float(torch.sqrt(torch.mean(diff * diff)).item())
-    error = {
-        "weight_rmse": rmse,
-        "weight_max_abs": float(diff.abs().max().item()),
-        "weight_rms": weight_rms,
-        "weight_relative_rmse": rmse / max(weight_rms, 1.0e-30),
-        "residual_mode": FORMAT_NAME,
-        "storage_layout": "int16(q0*4+q1) + int8(q2)",
-        "nf8_derived_alphabet_size": int(alphabet.numel()),
-    }
+    error = _stage_errors(torch, w, base, alphabet)
     return [code01_t, q2_t, q2_t], [scale, scale, scale], error
+
+
+def _stage_errors(torch, w, base, alphabet):
+    """The packer's error report, keys and statistics as the reference's
+    (native_linear_rnf8_avx512_patch.py:38-87): the residual left after each
+    digit -- the NF8-derived level q0 at the base scale, then the radix-4 and
+    radix-1024 corrections -- with its RMSE, max-abs and the count of
+    corrections clamped to int8; weight_rmse / weight_max_abs are those of the
+    last residual.  The digits are recomputed here with the same fp32
+    elementwise steps as the packing kernel (the int16 code 4 q0 + q1 does not
+    give the digits back); base is the kernel's max|row| / 127."""
+    b = base[:, None]
+    midpoints = ((alphabet[:-1] + alphabet[1:]) * 0.5).contiguous()
+    q0 = alphabet[torch.bucketize(w / b, midpoints)]
+    r1 = w - q0 * b
+    s1 = b / 4.0
+    q1u = torch.floor(r1 / s1 + 0.5)
+    r2 = r1 - q1u.clamp(-128, 127) * s1
+    s2 = b / 1024.0
+    q2u = torch.floor(r2 / s2 + 0.5)
+    r3 = r2 - q2u.clamp(-128, 127) * s2
+    stages = []
+    for stage, (rem, quantizer, unclamped) in enumerate(
+            ((r1, "nf8_derived_int8_alphabet", None), (r2, "shared_scale_int8_radix4", q1u),
+             (r3, "shared_scale_int8_radix256", q2u)), start=1):
+        stages.append({
+            "stage": stage,
+            "quantizer": quantizer,
+            "residual_rmse": float(torch.sqrt(torch.mean(rem * rem)).item()),
+            "residual_max_abs": float(rem.abs().max().item()),
+            "saturated_values": 0 if unclamped is None else int(((unclamped < -128) | (unclamped > 127)).sum().item()),
+        })
+    weight_rms = float(torch.sqrt(torch.mean(w * w)).item())
+    return {
+        "weight_rmse": stages[-1]["residual_rmse"],
+        "weight_max_abs": stages[-1]["residual_max_abs"],
+        "weight_rms": weight_rms,
+        "weight_relative_rmse": stages[-1]["residual_rmse"] / max(weight_rms, 1.0e-30),
+        "residual_mode": FORMAT_NAME,
+        "nf8_derived_alphabet_size": int(alphabet.numel()),
+        "stages": stages,
+        "storage_layout": "int16(q0*4+q1) + int8(q2)",
+    }
 
 
 def _decode(code01_t, q2_t, scale, transposed):
