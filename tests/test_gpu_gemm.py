@@ -69,11 +69,12 @@ SHAPES = [(25, 96, 64), (40, 96, 64), (10, 96, 64), (3, 96, 5), (1, 1024, 3072),
           (9, 1024, 520), (13, 2048, 1024),
           # more K splits than the staged merge holds: the one-thread-per-output merge
           (1, 40000, 96),
-          # the MFMA few-row form (6..16 rows, >= 96 slabs of 32 columns): every row count
-          # at its edges, ragged K (a partial last chunk and a partial last wave), a K
-          # that only two waves reach, the wide N
+          # the MFMA few-row form (4..16 rows, >= 192 slabs of 16 columns; 32-column slabs
+          # where those alone give 192): both slab widths, the row-count edges, ragged K (a
+          # partial last chunk and a partial last wave), a K only two waves reach; 3 rows and
+          # 190 slabs stay on the split kernel
           (6, 1024, 3072), (8, 1000, 3072), (11, 2048, 6144), (16, 40, 3072), (13, 4100, 3104),
-          (5, 1024, 3072), (16, 1024, 3040)]
+          (4, 1024, 6144), (4, 96, 3072), (3, 1024, 3072), (16, 1024, 3040)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)

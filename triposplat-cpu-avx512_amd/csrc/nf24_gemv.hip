@@ -295,7 +295,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void nf24_gemv_wide_kernel(GemvArg
 }
 
 // ---------------------------------------------------------------------------
-// MFMA form for M <= 16 (columns, column offset and N multiples of kCols,
+// MFMA form for 4 <= M <= 16 (columns, column offset and N multiples of kCols,
 // 16-byte aligned codes, scales and x rows): one workgroup owns kCols
 // columns over the whole K range, so no partial sums leave the chip and no
 // second kernel runs.  Each wave takes consecutive 32-row chunks of K
@@ -324,7 +324,10 @@ __global__ __launch_bounds__(kWaves * 64) void nf24_gemv_mfma_kernel(GemvArgs a)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int c0 = blockIdx.x * kCols;                 // first local column of the slab
+  // Neighbouring slabs share cache lines (a 32-column slab is half a 128-byte
+  // line of code01 and a quarter of one of q2): each XCD takes a contiguous
+  // run of slabs so that a line is fetched into one L2, not up to four.
+  const int c0 = xcd_tile_index(blockIdx.x, gridDim.x) * kCols;  // first local column of the slab
   const int cg = lane % kLanesPerRow, lr = lane / kLanesPerRow;
   const int64_t ncol = a.n_start + c0 + 8 * cg;      // this lane's first column
   const int kw0 = wave * a.k_per_split;              // k_per_split: rows per wave
@@ -517,39 +520,45 @@ int launch_mt(GemvArgs a, int cgroups, int splits, hipStream_t stream) {
 // the partial sums (splits * M * count * 8 bytes) stay under half the weight
 // bytes; a split costs a second, small kernel.
 namespace {
-// The MFMA form: 32-column slabs, 8 waves, all loads of 4 chunks in flight.
-// Measured against the K-split wide kernel (cold weights, HIP-graph replay,
-// per call): at N = 3072 / 6144, K = 1024 it is 10.1 / 11.6 us for every M
-// <= 16, where the split kernel takes 7.2 / 9.4 us at M = 1 and 16.3 / 22.0
-// us at M = 16 (the crossing is near M = 6); with fewer than 96 slabs
-// (N = 1024, K = 4096: 27-29 us against 9-19 us) too few CUs stream.
-// 64-column slabs and 4 or 16 waves measured slower.
-constexpr int kMfmaCols = 32;
+// The MFMA form, 8 waves, all loads of 4 chunks in flight, slabs of 32
+// columns when that gives at least 192 workgroups, else of 16 (N = 3072:
+// 192 slabs of 16).  Measured against the K-split wide kernel (cold weights,
+// HIP-graph replay, per call; M = 16 / 8 / 4): N = 3072, K = 1024: 8.4 /
+// 8.3 / ~8.2 us (16-column slabs; 32-column: 9.9 / 9.6) against 16.3 / 11.4 /
+// 9.1 us; N = 6144: 10.5 / 10.2 / ~10.2 us (32-column; 16-column: 13.9 /
+// 13.4) against 22.0 / 14.9 / 11.3 us.  With fewer than 192 slabs of 16
+// (N = 1024, K = 4096) too few CUs stream, and at M <= 2 the split kernel
+// is faster (7.2-9.5 us), so those stay on it.  64-column slabs and 4 or 16
+// waves measured slower.
 constexpr int kMfmaWaves = 8;
-constexpr int kMfmaMinRows = 6;
-constexpr int kMfmaMinSlabs = 96;
+constexpr int kMfmaMinRows = 4;
+constexpr int kMfmaMinWorkgroups = 192;
 
+template <int kCols>
 int launch_mfma_form(const GemmParams& p, hipStream_t stream) {
   const int per_wave =
       ((p.K + kMfmaWaves * kMfmaRows - 1) / (kMfmaWaves * kMfmaRows)) * kMfmaRows;
   GemvArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out, nullptr, p.M, p.K, p.N,
              p.n_start, p.n_count, p.stride_x, p.stride_out, per_wave, 1};
-  hipLaunchKernelGGL((nf24_gemv_mfma_kernel<kMfmaCols, kMfmaWaves, 4>),
-                     dim3((unsigned)(p.n_count / kMfmaCols)), dim3(kMfmaWaves * 64), 0, stream, a);
+  hipLaunchKernelGGL((nf24_gemv_mfma_kernel<kCols, kMfmaWaves, 4>),
+                     dim3((unsigned)(p.n_count / kCols)), dim3(kMfmaWaves * 64), 0, stream, a);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 }  // namespace
 
 int launch_nf24_gemv(const GemmParams& p, hipStream_t stream) {
   if (p.M < 1 || p.M > 32) return kErrDims;
-  const bool mfma_ok = p.M >= kMfmaMinRows && p.M <= 16 &&
-                       ((p.N | p.n_start | p.n_count) % kMfmaCols) == 0 &&
-                       p.n_count / kMfmaCols >= kMfmaMinSlabs && (p.stride_x & 3) == 0 &&
+  const bool mfma_ok = p.M >= kMfmaMinRows && p.M <= 16 && ((p.N | p.n_start | p.n_count) % 16) == 0 &&
+                       p.n_count / 16 >= kMfmaMinWorkgroups && (p.stride_x & 3) == 0 &&
                        (reinterpret_cast<uintptr_t>(p.x) & 15) == 0 &&
                        (reinterpret_cast<uintptr_t>(p.code01) & 15) == 0 &&
                        (reinterpret_cast<uintptr_t>(p.q2) & 15) == 0 &&
                        (reinterpret_cast<uintptr_t>(p.scale) & 15) == 0;
-  if (mfma_ok) return launch_mfma_form(p, stream);
+  if (mfma_ok) {
+    if (((p.N | p.n_start | p.n_count) % 32) == 0 && p.n_count / 32 >= kMfmaMinWorkgroups)
+      return launch_mfma_form<32>(p, stream);
+    return launch_mfma_form<16>(p, stream);
+  }
   const bool wide = p.M <= 16 && ((p.N | p.n_start | p.n_count) & 7) == 0 &&
                     (reinterpret_cast<uintptr_t>(p.code01) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(p.q2) & 7) == 0 &&
