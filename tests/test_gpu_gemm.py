@@ -203,6 +203,50 @@ def test_reference_named_entry_points(oracle, cuda, hiplib):
     assert hiplib.triposplat_gemm_rnf8_avx512_residual_mode() == 4
 
 
+def test_pointer_checks_within_one_allocation(oracle, cuda, hiplib):
+    """A call's pointer checks accept a range inside an allocation an earlier
+    check of the same call validated without asking the runtime again; a
+    pointer into that same allocation whose extent runs past its end must
+    still be rejected with -6 before any launch, and the in-bounds call must
+    equal the same GEMM on separate tensors bit for bit."""
+    import torch
+
+    M, K, N = 8, 256, 512
+    x, w, b = seeded_linear(M, M, K, N, w_scale=0.02)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    ref = _run_async(torch, hiplib, cuda, x, c01, q2, s, b)
+    hip = ctypes.CDLL("libamdhip64.so")
+    size = 4 << 20
+    base = ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(base), ctypes.c_size_t(size)) == 0
+    try:
+        h2d = 1
+        def put(off, a):
+            a = np.ascontiguousarray(a)
+            assert hip.hipMemcpy(ctypes.c_void_p(base.value + off), a.ctypes.data_as(ctypes.c_void_p),
+                                 ctypes.c_size_t(a.nbytes), h2d) == 0
+        put(0, x)
+        put(65536, s)
+        put(131072, b)
+        d01, dq2 = _dev(torch, c01, cuda), _dev(torch, q2, cuda)
+        stream = torch.cuda.current_stream(cuda).cuda_stream
+        def call(out_off):
+            return hiplib.tsplat_nf24_gemm_async(
+                base.value, d01.data_ptr(), dq2.data_ptr(), base.value + 65536, base.value + 131072,
+                base.value + out_off, M, K, N, 0, N, K, N, stream)
+        assert call(size - M * N * 4 + 4) == -6          # 4 bytes past the allocation's end
+        assert call(size - M * N * 4) == 0               # ends exactly at the end
+        torch.cuda.synchronize(cuda)
+        got = np.empty((M, N), np.float32)
+        assert hip.hipMemcpy(got.ctypes.data_as(ctypes.c_void_p),
+                             ctypes.c_void_p(base.value + size - M * N * 4),
+                             ctypes.c_size_t(got.nbytes), 2) == 0
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    finally:
+        torch.cuda.synchronize(cuda)
+        assert hip.hipFree(base) == 0
+
+
 @pytest.mark.parametrize("M,K,N", [(16385, 1024, 1024), (8194, 1024, 3072)])
 def test_gemm_tail_rows(oracle, cuda, hiplib, M, K, N):
     """M = 256 k + r with r <= 32 (e.g. the compressed negative branch, L + 1

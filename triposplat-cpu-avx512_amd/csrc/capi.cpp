@@ -32,12 +32,18 @@ int note(hipError_t e) {
   return e == hipSuccess ? kOk : kErrLaunch;
 }
 
-// The allocation containing [p, p + bytes) must be device (or managed) memory
-// of the current device.  This turns a wrong pointer into a status code
-// instead of a GPU memory fault.
-int check_dev(const void* p, int64_t bytes) {
+int DeviceRanges::check(const void* p, int64_t bytes) {
   if (p == nullptr) return kErrNull;
   if (bytes <= 0) return kOk;
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+  if ((uint64_t)bytes > UINTPTR_MAX - lo) return kErrPointer;
+  const uintptr_t hi = lo + (uintptr_t)bytes;
+  for (int i = 0; i < count_; ++i)
+    if (lo >= lo_[i] && hi <= hi_[i]) return kOk;
+  if (device_ < 0 && hipGetDevice(&device_) != hipSuccess) {
+    device_ = -1;
+    return kErrPointer;
+  }
   hipPointerAttribute_t attr;
   hipError_t e = hipPointerGetAttributes(&attr, p);
   if (e != hipSuccess) {
@@ -45,8 +51,7 @@ int check_dev(const void* p, int64_t bytes) {
     return kErrPointer;
   }
   if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged) return kErrPointer;
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || attr.device != dev) return kErrPointer;
+  if (attr.device != device_) return kErrPointer;
   hipDeviceptr_t base = nullptr;
   size_t size = 0;
   e = hipMemGetAddressRange(&base, &size, const_cast<void*>(p));
@@ -54,9 +59,13 @@ int check_dev(const void* p, int64_t bytes) {
     (void)hipGetLastError();
     return kErrPointer;
   }
-  const char* lo = static_cast<const char*>(base);
-  const char* q = static_cast<const char*>(p);
-  if (q < lo || (uint64_t)(q - lo) + (uint64_t)bytes > (uint64_t)size) return kErrPointer;
+  const uintptr_t base_lo = reinterpret_cast<uintptr_t>(base);
+  if (lo < base_lo || hi - base_lo > (uintptr_t)size) return kErrPointer;
+  if (count_ < kMaxRanges) {
+    lo_[count_] = base_lo;
+    hi_[count_] = base_lo + (uintptr_t)size;
+    ++count_;
+  }
   return kOk;
 }
 
@@ -78,12 +87,13 @@ int sdpa_checked(const float* q, const float* k, const float* v, const float* bi
   if (has_bias && bias_head_stride != 0 && bias_head_stride < Lk) return kErrRange;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return kErrAlign;
   const int64_t bh = (int64_t)B * H;
-  TSPLAT_CHECK(check_dev(q, bh * Lq * kSdpaHeadDim * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(q, bh * Lq * kSdpaHeadDim * 4));
   const int64_t kv_elems = kv_packed ? bh * kSdpaHeadDim * Lkp : bh * Lk * kSdpaHeadDim;
-  TSPLAT_CHECK(check_dev(k, kv_elems * 4));
-  TSPLAT_CHECK(check_dev(v, kv_elems * 4));
-  TSPLAT_CHECK(check_dev(out, bh * Lq * kSdpaHeadDim * 4));
-  if (has_bias) TSPLAT_CHECK(check_dev(bias, ((int64_t)(H - 1) * bias_head_stride + Lk) * 4));
+  TSPLAT_CHECK(ptrs.check(k, kv_elems * 4));
+  TSPLAT_CHECK(ptrs.check(v, kv_elems * 4));
+  TSPLAT_CHECK(ptrs.check(out, bh * Lq * kSdpaHeadDim * 4));
+  if (has_bias) TSPLAT_CHECK(ptrs.check(bias, ((int64_t)(H - 1) * bias_head_stride + Lk) * 4));
   SdpaParams p{q, k, v, has_bias ? bias : nullptr, out, B, H, Lq, Lk, kv_packed, Lkp,
                bias_head_stride, out_blhd, precision, scratch, scratch_bytes};
   const int st = launch_sdpa(p, stream);
@@ -113,12 +123,13 @@ std::atomic<uint64_t> g_sdpa_free_ns{0};
 int gemm_checked(const float* x, const int16_t* code01, const int8_t* q2, const float* scale,
                  const float* bias, float* out, int M, int K, int N, int start, int count,
                  int stride_x, int stride_out, hipStream_t stream) {
-  TSPLAT_CHECK(check_dev(x, ((int64_t)(M - 1) * stride_x + K) * 4));
-  TSPLAT_CHECK(check_dev(code01, (int64_t)K * N * 2));
-  TSPLAT_CHECK(check_dev(q2, (int64_t)K * N));
-  TSPLAT_CHECK(check_dev(scale, (int64_t)N * 4));
-  TSPLAT_CHECK(check_dev(bias, (int64_t)N * 4));
-  TSPLAT_CHECK(check_dev(out, ((int64_t)(M - 1) * stride_out + count) * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(x, ((int64_t)(M - 1) * stride_x + K) * 4));
+  TSPLAT_CHECK(ptrs.check(code01, (int64_t)K * N * 2));
+  TSPLAT_CHECK(ptrs.check(q2, (int64_t)K * N));
+  TSPLAT_CHECK(ptrs.check(scale, (int64_t)N * 4));
+  TSPLAT_CHECK(ptrs.check(bias, (int64_t)N * 4));
+  TSPLAT_CHECK(ptrs.check(out, ((int64_t)(M - 1) * stride_out + count) * 4));
   GemmParams p{x, code01, q2, scale, bias, out, M, K, N, start, count, stride_x, stride_out};
   const int st = launch_nf24_gemm(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
@@ -165,13 +176,14 @@ int post_checked(const float* qkv, const float* freqs, const float* qg, const fl
       !aligned16(q) || !aligned16(pk) || !aligned16(pv))
     return kErrAlign;
   const int64_t C = (int64_t)H * kHeadDim;
-  TSPLAT_CHECK(check_dev(qkv, (int64_t)B * L * 3 * C * 4));
-  TSPLAT_CHECK(check_dev(freqs, (int64_t)fb * L * C * 4));
-  TSPLAT_CHECK(check_dev(qg, C * 4));
-  TSPLAT_CHECK(check_dev(kg, C * 4));
-  TSPLAT_CHECK(check_dev(q, (int64_t)B * L * C * 4));
-  TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * Lp * 4));
-  TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lp * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(qkv, (int64_t)B * L * 3 * C * 4));
+  TSPLAT_CHECK(ptrs.check(freqs, (int64_t)fb * L * C * 4));
+  TSPLAT_CHECK(ptrs.check(qg, C * 4));
+  TSPLAT_CHECK(ptrs.check(kg, C * 4));
+  TSPLAT_CHECK(ptrs.check(q, (int64_t)B * L * C * 4));
+  TSPLAT_CHECK(ptrs.check(pk, (int64_t)B * C * Lp * 4));
+  TSPLAT_CHECK(ptrs.check(pv, (int64_t)B * C * Lp * 4));
   QkvPostParams p{qkv, freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb, kv_round};
   const int st = launch_qkv_postprocess(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
@@ -189,15 +201,16 @@ int selected_checked(const float* q, const float* kv, const float* freqs, const 
     return kErrDims;
   if (!aligned16(pk) || !aligned16(pv)) return kErrAlign;
   const int64_t C = (int64_t)H * kHeadDim;
-  TSPLAT_CHECK(check_dev(q, (int64_t)B * Lq * C * 4));
-  TSPLAT_CHECK(check_dev(kv, (int64_t)B * Lk * 2 * C * 4));
-  TSPLAT_CHECK(check_dev(freqs, (int64_t)fb * Lk * C * 4));
-  TSPLAT_CHECK(check_dev(sel, (int64_t)Lq * 8));
-  TSPLAT_CHECK(check_dev(qg, C * 4));
-  TSPLAT_CHECK(check_dev(kg, C * 4));
-  TSPLAT_CHECK(check_dev(q_out, (int64_t)B * Lq * C * 4));
-  TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * Lkp * 4));
-  TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * Lkp * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(q, (int64_t)B * Lq * C * 4));
+  TSPLAT_CHECK(ptrs.check(kv, (int64_t)B * Lk * 2 * C * 4));
+  TSPLAT_CHECK(ptrs.check(freqs, (int64_t)fb * Lk * C * 4));
+  TSPLAT_CHECK(ptrs.check(sel, (int64_t)Lq * 8));
+  TSPLAT_CHECK(ptrs.check(qg, C * 4));
+  TSPLAT_CHECK(ptrs.check(kg, C * 4));
+  TSPLAT_CHECK(ptrs.check(q_out, (int64_t)B * Lq * C * 4));
+  TSPLAT_CHECK(ptrs.check(pk, (int64_t)B * C * Lkp * 4));
+  TSPLAT_CHECK(ptrs.check(pv, (int64_t)B * C * Lkp * 4));
   QkvSelectedParams p{q, kv, freqs, sel, qg, kg, q_out, pk, pv, B, Lq, Lk, H, Lkp, fb, kv_round};
   const int st = launch_qkv_selected_postprocess(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
@@ -223,18 +236,19 @@ int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
   if (M > 0x7fffffff) return kErrDims;
   if (!aligned16(pk) || !aligned16(pv)) return kErrAlign;
   const int64_t C = (int64_t)H * kHeadDim;
-  TSPLAT_CHECK(check_dev(x, M * K * 4));
-  TSPLAT_CHECK(check_dev(code01, (int64_t)K * N * 2));
-  TSPLAT_CHECK(check_dev(q2, (int64_t)K * N));
-  TSPLAT_CHECK(check_dev(scale, (int64_t)N * 4));
-  TSPLAT_CHECK(check_dev(bias, (int64_t)N * 4));
-  TSPLAT_CHECK(check_dev(freqs, (int64_t)fb * L * C * 4));
-  TSPLAT_CHECK(check_dev(qg, C * 4));
-  TSPLAT_CHECK(check_dev(kg, C * 4));
-  TSPLAT_CHECK(check_dev(q, M * C * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(x, M * K * 4));
+  TSPLAT_CHECK(ptrs.check(code01, (int64_t)K * N * 2));
+  TSPLAT_CHECK(ptrs.check(q2, (int64_t)K * N));
+  TSPLAT_CHECK(ptrs.check(scale, (int64_t)N * 4));
+  TSPLAT_CHECK(ptrs.check(bias, (int64_t)N * 4));
+  TSPLAT_CHECK(ptrs.check(freqs, (int64_t)fb * L * C * 4));
+  TSPLAT_CHECK(ptrs.check(qg, C * 4));
+  TSPLAT_CHECK(ptrs.check(kg, C * 4));
+  TSPLAT_CHECK(ptrs.check(q, M * C * 4));
   const int64_t kv_keys = kv_layout == 1 ? L : Lp;
-  TSPLAT_CHECK(check_dev(pk, (int64_t)B * C * kv_keys * 4));
-  TSPLAT_CHECK(check_dev(pv, (int64_t)B * C * kv_keys * 4));
+  TSPLAT_CHECK(ptrs.check(pk, (int64_t)B * C * kv_keys * 4));
+  TSPLAT_CHECK(ptrs.check(pv, (int64_t)B * C * kv_keys * 4));
   // RoPE, RMSNorm and the q / packed k,v stores run in the GEMM's epilogue.
   QkvFusedParams p{{x, code01, q2, scale, bias, nullptr, (int)M, K, N, 0, N, K, N, precision},
                    freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb, kv_layout, kv_round};
@@ -471,7 +485,8 @@ int triposplat_q_kv_selected_rope_rmsnorm_pack_f32_avx512_v2(
     return kErrDims;
   // The reference rejects an index outside [0, Lk) with -3 before any work;
   // the indices are device data, so they are read back first.
-  TSPLAT_CHECK(check_dev(selected_indices, (int64_t)Lq * 8));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(selected_indices, (int64_t)Lq * 8));
   std::vector<int64_t> host((size_t)Lq);
   if (note(hipMemcpy(host.data(), selected_indices, (size_t)Lq * 8, hipMemcpyDeviceToHost)) != kOk)
     return kErrLaunch;
@@ -538,12 +553,13 @@ int tsplat_nf24_pack_async(const float* weight, int out_features, int in_feature
   if (out_features <= 0 || in_features <= 0 || alphabet_len < 2 || alphabet_len > 256)
     return kErrDims;
   const int64_t count = (int64_t)out_features * in_features;
-  TSPLAT_CHECK(check_dev(weight, count * 4));
-  TSPLAT_CHECK(check_dev(alphabet, (int64_t)alphabet_len * 4));
-  TSPLAT_CHECK(check_dev(base_workspace, (int64_t)out_features * 4));
-  TSPLAT_CHECK(check_dev(code01_t, count * 2));
-  TSPLAT_CHECK(check_dev(q2_t, count));
-  TSPLAT_CHECK(check_dev(scale, (int64_t)out_features * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(weight, count * 4));
+  TSPLAT_CHECK(ptrs.check(alphabet, (int64_t)alphabet_len * 4));
+  TSPLAT_CHECK(ptrs.check(base_workspace, (int64_t)out_features * 4));
+  TSPLAT_CHECK(ptrs.check(code01_t, count * 2));
+  TSPLAT_CHECK(ptrs.check(q2_t, count));
+  TSPLAT_CHECK(ptrs.check(scale, (int64_t)out_features * 4));
   const int st = launch_nf24_pack(weight, out_features, in_features, alphabet, alphabet_len,
                                   base_workspace, code01_t, q2_t, scale,
                                   static_cast<hipStream_t>(stream));
@@ -557,10 +573,11 @@ int tsplat_nf24_decode_async(const int16_t* code01_t, const int8_t* q2_t, const 
   if (!code01_t || !q2_t || !scale || !out) return kErrNull;
   if (in_features <= 0 || out_features <= 0) return kErrDims;
   const int64_t count = (int64_t)in_features * out_features;
-  TSPLAT_CHECK(check_dev(code01_t, count * 2));
-  TSPLAT_CHECK(check_dev(q2_t, count));
-  TSPLAT_CHECK(check_dev(scale, (int64_t)out_features * 4));
-  TSPLAT_CHECK(check_dev(out, count * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(code01_t, count * 2));
+  TSPLAT_CHECK(ptrs.check(q2_t, count));
+  TSPLAT_CHECK(ptrs.check(scale, (int64_t)out_features * 4));
+  TSPLAT_CHECK(ptrs.check(out, count * 4));
   const int st = launch_nf24_decode(code01_t, q2_t, scale, out, in_features, out_features,
                                     transposed ? 1 : 0, static_cast<hipStream_t>(stream));
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);

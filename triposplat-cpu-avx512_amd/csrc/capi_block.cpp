@@ -40,16 +40,17 @@ int layernorm_checked(const float* input, const float* weight, const float* bias
   const bool modulate = scale != nullptr || shift != nullptr;
   if (modulate && (!scale || !shift || rows_per_batch <= 0 || mod_batch_stride < cols))
     return kErrRange;
-  TSPLAT_CHECK(check_dev(input, rows * cols * 4));
-  TSPLAT_CHECK(check_dev(output, rows * cols * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(input, rows * cols * 4));
+  TSPLAT_CHECK(ptrs.check(output, rows * cols * 4));
   if (has_affine) {
-    TSPLAT_CHECK(check_dev(weight, (int64_t)cols * 4));
-    TSPLAT_CHECK(check_dev(bias, (int64_t)cols * 4));
+    TSPLAT_CHECK(ptrs.check(weight, (int64_t)cols * 4));
+    TSPLAT_CHECK(ptrs.check(bias, (int64_t)cols * 4));
   }
   if (modulate) {
     const int64_t batches = (rows + rows_per_batch - 1) / rows_per_batch;
-    TSPLAT_CHECK(check_dev(scale, ((batches - 1) * mod_batch_stride + cols) * 4));
-    TSPLAT_CHECK(check_dev(shift, ((batches - 1) * mod_batch_stride + cols) * 4));
+    TSPLAT_CHECK(ptrs.check(scale, ((batches - 1) * mod_batch_stride + cols) * 4));
+    TSPLAT_CHECK(ptrs.check(shift, ((batches - 1) * mod_batch_stride + cols) * 4));
   }
   LayerNormParams p{input, weight, bias, output, rows, cols, eps, has_affine ? 1 : 0,
                     modulate ? 1 : 0, scale, shift, mod_batch_stride,
@@ -64,9 +65,10 @@ int head_rmsnorm_checked(const float* input, int64_t in_token_stride, const floa
   if (B <= 0 || L <= 0 || H <= 0 || dim <= 0 || !(eps >= 0.0f)) return kErrDims;
   if (in_token_stride < (int64_t)H * dim) return kErrRange;
   const int64_t tokens = (int64_t)B * L;
-  TSPLAT_CHECK(check_dev(input, ((tokens - 1) * in_token_stride + (int64_t)H * dim) * 4));
-  TSPLAT_CHECK(check_dev(output, tokens * H * dim * 4));
-  if (normalize) TSPLAT_CHECK(check_dev(gamma, (int64_t)H * dim * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(input, ((tokens - 1) * in_token_stride + (int64_t)H * dim) * 4));
+  TSPLAT_CHECK(ptrs.check(output, tokens * H * dim * 4));
+  if (normalize) TSPLAT_CHECK(ptrs.check(gamma, (int64_t)H * dim * 4));
   HeadNormParams p{input, gamma, output, B, L, H, dim, in_token_stride, eps, out_bhld ? 1 : 0,
                    normalize ? 1 : 0};
   return launched(launch_head_rmsnorm(p, stream));
@@ -80,9 +82,10 @@ int rope_checked(const float* input, const float* freqs, float* output, int64_t 
                         reinterpret_cast<uintptr_t>(output);
   if ((mis & 7u) != 0) return kErrAlign;
   const int64_t n = vectors * dim;
-  TSPLAT_CHECK(check_dev(input, n * 4));
-  TSPLAT_CHECK(check_dev(freqs, n * 4));
-  TSPLAT_CHECK(check_dev(output, n * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(input, n * 4));
+  TSPLAT_CHECK(ptrs.check(freqs, n * 4));
+  TSPLAT_CHECK(ptrs.check(output, n * 4));
   return launched(launch_rope_complex(input, freqs, output, n / 2, stream));
 }
 
@@ -91,21 +94,23 @@ int rows_op_checked(bool gated, float* x, float* y, const float* a, const float*
   if (!x || !a || (gated ? !y : !b)) return kErrNull;
   if (batch <= 0 || rows <= 0 || cols <= 0) return kErrDims;
   const int64_t n = (int64_t)batch * rows * cols;
-  TSPLAT_CHECK(check_dev(x, n * 4));
-  TSPLAT_CHECK(check_dev(a, (int64_t)batch * cols * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(x, n * 4));
+  TSPLAT_CHECK(ptrs.check(a, (int64_t)batch * cols * 4));
   if (gated) {
-    TSPLAT_CHECK(check_dev(y, n * 4));
+    TSPLAT_CHECK(ptrs.check(y, n * 4));
     return launched(launch_gated_residual(x, y, a, batch, rows, cols, stream));
   }
-  TSPLAT_CHECK(check_dev(b, (int64_t)batch * cols * 4));
+  TSPLAT_CHECK(ptrs.check(b, (int64_t)batch * cols * 4));
   return launched(launch_modulate(x, a, b, batch, rows, cols, stream));
 }
 
 int unary_checked(int op, const float* input, float* output, int64_t count, hipStream_t stream) {
   if (!input || !output) return kErrNull;
   if (count <= 0) return kErrDims;
-  TSPLAT_CHECK(check_dev(input, count * 4));
-  TSPLAT_CHECK(check_dev(output, count * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(input, count * 4));
+  TSPLAT_CHECK(ptrs.check(output, count * 4));
   switch (op) {
     case 0: return launched(launch_add(output, input, count, stream));
     case 1: return launched(launch_gelu_tanh(input, output, count, stream));
@@ -120,13 +125,14 @@ int sampler_checked(int op, float* x, const float* a, const float* p, const floa
   if (!x || !a || !s0 || (op == 2 && (!p || !s1))) return kErrNull;
   if (batch <= 0 || per_batch <= 0) return kErrDims;
   const int64_t n = (int64_t)batch * per_batch;
-  TSPLAT_CHECK(check_dev(x, n * 4));
-  TSPLAT_CHECK(check_dev(a, n * 4));
-  TSPLAT_CHECK(check_dev(s0, (int64_t)batch * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(x, n * 4));
+  TSPLAT_CHECK(ptrs.check(a, n * 4));
+  TSPLAT_CHECK(ptrs.check(s0, (int64_t)batch * 4));
   if (op == 0) return launched(launch_cfg_combine(x, a, s0, batch, per_batch, stream));
   if (op == 1) return launched(launch_euler_update(x, a, s0, batch, per_batch, stream));
-  TSPLAT_CHECK(check_dev(p, n * 4));
-  TSPLAT_CHECK(check_dev(s1, (int64_t)batch * 4));
+  TSPLAT_CHECK(ptrs.check(p, n * 4));
+  TSPLAT_CHECK(ptrs.check(s1, (int64_t)batch * 4));
   return launched(launch_ab2_update(x, a, p, s0, s1, batch, per_batch, stream));
 }
 
@@ -299,17 +305,18 @@ int tsplat_nf24_gemm_precision_async(const float* x, const int16_t* code01_t,
     return kErrDims;
   if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
     return kErrDims;
-  TSPLAT_CHECK(check_dev(x, ((int64_t)(M - 1) * stride_x + K) * 4));
-  TSPLAT_CHECK(check_dev(code01_t, (int64_t)K * N * 2));
-  TSPLAT_CHECK(check_dev(q2_t, (int64_t)K * N));
-  TSPLAT_CHECK(check_dev(scale, (int64_t)N * 4));
-  TSPLAT_CHECK(check_dev(bias, (int64_t)N * 4));
-  TSPLAT_CHECK(check_dev(out, ((int64_t)(M - 1) * stride_out + output_count) * 4));
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(x, ((int64_t)(M - 1) * stride_x + K) * 4));
+  TSPLAT_CHECK(ptrs.check(code01_t, (int64_t)K * N * 2));
+  TSPLAT_CHECK(ptrs.check(q2_t, (int64_t)K * N));
+  TSPLAT_CHECK(ptrs.check(scale, (int64_t)N * 4));
+  TSPLAT_CHECK(ptrs.check(bias, (int64_t)N * 4));
+  TSPLAT_CHECK(ptrs.check(out, ((int64_t)(M - 1) * stride_out + output_count) * 4));
   if (epilogue == kEpilogueGated) {
     if (!gate) return kErrNull;
     if (rows_per_batch <= 0 || gate_stride < N) return kErrRange;
     const int64_t batches = ((int64_t)M + rows_per_batch - 1) / rows_per_batch;
-    TSPLAT_CHECK(check_dev(gate, ((batches - 1) * gate_stride + N) * 4));
+    TSPLAT_CHECK(ptrs.check(gate, ((batches - 1) * gate_stride + N) * 4));
   }
   GemmParams p{x, code01_t, q2_t, scale, bias, out, M, K, N, output_start, output_count,
                stride_x, stride_out, precision};

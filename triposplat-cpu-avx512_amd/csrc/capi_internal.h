@@ -8,9 +8,25 @@ namespace tsplat {
 
 // Records a failed HIP call for tsplat_last_hip_error(); kOk or kErrLaunch.
 int note(hipError_t e);
-// kOk when [p, p + bytes) lies inside one device (or managed) allocation of
-// the current device; kErrNull / kErrPointer otherwise.
-int check_dev(const void* p, int64_t bytes);
+// The pointer checks of one C-ABI call.  check(p, bytes) is kOk when
+// [p, p + bytes) lies inside one device (or managed) allocation of the
+// current device, kErrNull / kErrPointer otherwise: a wrong pointer becomes a
+// status code instead of a GPU memory fault.  Each runtime query costs about
+// 0.1 us of host time and a call checks 3-11 pointers, so the current device
+// is read once per call, and a range inside an allocation that an earlier
+// check of the same call validated is accepted without a query (torch's
+// caching allocator carves many tensors out of one segment).
+class DeviceRanges {
+ public:
+  int check(const void* p, int64_t bytes);
+
+ private:
+  static constexpr int kMaxRanges = 12;
+  int device_ = -1;
+  int count_ = 0;
+  uintptr_t lo_[kMaxRanges];
+  uintptr_t hi_[kMaxRanges];
+};
 bool aligned16(const void* p);
 // Waits for the null stream (the blocking reference-named entry points).
 int sync_null_stream();
