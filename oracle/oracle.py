@@ -134,16 +134,30 @@ def bf16_split(a):
     return hi, bf16_round((a - hi).astype(np.float32))
 
 
+def nf24_bf16_split_w(code01_t, q2_t, scale):
+    """(wh, wl) of the bf16 modes' weights: w = fp32(p * s), the reference's
+    decode of payload p = q01 * 256 + q2 and row scale s; wh = bf16(w);
+    wl = bf16(fp32(p * s - wh)), the exact product minus wh rounded once to
+    fp32 (the device forms it with one FMA).  p * s is exact in float64
+    (24-bit by 24-bit significands) and so is p * s - wh (|p*s - wh| <=
+    2^-8 |p*s|, on the product's grid)."""
+    p = (np.asarray(code01_t).astype(np.int64) * 256 + np.asarray(q2_t).astype(np.int64))
+    prod = p.astype(np.float64) * np.asarray(scale, np.float32).astype(np.float64)[None, :]
+    wh = bf16_round(prod.astype(np.float32))
+    wl = bf16_round((prod - wh.astype(np.float64)).astype(np.float32))
+    return wh, wl
+
+
 def nf24_gemm_bf16_terms(x, code01_t, q2_t, scale, bias, precision):
     """float64 value of bias + sum_k of the products the bf16 modes form:
-    "bf16": xh*wh; "bf16x3": xh*wh + xh*wl + xl*wh (w = the exact decode).
-    Products of two bf16 values are exact in fp32 and float64, so a device
-    result differs from this only by its fp32 summation order."""
+    "bf16": xh*wh; "bf16x3": xh*wh + xh*wl + xl*wh (x split by bf16_split,
+    w by nf24_bf16_split_w).  Products of two bf16 values are exact in fp32
+    and float64, so a device result differs from this only by its fp32
+    summation order."""
     if precision not in ("bf16", "bf16x3"):
         raise ValueError(precision)
-    w = decode_nf24(code01_t, q2_t, scale)
     xh, xl = bf16_split(x)
-    wh, wl = bf16_split(w)
+    wh, wl = nf24_bf16_split_w(code01_t, q2_t, scale)
     f = lambda a: a.astype(np.float64)  # noqa: E731
     y = f(xh) @ f(wh)
     if precision == "bf16x3":
@@ -153,9 +167,8 @@ def nf24_gemm_bf16_terms(x, code01_t, q2_t, scale, bias, precision):
 
 def nf24_gemm_bf16_abs_terms(x, code01_t, q2_t, scale, bias, precision):
     """|bias| + sum_k |terms| of nf24_gemm_bf16_terms (for order bounds)."""
-    w = decode_nf24(code01_t, q2_t, scale)
     xh, xl = bf16_split(x)
-    wh, wl = bf16_split(w)
+    wh, wl = nf24_bf16_split_w(code01_t, q2_t, scale)
     f = lambda a: np.abs(a.astype(np.float64))  # noqa: E731
     y = f(xh) @ f(wh)
     if precision == "bf16x3":

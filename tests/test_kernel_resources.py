@@ -19,7 +19,12 @@ BUILD = Path(__file__).resolve().parents[1] / "triposplat-cpu-avx512_amd" / "_bu
 
 # (source, mangled-name fragment) -> scratch bytes per lane allowed
 BUDGET = {
-    # fp32 SDPA, key-contiguous k/v without bias (the reference's packed entry)
+    # fp32 SDPA, key-contiguous k/v without bias (the reference's packed
+    # entry): one dword (the wave's first query row) stored before the key
+    # loop and reloaded for the final store, i.e. one scratch store and one
+    # load per lane per workgroup, none inside the loop.  Variants that keep
+    # it in registers (wave index in an SGPR, 32-bit K/V offsets) move a
+    # spill into the key-bias or bf16 kernels instead.
     ("sdpa", "sdpa_kernelILi1ELb0ELi16ELi64ELb0E"): 8,
     # opt-in bf16x3 / bf16 SDPA at 16 waves ([B,H,L,64] k/v): 8 waves spill
     # nothing but run 6 % slower

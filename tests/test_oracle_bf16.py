@@ -56,6 +56,35 @@ def test_bf16_split_invariants(oracle):
     assert np.all(np.abs(lo) <= 2.0 ** -8 * np.abs(hi) * (1 + 2.0 ** -7))
 
 
+def test_nf24_bf16_split_w_exact(oracle):
+    """wh = bf16(fp32(p*s)), wl = bf16(fp32(p*s - wh)) against exact rational
+    arithmetic: the product and the residual are exact in float64 (checked
+    here), so their fp32 roundings are the single roundings the definition
+    names; and the FMA residual is a different split from bf16_split(w)."""
+    from fractions import Fraction
+    r = np.random.default_rng(11)
+    K, N = 64, 48
+    w = (r.standard_normal((N, K)) * 0.02).astype(np.float32)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    wh, wl = oracle.nf24_bf16_split_w(c01, q2, s)
+    assert not np.any(wh.view(np.uint32) & 0xFFFF) and not np.any(wl.view(np.uint32) & 0xFFFF)
+    for k, n in zip(r.integers(0, K, 400), r.integers(0, N, 400)):
+        p = int(c01[k, n]) * 256 + int(q2[k, n])
+        prod = Fraction(p) * Fraction(float(s[n]))
+        assert Fraction(float(prod)) == prod                    # exact in float64
+        assert np.float32(float(prod)) == oracle.decode_nf24(c01, q2, s)[k, n]
+        assert oracle.bf16_round(np.float32(float(prod))) == wh[k, n]
+        res = prod - Fraction(float(wh[k, n]))
+        assert Fraction(float(res)) == res                      # exact in float64
+        assert oracle.bf16_round(np.float32(float(res))) == wl[k, n]
+    wd = oracle.decode_nf24(c01, q2, s).astype(np.float64)
+    prod = (c01.astype(np.float64) * 256 + q2) * s.astype(np.float64)[None, :]
+    assert np.all(np.abs(prod - wh - wl) <= 2.0 ** -16 * np.abs(prod) + 1e-300)
+    h2, l2 = oracle.bf16_split(wd.astype(np.float32))
+    assert np.array_equal(h2, wh)
+    assert 0 < np.count_nonzero(l2 != wl) < l2.size // 4       # distinct, rarely
+
+
 def _exact_bf16_linear(oracle, seed, M, K, N):
     """x exact in bf16; NF24 codes with q2 = 0, |q01| < 128 and a power-of-two
     scale, so every decoded weight has at most 8 significant bits."""

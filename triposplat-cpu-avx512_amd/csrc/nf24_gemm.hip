@@ -21,6 +21,8 @@
 
 #include "nf24_gemm_common.h"
 
+#include <atomic>
+
 #include <type_traits>
 
 namespace tsplat {
@@ -423,19 +425,6 @@ struct Choice {
 constexpr Choice kChoices[] = {
     {256, 256, 1, 16, 126.0}, {256, 192, 1, 12, 125.0}, {128, 128, 3, 4, 111.0}};
 
-int compute_units() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 // Modelled time of configuration i (kChoices) over M x n_count outputs.
 double model_time(int i, int M, int n_count) {
   const int cus = compute_units();
@@ -486,12 +475,14 @@ int round_split_rows(int M, int n_count) {
   return two < 0.97 * one ? (int)m1 : 0;
 }
 
-// Rows past the last multiple of 256 that number at most kTailRows would
-// occupy a whole extra round of 256-row tiles (e.g. M = 16385: 1040 tiles =
-// 4 rounds + 16 one-row tiles, ~270 us at K = 1024); they run as a second
-// launch of 32-row tiles instead (~30 us).  Every MFMA tile shape sums each
-// output in the same order, so the tail rows are bit-identical to what the
-// 256-row tiles would have produced.
+// Rows past the last multiple of 256 that number at most kTailRows, when
+// they would occupy a whole extra round of 256-row tiles (e.g. M = 16385:
+// 1040 tiles = 4 rounds + 16 one-row tiles, ~270 us at K = 1024), run as a
+// second launch of 32-row tiles instead (~30 us).  When they fit in the last
+// round the main launch already has (e.g. M = 12294: 576 + 12 tiles, three
+// rounds either way), they stay in it: the partial tile costs nothing there,
+// while a second launch would add its own time.  Every MFMA tile shape sums
+// each output in the same order, so the tail rows are bit-identical either way.
 constexpr int kTailRows = 32;
 
 GemmParams rows_slice(const GemmParams& p, int first, int count) {
@@ -502,12 +493,30 @@ GemmParams rows_slice(const GemmParams& p, int first, int count) {
   return q;
 }
 
-int tail_rows(int M) {
+int tail_rows(int M, int n_count) {
   const int rem = M % 256;
-  return (M > 256 && rem != 0 && rem <= kTailRows) ? rem : 0;
+  if (M <= 256 || rem == 0 || rem > kTailRows) return 0;
+  const double with_tail = model_time(pick_config(M, n_count), M, n_count);
+  const double without = model_time(pick_config(M - rem, n_count), M - rem, n_count);
+  return with_tail > without ? rem : 0;
 }
 
 }  // namespace
+
+namespace nf24 {
+int compute_units() {
+  static std::atomic<int> cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+}  // namespace nf24
 
 int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
   if (p.precision != kPrecisionFp32 && p.M > 32)
@@ -519,7 +528,7 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
     if (p.M > 8 && p.K <= 256) return launch_cfg<CfgSkinny>(p, stream);
     return launch_nf24_gemv(p, stream);
   }
-  if (const int rem = tail_rows(p.M)) {
+  if (const int rem = tail_rows(p.M, p.n_count)) {
     const int st = launch_nf24_gemm(rows_slice(p, 0, p.M - rem), stream);
     return st != kOk ? st : launch_cfg<CfgTailNarrow>(rows_slice(p, p.M - rem, rem), stream);
   }
@@ -538,7 +547,7 @@ template <int kEpi>
 int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_t stream,
                     const QkvArgs& q = QkvArgs{}, int row0 = 0) {
   if (p.precision != kPrecisionFp32 && p.M > 32) return launch_gemm_bf16(p, kEpi, q, e, row0, stream);
-  if (const int rem = tail_rows(p.M)) {
+  if (const int rem = tail_rows(p.M, p.n_count)) {
     const int st = launch_epi_kind<kEpi>(rows_slice(p, 0, p.M - rem), e, stream, q, row0);
     return st != kOk ? st
                      : launch_cfg<TailCfg<kEpi>, kEpi>(rows_slice(p, p.M - rem, rem), stream, q, e,

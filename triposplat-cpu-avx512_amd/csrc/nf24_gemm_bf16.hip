@@ -7,13 +7,15 @@
 // HBM -- but the products run on v_mfma_f32_32x32x16_bf16 with fp32
 // accumulation:
 //   kPrecisionBf16:   bf16(x) * bf16(w)
-//   kPrecisionBf16x3: xh*wh + xh*wl + xl*wh with xh = bf16(x), xl = bf16(x - xh)
-//                     and likewise wh, wl
+//   kPrecisionBf16x3: xh*wh + xh*wl + xl*wh with xh = bf16(x), xl = bf16(x - xh),
+//                     wh = bf16(w), wl = bf16(fma(p, s, -wh))
 // where bf16() rounds the fp32 value to nearest even (v_cvt_pk_bf16_f32,
-// the rounding torch's float32 -> bfloat16 conversion uses).  x - xh is
-// exact in fp32, so xh + xl holds 16 significant bits of x; the dropped
-// xl*wl term and the rounding of xl leave a product error near 2^-16
-// relative, against 2^-8 for bf16 alone.  Products of two bf16 values are
+// the rounding torch's float32 -> bfloat16 conversion uses), w = fp32(p * s)
+// is the decoded weight of payload p = q01 * 256 + q2 and scale s, and the
+// FMA takes the exact product minus wh, rounded once.  x - xh is exact in
+// fp32, so xh + xl holds 16 significant bits of x (wh + wl likewise of
+// p * s); the dropped xl*wl term and the rounding of xl leave a product
+// error near 2^-16 relative, against 2^-8 for bf16 alone.  Products of two bf16 values are
 // exact in fp32, so the only other difference from a float64 sum of the same
 // terms is the fp32 accumulation order.
 //
@@ -85,6 +87,40 @@ __device__ __forceinline__ void split4(const floatx4& v, bf16x4& hi, bf16x4& lo)
     if constexpr (kTerms == 3) {
       const float ha = __uint_as_float(h[p] << 16), hb = __uint_as_float(h[p] & 0xffff0000u);
       l[p] = __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{a - ha, b - hb}, bf16x2));
+    }
+  }
+  hi = __builtin_bit_cast(bf16x4, uintx2{h[0], h[1]});
+  if constexpr (kTerms == 3) lo = __builtin_bit_cast(bf16x4, uintx2{l[0], l[1]});
+}
+
+// Integer payload (int32)q01 * 256 + q2 of column e of a staged unit row, as
+// fp32 (exact: its magnitude is below 2^24), codes packed as loaded (two
+// int16 codes per word, four int8 codes per word).
+__device__ __forceinline__ float w_payload(const uint32_t (&c)[2], uint32_t q, int e) {
+  const int32_t code = (int32_t)(int16_t)(c[e >> 1] >> (16 * (e & 1)));
+  const int32_t q2 = (int32_t)(int8_t)(q >> (8 * e));
+  return (float)(code * 256 + q2);
+}
+
+// Four weights w = fp32(p * s) of one column -- the reference's decode
+// (scripts/gemm_nf24_i16_avx512.c:26-33) -- split: hi = bf16(w), and with
+// three terms lo = bf16 of fma(p, s, -hi), the exact p * s minus hi rounded
+// once to fp32.  Spelled out so that the result does not depend on whether
+// the compiler contracts w - hi with the product that made w.
+template <int kTerms>
+__device__ __forceinline__ void split_w4(const float (&p)[4], float s, bf16x4& hi, bf16x4& lo) {
+#pragma clang fp contract(off)
+  unsigned h[2], l[2] = {0, 0};
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const float w0 = p[2 * q] * s, w1 = p[2 * q + 1] * s;
+    h[q] = __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{w0, w1}, bf16x2));
+    if constexpr (kTerms == 3) {
+      const float h0 = __uint_as_float(h[q] << 16), h1 = __uint_as_float(h[q] & 0xffff0000u);
+      l[q] = __builtin_bit_cast(unsigned, __builtin_convertvector(
+                                              floatx2{__builtin_fmaf(p[2 * q], s, -h0),
+                                                      __builtin_fmaf(p[2 * q + 1], s, -h1)},
+                                              bf16x2));
     }
   }
   hi = __builtin_bit_cast(bf16x4, uintx2{h[0], h[1]});
@@ -205,15 +241,11 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
     for (int j = 0; j < C::kWIter; ++j) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        floatx4 w;
+        float pw[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int32_t code = (int32_t)(int16_t)(cr[S][j][i][e >> 1] >> (16 * (e & 1)));
-          const int32_t q2 = (int32_t)(int8_t)(qr[S][j][i] >> (8 * e));
-          w[i] = (float)(code * 256 + q2) * w_sc[j][e];
-        }
+        for (int i = 0; i < 4; ++i) pw[i] = w_payload(cr[S][j][i], qr[S][j][i], e);
         bf16x4 hi, lo;
-        split4<kTerms>(w, hi, lo);
+        split_w4<kTerms>(pw, w_sc[j][e], hi, lo);
         const int col = w_col[j] + e;
         const int off = chunk_offset(col, w_k[j] >> 3) + (w_k[j] & 7);
         *reinterpret_cast<bf16x4*>(&ws[buf][0][off]) = hi;
@@ -351,12 +383,18 @@ int launch_gemm_bf16(const GemmParams& p, int epi, const QkvArgs& e, const GemmE
                    (p.n_count % 4 == 0) && (reinterpret_cast<uintptr_t>(p.code01) % 8 == 0) &&
                    (reinterpret_cast<uintptr_t>(p.q2) % 4 == 0);
   if (!vec) return launch_shape<Bf16Small, false>(a, terms, epi, stream);
-  // 256 x 256 tiles where there are rows and columns to fill them; rows past
-  // the last multiple of 256 that number at most 32 run as 128-row tiles
-  // (both shapes sum every output in the same order).
+  // 256 x 256 tiles where there are rows and columns to fill them.  Rows
+  // past the last multiple of 256 that number at most 32 stay in that grid
+  // when their partial tiles fit in its last round (M = 12294, N = 3072:
+  // 588 tiles, three rounds as without them; 286 against 329 us as a second
+  // launch), else they run as 128-row tiles; both shapes sum every output in
+  // the same order.
   if (p.M < 256 || p.n_count < 256) return launch_shape<Bf16Small, true>(a, terms, epi, stream);
   const int rem = p.M % 256;
-  if (rem == 0 || rem > 32) return launch_shape<Bf16Large, true>(a, terms, epi, stream);
+  const int64_t bands = (p.n_count + 255) / 256, cus = compute_units();
+  const int64_t base = (int64_t)(p.M / 256) * bands;
+  if (rem == 0 || rem > 32 || (base + bands + cus - 1) / cus == (base + cus - 1) / cus)
+    return launch_shape<Bf16Large, true>(a, terms, epi, stream);
   const int st = launch_shape<Bf16Large, true>(rows_of(a, 0, p.M - rem), terms, epi, stream);
   return st != kOk ? st : launch_shape<Bf16Small, true>(rows_of(a, p.M - rem, rem), terms, epi, stream);
 }

@@ -135,6 +135,9 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
                          : floatx4{0, 0, 0, 0};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
+          // q' = fp32(q * c1) is split, not the exact product: no contraction
+          // of v - hv with the multiply.
+#pragma clang fp contract(off)
           const float v = x[e] * c1;
           const __bf16 hv = (__bf16)v;
           qh[c][4 * half + e] = hv;
