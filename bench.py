@@ -19,6 +19,8 @@ cpu_baseline: the reference's own AVX-512 kernel (oracle/_ref, compiled from
 the reference sources) on the host cores, on a bounded sample of the same
 workload (all 16 heads, a subset of query rows against all 16384 keys),
 scaled to TFLOP/s.  Falls back to the oracle port if _ref is absent.
+Each timed CPU run follows a device call (alternating order), with all host
+threads and with the reference's published thread counts (SDPA 4, GEMM 8).
 """
 from __future__ import annotations
 
@@ -33,6 +35,16 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "triposplat-cpu-avx512_amd"))
+# Host threads for the CPU baselines, taken before anything starts an OpenMP
+# runtime.  (Binding OpenMP threads with OMP_PROC_BIND=true pins the main
+# thread to one core, after which its affinity mask -- and any thread count
+# read from it -- is a single CPU; the baselines therefore leave binding to
+# the environment and report it.)
+HOST_THREADS = len(os.sched_getaffinity(0))
+
+
+def omp_binding():
+    return {k: os.environ.get(k) for k in ("OMP_PROC_BIND", "OMP_PLACES", "OMP_NUM_THREADS")}
 
 METRIC = "NF24 GEMM + exact SDPA TFLOP/s (% MFMA peak) at L=16384; s/denoise step"
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
@@ -104,7 +116,7 @@ def parity_stats(got, ref, tol_abs=None):
     return out
 
 
-def cpu_baseline_sdpa(q, k, v, budget_s=12.0, gpu_out=None):
+def cpu_baseline_sdpa(q, k, v, budget_s=12.0, gpu_out=None, gpu_fn=None):
     """Time the reference AVX-512 SDPA (or the oracle port) on the host.
 
     The sample is the whole configs[1] call when it fits the budget (it does
@@ -114,13 +126,15 @@ def cpu_baseline_sdpa(q, k, v, budget_s=12.0, gpu_out=None):
     count (4).  With `gpu_out` (the device result, [B, L, H, D]) and the
     reference build present, the sampled rows of the reference's own output
     are also compared with it (`parity_vs_reference`; the GPU tests' bound
-    is 1e-5 * max|v| max-abs)."""
+    is 1e-5 * max|v| max-abs).  With `gpu_fn` (one timed device call, ms)
+    each timed CPU run follows a device call, so both sides see the same
+    host and clock state (`alternating_gpu_ms`)."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as O
 
-    threads = len(os.sched_getaffinity(0))
+    threads = HOST_THREADS
     kind = "reference" if O.ref_available() else "port"
     B, H, L, D = q.shape
 
@@ -135,12 +149,18 @@ def cpu_baseline_sdpa(q, k, v, budget_s=12.0, gpu_out=None):
             O.sdpa_q8t512(qs, k, v)
         return time.perf_counter() - t0
 
+    gpu_ms = []
+
     def measure(nthreads):
         run(256, nthreads)  # warmup: K/V pack workspace, page-in, thread pool
         t1 = run(1024, nthreads)
         rows = L if t1 * L / 1024 * 3 <= budget_s else max(1024, int(budget_s / 3 / t1 * 1024) // 128 * 128)
-        times = sorted(run(rows, nthreads) for _ in range(3))
-        return rows, times[1]
+        times = []
+        for _ in range(3):  # device call, CPU run, alternating
+            if gpu_fn is not None:
+                gpu_ms.append(gpu_fn())
+            times.append(run(rows, nthreads))
+        return rows, sorted(times)[1]
 
     rows, t_med = measure(threads)
     parity = None
@@ -162,6 +182,9 @@ def cpu_baseline_sdpa(q, k, v, budget_s=12.0, gpu_out=None):
         "seconds_per_call": t_med * L / rows,
         "threads4_tflops": flop4 / t4 / 1e12,
         "threads4_seconds_per_call": t4 * L / rows4,
+        "order": "device call then CPU run, three times per thread count (median of the CPU runs)",
+        "alternating_gpu_ms": gpu_ms,
+        "omp": omp_binding(),
         "parity_vs_reference": parity,
     }
 
@@ -270,7 +293,7 @@ def run_sdpa_variants(torch, dev, host, iters=5, ref_parity=False):
 
         if not O.ref_available():
             O = None
-    threads = len(os.sched_getaffinity(0))
+    threads = HOST_THREADS
 
     def ref_per_head():
         return np.concatenate([O.ref_sdpa_q8t512(q_h[:, h:h + 1], k_h[:, h:h + 1], v_h[:, h:h + 1], bias_h[h],
@@ -350,17 +373,36 @@ def run_gemm(torch, dev, iters, ref_parity=False):
             "rel_rmse_vs_fp32": float(d.pow(2).mean().sqrt() / strict.double().pow(2).mean().sqrt()),
             "max_abs_vs_fp32": float(d.abs().max()),
         }
-    parity = None
+    parity = cpu_ref = None
     if ref_parity:
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle as O
 
         if O.ref_available():
-            ref = O.ref_nf24_gemm(x.cpu().numpy(), codes[0].cpu().numpy(), codes[1].cpu().numpy(),
-                                  scales[0].cpu().numpy(), bias.cpu().numpy(),
-                                  threads=len(os.sched_getaffinity(0)))
+            host = [t.cpu().numpy() for t in (x, codes[0], codes[1], scales[0], bias)]
+            threads = HOST_THREADS
+            ref = O.ref_nf24_gemm(*host, threads=threads)
             parity = parity_stats(strict.cpu().numpy(), ref)
             parity["rows"] = f"all {M} rows"
+            # the reference kernel on the host: all cores and the reference's
+            # published GEMM thread count (8); device batch and CPU call
+            # alternate, median of 3 CPU calls after one warmup
+            cpu_ref = {"host_cpu": host_cpu_model(), "omp": omp_binding(),
+                       "order": "device batch then CPU call, three times per thread count"}
+            for tag, nthr in (("", threads), ("threads8_", 8)):
+                O.ref_nf24_gemm(*host, threads=nthr)
+                times, gms = [], []
+                for _ in range(3):
+                    gms.append(time_events(torch, step, iters))
+                    t0 = time.perf_counter()
+                    O.ref_nf24_gemm(*host, threads=nthr)
+                    times.append(time.perf_counter() - t0)
+                t_med = sorted(times)[1]
+                cpu_ref[tag + "threads"] = nthr
+                cpu_ref[tag + "s_per_call"] = t_med
+                cpu_ref[tag + "tflops"] = g_flop / t_med / 1e12
+                cpu_ref[tag + "alternating_gpu_ms"] = gms
+            cpu_ref["speedup_gpu_vs_cpu_threads8"] = cpu_ref["threads8_s_per_call"] / (g_ms * 1e-3)
     return {
         "workload": "configs[0] NF24 Linear X[4096x1024] @ W[1024x3072] + bias, fp32 MFMA accumulate",
         "ms": g_ms,
@@ -370,6 +412,7 @@ def run_gemm(torch, dev, iters, ref_parity=False):
         "traffic": load_traffic("nf24_gemm_config0"),
         "opt_in_bf16": opt_in,
         "parity_vs_reference": parity,
+        "cpu_reference": cpu_ref,
     }
 
 
@@ -622,7 +665,7 @@ def run_flow(torch, dev, steps, with_cpu, validate):
         import oracle as O
         from flow_ref import CpuFlow, combined_rmse
 
-        threads = len(os.sched_getaffinity(0))
+        threads = HOST_THREADS
         backend = "reference" if O.ref_available() else "oracle"
         params = model.host()
         cpu = CpuFlow(params, cfg, backend=backend, threads=threads)
@@ -854,7 +897,16 @@ def main():
     gemm["l16384"] = run_gemm_l16384(torch, dev)
     refshapes = run_reference_shapes(torch, dev, not args.no_cpu_baseline)
     flow = None if args.no_flow else run_flow(torch, dev, 3, not args.no_cpu_baseline, args.validate_flow)
-    cpu = None if args.no_cpu_baseline else cpu_baseline_sdpa(*host, gpu_out=sdpa_out)
+    cpu = None
+    if not args.no_cpu_baseline:
+        from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
+
+        qd, kd, vd = (torch.from_numpy(a).to(dev) for a in host)
+        od = torch.empty((B, L, H, D), dtype=torch.float32, device=dev)
+        gpu_fn = lambda: time_events(  # noqa: E731
+            torch, lambda: native_sdpa_f32_ex(qd, kd, vd, out=od, out_layout="blhd"), 1)
+        cpu = cpu_baseline_sdpa(*host, gpu_out=sdpa_out, gpu_fn=gpu_fn)
+        del qd, kd, vd, od
 
     line = {
         "metric": METRIC,
