@@ -41,6 +41,8 @@ sys.path.insert(0, str(ROOT / "triposplat-cpu-avx512_amd"))
 # read from it -- is a single CPU; the baselines therefore leave binding to
 # the environment and report it.)
 HOST_THREADS = len(os.sched_getaffinity(0))
+# Input seeds of every workload (configs/workloads.json describes the inputs).
+SEEDS = json.loads((ROOT / "configs" / "workloads.json").read_text())["seeds"]
 
 
 def omp_binding():
@@ -193,9 +195,9 @@ def sdpa_inputs(torch, dev):
     import numpy as np
 
     B, H, L, D = 1, 16, 16384, 64
-    q_h = rope_rmsnorm_host(np.random.default_rng(10).standard_normal((B, H, L, D), dtype=np.float32))
-    k_h = rope_rmsnorm_host(np.random.default_rng(11).standard_normal((B, H, L, D), dtype=np.float32))
-    v_h = np.random.default_rng(12).standard_normal((B, H, L, D), dtype=np.float32)
+    q_h = rope_rmsnorm_host(np.random.default_rng(SEEDS["c2_q"]).standard_normal((B, H, L, D), dtype=np.float32))
+    k_h = rope_rmsnorm_host(np.random.default_rng(SEEDS["c2_k"]).standard_normal((B, H, L, D), dtype=np.float32))
+    v_h = np.random.default_rng(SEEDS["c2_v"]).standard_normal((B, H, L, D), dtype=np.float32)
     return q_h, k_h, v_h
 
 
@@ -279,13 +281,13 @@ def run_sdpa_variants(torch, dev, host, iters=5, ref_parity=False):
     k = torch.from_numpy(k_h).to(dev)
     v = torch.from_numpy(v_h).to(dev)
     out = torch.empty((B, L, H, D), dtype=torch.float32, device=dev)
-    bias_h = np.random.default_rng(13).uniform(-2.0, 0.0, (H, L)).astype(np.float32)
+    bias_h = np.random.default_rng(SEEDS["c3_key_bias"]).uniform(-2.0, 0.0, (H, L)).astype(np.float32)
     bias = torch.from_numpy(bias_h).to(dev)
     shared = torch.zeros(L, dtype=torch.float32, device=dev)
     shared[4096] = math.log(2048.0)
     Lc = 2048
-    kc = torch.from_numpy(np.random.default_rng(14).standard_normal((B, H, Lc, D), dtype=np.float32)).to(dev)
-    vc = torch.from_numpy(np.random.default_rng(15).standard_normal((B, H, Lc, D), dtype=np.float32)).to(dev)
+    kc = torch.from_numpy(np.random.default_rng(SEEDS["c3_cross_k"]).standard_normal((B, H, Lc, D), dtype=np.float32)).to(dev)
+    vc = torch.from_numpy(np.random.default_rng(SEEDS["c3_cross_v"]).standard_normal((B, H, Lc, D), dtype=np.float32)).to(dev)
     O = None
     if ref_parity:
         sys.path.insert(0, str(ROOT / "oracle"))
@@ -333,10 +335,10 @@ def run_gemm(torch, dev, iters, ref_parity=False):
     from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
 
     M, K, N = 4096, 1024, 3072
-    x = torch.from_numpy(np.random.default_rng(0).standard_normal((M, K), dtype=np.float32)).to(dev)
-    w = torch.from_numpy((np.random.default_rng(1).standard_normal((N, K), dtype=np.float32)
+    x = torch.from_numpy(np.random.default_rng(SEEDS["c1_x"]).standard_normal((M, K), dtype=np.float32)).to(dev)
+    w = torch.from_numpy((np.random.default_rng(SEEDS["c1_w"]).standard_normal((N, K), dtype=np.float32)
                           * np.float32(0.02)).astype(np.float32)).to(dev)
-    bias = torch.from_numpy((np.random.default_rng(2).standard_normal(N, dtype=np.float32)
+    bias = torch.from_numpy((np.random.default_rng(SEEDS["c1_bias"]).standard_normal(N, dtype=np.float32)
                              * np.float32(0.01)).astype(np.float32)).to(dev)
     codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
     gout = torch.empty((M, N), dtype=torch.float32, device=dev)
@@ -456,8 +458,8 @@ def run_gemm_l16384(torch, dev, iters=8):
     res = {}
     fns, meta = {}, {}
     for i, (name, K, N) in enumerate(GEMM_L16384):
-        x = torch.from_numpy(np.random.default_rng(40 + i).standard_normal((M, K), dtype=np.float32)).to(dev)
-        c01, q2, sc, b = packed_linear(torch, dev, K, N, 50 + 2 * i)
+        x = torch.from_numpy(np.random.default_rng(SEEDS["l16384_gemm_x_base"] + i).standard_normal((M, K), dtype=np.float32)).to(dev)
+        c01, q2, sc, b = packed_linear(torch, dev, K, N, SEEDS["l16384_gemm_w_base"] + 2 * i)
         out = torch.empty((M, N), dtype=torch.float32, device=dev)
         fns[name] = (lambda x=x, c01=c01, q2=q2, sc=sc, b=b, out=out: nf24_linear(x, c01, q2, sc, b, out=out))
         meta[name] = (K, N)
@@ -512,9 +514,9 @@ def run_reference_shapes(torch, dev, with_cpu, iters=5):
     for name, Lq, Lk, logm in (("sdpa_L12294_dense", 12294, 12294, False),
                                ("sdpa_L8194_keybias_log4101", 8194, 8194, True),
                                ("sdpa_selected_8193x12294", 8193, 12294, False)):
-        q_h = rope_rmsnorm_host(np.random.default_rng(30).standard_normal((1, H, Lq, D), dtype=np.float32))
-        k_h = rope_rmsnorm_host(np.random.default_rng(31).standard_normal((1, H, Lk, D), dtype=np.float32))
-        v_h = np.random.default_rng(32).standard_normal((1, H, Lk, D), dtype=np.float32)
+        q_h = rope_rmsnorm_host(np.random.default_rng(SEEDS["refshapes_q"]).standard_normal((1, H, Lq, D), dtype=np.float32))
+        k_h = rope_rmsnorm_host(np.random.default_rng(SEEDS["refshapes_k"]).standard_normal((1, H, Lk, D), dtype=np.float32))
+        v_h = np.random.default_rng(SEEDS["refshapes_v"]).standard_normal((1, H, Lk, D), dtype=np.float32)
         bias_h = None
         if logm:
             bias_h = np.zeros(Lk, np.float32)
@@ -551,9 +553,9 @@ def run_reference_shapes(torch, dev, with_cpu, iters=5):
     M = 12294
     for i, (tag, K, N) in enumerate((("qkv", 1024, 3072), ("fc1", 1024, 4096), ("fc2", 4096, 1024), ("out", 1024, 1024))):
         name = f"gemm_{M}x{K}x{N}_{tag}"
-        x_h = np.random.default_rng(60 + i).standard_normal((M, K), dtype=np.float32)
+        x_h = np.random.default_rng(SEEDS["refshapes_gemm_x_base"] + i).standard_normal((M, K), dtype=np.float32)
         x = torch.from_numpy(x_h).to(dev)
-        c01, q2, sc, b = packed_linear(torch, dev, K, N, 70 + 2 * i)
+        c01, q2, sc, b = packed_linear(torch, dev, K, N, SEEDS["refshapes_gemm_w_base"] + 2 * i)
         out = torch.empty((M, N), dtype=torch.float32, device=dev)
         fn = lambda: nf24_linear(x, c01, q2, sc, b, out=out)
         ms = time_interleaved(torch, {"x": fn}, iters)["x"]
@@ -584,8 +586,8 @@ def run_reference_shapes(torch, dev, with_cpu, iters=5):
 def flow_inputs(cfg):
     import numpy as np
 
-    z = np.random.default_rng(20).standard_normal((cfg.latent_tokens, cfg.hidden), dtype=np.float32)
-    c = np.random.default_rng(21).standard_normal((cfg.cond_tokens, cfg.hidden), dtype=np.float32)
+    z = np.random.default_rng(SEEDS["flow_latent"]).standard_normal((cfg.latent_tokens, cfg.hidden), dtype=np.float32)
+    c = np.random.default_rng(SEEDS["flow_condition"]).standard_normal((cfg.cond_tokens, cfg.hidden), dtype=np.float32)
     return z, c
 
 
@@ -773,7 +775,7 @@ def run_gemm_skinny(torch, dev, replays=5):
     counted) and the replays are timed with HIP events."""
     from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
 
-    g = torch.Generator(device=dev).manual_seed(3)
+    g = torch.Generator(device=dev).manual_seed(SEEDS["skinny_torch"])
     rows = []
     stream = torch.cuda.Stream(device=dev)
     for K, N in ((1024, 3072), (1024, 6144), (4096, 1024)):
