@@ -250,10 +250,12 @@ def test_pointer_checks_within_one_allocation(oracle, cuda, hiplib):
 @pytest.mark.parametrize("M,K,N", [(16385, 1024, 1024), (8194, 1024, 3072)])
 def test_gemm_tail_rows(oracle, cuda, hiplib, M, K, N):
     """M = 256 k + r with r <= 32 (e.g. the compressed negative branch, L + 1
-    tokens) runs the r tail rows as a separate 32-row-tile launch.  Rows of
-    the 256-row part equal a GEMM over exactly those rows, the tail rows equal
+    tokens): 16385 x 1024 runs the tail row as a separate 32-row-tile launch
+    (in the 256-row grid it would add a round), 8194 x 3072 keeps its two tail
+    rows in the grid (their tiles fit the last round).  Either way rows of the
+    256-row part equal a GEMM over exactly those rows and the tail rows equal
     the same rows computed inside a 256-row tile (a larger M with no tail),
-    all bit for bit; sampled rows and the tail against the oracle."""
+    bit for bit; sampled rows and the tail against the oracle."""
     import torch
 
     print(f"gemm tail rows M={M} K={K} N={N}", flush=True)

@@ -69,7 +69,7 @@ def _check_terms(oracle, x, c01, q2, s, b, got, precision):
     (64, 256, 512),      # 128 x 128 tiles
     (520, 96, 200),      # K not a multiple of 32, N below one 256-column tile
     (100, 33, 50),       # K, N not multiples of 4: the scalar-load kernel
-    (544, 256, 512),     # 512 + 32 tail rows as a 128-row launch
+    (544, 256, 512),     # 512 + 32 tail rows, kept in the 256-row grid (no extra round)
 ])
 def test_bf16_gemm_matches_oracle(oracle, cuda, hiplib, precision, M, K, N):
     import torch
@@ -105,20 +105,29 @@ def test_bf16_few_rows_run_strict(oracle, cuda, hiplib):
 
 
 @pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
-def test_bf16_tail_rows_bitwise(oracle, cuda, hiplib, precision):
+@pytest.mark.parametrize("M,K,N", [
+    (528, 256, 512),     # 16 tail rows whose partial tiles fit the grid's only round: one launch
+    (16400, 64, 1024),   # 256 full tiles = one round on 256 CUs; the tail would add one: 128-row launch
+])
+def test_bf16_tail_rows_bitwise(oracle, cuda, hiplib, precision, M, K, N):
+    """Rows past a multiple of 256 give the same bits whether they stay in the
+    256-row grid or run as a separate 128-row launch, and equal the same rows
+    computed inside a larger grid; 128-row tiles equal 256-row tiles."""
     import torch
 
-    M, K, N = 528, 256, 512                       # 512 rows of 256-row tiles + 16 tail rows
-    x, w, b = seeded_linear(21, 768, K, N, w_scale=0.02)
+    print(f"bf16 tail rows {precision} M={M} K={K} N={N}", flush=True)
+    r = M % 256
+    x, w, b = seeded_linear(21 + M, M - r + 256, K, N, w_scale=0.02)
     c01, q2, s = oracle.quantize_nf24_i16(w)
     got = _run(torch, hiplib, cuda, x[:M], c01, q2, s, b, precision)
-    head = _run(torch, hiplib, cuda, x[:512], c01, q2, s, b, precision)
+    head = _run(torch, hiplib, cuda, x[:M - r], c01, q2, s, b, precision)
     full = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision)
     small = _run(torch, hiplib, cuda, x[:128], c01, q2, s, b[:N], precision)   # 128-row tiles
-    assert np.array_equal(got[:512].view(np.uint32), head.view(np.uint32))
-    assert np.array_equal(got[512:].view(np.uint32), full[512:M].view(np.uint32))
+    assert np.array_equal(got[:M - r].view(np.uint32), head.view(np.uint32))
+    assert np.array_equal(got[M - r:].view(np.uint32), full[M - r:M].view(np.uint32))
     assert np.array_equal(small.view(np.uint32), full[:128].view(np.uint32))
-    _check_terms(oracle, x[:M], c01, q2, s, b, got, precision)
+    rows = np.concatenate([np.arange(0, 256), np.arange(M - r - 64, M)])
+    _check_terms(oracle, x[rows], c01, q2, s, b, got[rows], precision)
 
 
 @pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
