@@ -66,7 +66,7 @@ SHAPES = [(25, 96, 64), (40, 96, 64), (10, 96, 64), (3, 96, 5), (1, 1024, 3072),
           (4, 2048, 640), (16, 1024, 3072), (32, 512, 384), (5, 4096, 1024), (12, 1000, 130),
           (3, 1000, 512), (7, 70, 1032), (1, 8200, 1024), (6, 4096, 8), (2, 1024, 6144),
           # 9-16 rows on the wide kernel (two LDS reduction passes), partial slab
-          (9, 1024, 520), (13, 2048, 1024),
+          (9, 1024, 520), (13, 2048, 1032),
           # more K splits than the staged merge holds: the one-thread-per-output merge
           (1, 40000, 96),
           # the MFMA few-row form (4..16 rows, >= 192 slabs of 16 columns; 32-column slabs
@@ -74,7 +74,12 @@ SHAPES = [(25, 96, 64), (40, 96, 64), (10, 96, 64), (3, 96, 5), (1, 1024, 3072),
           # partial last chunk and a partial last wave), a K only two waves reach; 3 rows and
           # 190 slabs stay on the split kernel
           (6, 1024, 3072), (8, 1000, 3072), (11, 2048, 6144), (16, 40, 3072), (13, 4100, 3104),
-          (4, 1024, 6144), (4, 96, 3072), (3, 1024, 3072), (16, 1024, 3040)]
+          (4, 1024, 6144), (4, 96, 3072), (3, 1024, 3072), (16, 1024, 3040),
+          # ... with K split across workgroups when the slabs alone are fewer than 192
+          # (N = 1024: four splits of 1024 rows; ragged K: a partial last split and chunk;
+          # splits that rounding to whole chunks leaves empty are dropped)
+          (16, 4096, 1024), (8, 4096, 1024), (5, 4096, 1024), (13, 2048, 1024), (10, 4100, 1024),
+          (4, 1000, 1024), (4, 2048, 640)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
@@ -103,13 +108,14 @@ def test_gemm_reference_smoke_tolerance(oracle, cuda, hiplib):
         torch.testing.assert_close(torch.from_numpy(got), ref, rtol=2e-5, atol=2e-5)
 
 
-def test_few_row_mfma_range_and_strides(oracle, cuda, hiplib):
+@pytest.mark.parametrize("K,N,start,count", [(1024, 3200, 64, 3072),   # one workgroup per slab
+                                             (2048, 1088, 16, 1024)])   # K split across workgroups
+def test_few_row_mfma_range_and_strides(oracle, cuda, hiplib, K, N, start, count):
     """The MFMA few-row form on an output range with row strides (x padded,
     out wider than the range), equal to the same columns of the full call."""
     import torch
 
-    M, K, N = 12, 1024, 3200
-    start, count = 64, 3072
+    M = 12
     x, w, b = seeded_linear(71, M, K, N)
     c01, q2, s = oracle.quantize_nf24_i16(w)
     got = _run_async(torch, hiplib, cuda, x, c01, q2, s, b, start, count, stride_x=K + 12,

@@ -22,6 +22,8 @@
 #include "tsplat_common.h"
 #include "tsplat_launch.h"
 
+#include <algorithm>
+
 namespace tsplat {
 namespace {
 
@@ -309,7 +311,11 @@ __global__ __launch_bounds__(kWideWaves * 64) void nf24_gemv_wide_kernel(GemvArg
 // ds_read_b128.  The loads of kPass chunks are issued before any is used.
 // (Rows a wave does not own are multiplied by x = 0.)
 // The wave sums are added in wave order through LDS.  Rows of x past M read
-// row M - 1; their sums are never stored.
+// row M - 1; their sums are never stored.  With a.splits > 1 the K range is
+// also split across workgroups (workgroup (split, slab) runs waves split *
+// kWaves .. of a.k_per_split rows each) and each writes its sums to
+// a.partial[split][M][n_count] for nf24_gemv_merge_kernel, which adds the
+// bias and the splits in split order.
 constexpr int kMfmaRows = 32;            // K rows per chunk
 constexpr int kMfmaS = kMfmaRows + 4;    // LDS row stride in floats
 
@@ -327,10 +333,14 @@ __global__ __launch_bounds__(kWaves * 64) void nf24_gemv_mfma_kernel(GemvArgs a)
   // Neighbouring slabs share cache lines (a 32-column slab is half a 128-byte
   // line of code01 and a quarter of one of q2): each XCD takes a contiguous
   // run of slabs so that a line is fetched into one L2, not up to four.
-  const int c0 = xcd_tile_index(blockIdx.x, gridDim.x) * kCols;  // first local column of the slab
+  // Tiles are split-major, so an XCD's run holds neighbouring slabs of one split.
+  const int slabs = gridDim.x / a.splits;
+  const int tile = xcd_tile_index(blockIdx.x, gridDim.x);
+  const int split = tile / slabs;
+  const int c0 = (tile % slabs) * kCols;             // first local column of the slab
   const int cg = lane % kLanesPerRow, lr = lane / kLanesPerRow;
   const int64_t ncol = a.n_start + c0 + 8 * cg;      // this lane's first column
-  const int kw0 = wave * a.k_per_split;              // k_per_split: rows per wave
+  const int kw0 = (split * kWaves + wave) * a.k_per_split;  // k_per_split: rows per wave
   const int kw1 = min(a.K, kw0 + a.k_per_split);
   const int xm = min(lane >> 2, a.M - 1);            // x row this lane stages
   const int xk = 8 * (lane & 3);                     // its 8 k within a chunk
@@ -430,7 +440,11 @@ __global__ __launch_bounds__(kWaves * 64) void nf24_gemv_mfma_kernel(GemvArgs a)
     for (int w = 1; w < kWaves; ++w) v += red[w * kBlocks * 256 + i];
     const int b = i / 256, l = (i / 4) % 64, r = i % 4;
     const int row = 4 * (l >> 4) + r, col = c0 + 16 * b + (l & 15);
-    if (row < a.M) a.out[(int64_t)row * a.stride_out + col] = a.bias[a.n_start + col] + v;
+    if (row >= a.M) continue;
+    if (a.splits == 1)
+      a.out[(int64_t)row * a.stride_out + col] = a.bias[a.n_start + col] + v;
+    else
+      a.partial[((int64_t)split * a.M + row) * a.n_count + col] = v;
   }
 }
 
@@ -533,31 +547,51 @@ namespace {
 constexpr int kMfmaWaves = 8;
 constexpr int kMfmaMinRows = 4;
 constexpr int kMfmaMinWorkgroups = 192;
+// Fewer slabs than that (N = 1024): the K range is split too, so that about
+// kMfmaSplitTarget workgroups stream the weights, each wave keeping at least
+// one 32-row chunk; the partial sums (splits * M * N * 8 bytes moved, 0.5 MB
+// at K = 4096, N = 1024, M = 16, four splits) are a few percent of the
+// weight bytes, and nf24_gemv_merge_kernel adds them in split order.
+constexpr int kMfmaSplitTarget = 256;
 
 template <int kCols>
-int launch_mfma_form(const GemmParams& p, hipStream_t stream) {
-  const int per_wave =
-      ((p.K + kMfmaWaves * kMfmaRows - 1) / (kMfmaWaves * kMfmaRows)) * kMfmaRows;
+int launch_mfma_form(const GemmParams& p, int splits, hipStream_t stream) {
+  const int waves = kMfmaWaves * splits;
+  const int per_wave = ((p.K + waves * kMfmaRows - 1) / (waves * kMfmaRows)) * kMfmaRows;
+  // Splits left with no rows after the rounding to whole chunks are dropped.
+  splits = (p.K + kMfmaWaves * per_wave - 1) / (kMfmaWaves * per_wave);
   GemvArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out, nullptr, p.M, p.K, p.N,
-             p.n_start, p.n_count, p.stride_x, p.stride_out, per_wave, 1};
+             p.n_start, p.n_count, p.stride_x, p.stride_out, per_wave, splits};
+  if (splits > 1) {
+    a.partial = static_cast<float*>(
+        stream_workspace(stream, (size_t)splits * p.M * p.n_count * 4, kSlotGemvPartial));
+    if (a.partial == nullptr) return kErrWorkspace;
+  }
   hipLaunchKernelGGL((nf24_gemv_mfma_kernel<kCols, kMfmaWaves, 4>),
-                     dim3((unsigned)(p.n_count / kCols)), dim3(kMfmaWaves * 64), 0, stream, a);
-  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+                     dim3((unsigned)(p.n_count / kCols * splits)), dim3(kMfmaWaves * 64), 0, stream, a);
+  if (hipGetLastError() != hipSuccess) return kErrLaunch;
+  if (splits == 1) return kOk;
+  return launch_merge(a.partial, p.bias, p.out, p.M, p.n_count, p.n_start, p.stride_out, splits, stream);
 }
 }  // namespace
 
 int launch_nf24_gemv(const GemmParams& p, hipStream_t stream) {
   if (p.M < 1 || p.M > 32) return kErrDims;
-  const bool mfma_ok = p.M >= kMfmaMinRows && p.M <= 16 && ((p.N | p.n_start | p.n_count) % 16) == 0 &&
-                       p.n_count / 16 >= kMfmaMinWorkgroups && (p.stride_x & 3) == 0 &&
-                       (reinterpret_cast<uintptr_t>(p.x) & 15) == 0 &&
-                       (reinterpret_cast<uintptr_t>(p.code01) & 15) == 0 &&
-                       (reinterpret_cast<uintptr_t>(p.q2) & 15) == 0 &&
-                       (reinterpret_cast<uintptr_t>(p.scale) & 15) == 0;
-  if (mfma_ok) {
-    if (((p.N | p.n_start | p.n_count) % 32) == 0 && p.n_count / 32 >= kMfmaMinWorkgroups)
-      return launch_mfma_form<32>(p, stream);
-    return launch_mfma_form<16>(p, stream);
+  const bool mfma_shape = p.M >= kMfmaMinRows && p.M <= 16 && ((p.N | p.n_start | p.n_count) % 16) == 0 &&
+                          (p.stride_x & 3) == 0 && (reinterpret_cast<uintptr_t>(p.x) & 15) == 0 &&
+                          (reinterpret_cast<uintptr_t>(p.code01) & 15) == 0 &&
+                          (reinterpret_cast<uintptr_t>(p.q2) & 15) == 0 &&
+                          (reinterpret_cast<uintptr_t>(p.scale) & 15) == 0;
+  if (mfma_shape) {
+    const int slabs16 = p.n_count / 16;
+    if (slabs16 >= kMfmaMinWorkgroups) {
+      if (((p.N | p.n_start | p.n_count) % 32) == 0 && p.n_count / 32 >= kMfmaMinWorkgroups)
+        return launch_mfma_form<32>(p, 1, stream);
+      return launch_mfma_form<16>(p, 1, stream);
+    }
+    const int splits = std::min((kMfmaSplitTarget + slabs16 - 1) / slabs16, p.K / (kMfmaWaves * kMfmaRows));
+    if (splits >= 2 && splits <= kMergeMaxSplits && slabs16 * splits >= kMfmaMinWorkgroups)
+      return launch_mfma_form<16>(p, splits, stream);
   }
   const bool wide = p.M <= 16 && ((p.N | p.n_start | p.n_count) & 7) == 0 &&
                     (reinterpret_cast<uintptr_t>(p.code01) & 15) == 0 &&
