@@ -24,12 +24,17 @@ def _replays_match(torch, cuda, g, out, expected, eager_between):
         torch.cuda.synchronize(cuda)
 
 
-def test_graph_few_row_gemm(cuda):
+@pytest.mark.parametrize("M,K,N", [(2, 1024, 3072),    # the wide few-row kernel, K split
+                                   (12, 4096, 1024)])  # the MFMA few-row form, K split
+def test_graph_few_row_gemm(cuda, M, K, N):
+    """A few-row GEMM that splits K captures into a graph once its stream has
+    a workspace (a capture cannot allocate: before that it fails with -5),
+    and every replay equals the eager result bit for bit."""
     import torch
     from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
 
+    print(f"graph few-row gemm M={M} K={K} N={N}", flush=True)
     g0 = torch.Generator(device=cuda).manual_seed(3)
-    M, K, N = 2, 1024, 3072                          # few-row kernel with a K split
     x = torch.randn((M, K), generator=g0, device=cuda)
     w = torch.randn((N, K), generator=g0, device=cuda) * 0.02
     b = torch.randn((N,), generator=g0, device=cuda) * 0.01
