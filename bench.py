@@ -81,6 +81,20 @@ def host_cpu_model():
     return None
 
 
+def warm_up(torch, fn, seconds=0.05):
+    """Call fn until `seconds` of device work have run: after the host-side
+    reference runs the GPU sits idle and its clock ramps up again over the
+    first milliseconds, which a short call would otherwise be timed in."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < 2 or time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+        if n % 4 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def time_events(torch, fn, iters):
     """Average device duration of fn() (ms) from events on the current stream."""
     start = torch.cuda.Event(enable_timing=True)
@@ -249,9 +263,7 @@ def run_sdpa_opt_in(torch, dev, host, fp32_ms, iters=5):
         def step(p=precision):
             native_sdpa_f32_ex(q, k, v, out=out, precision=p)
 
-        for _ in range(3):
-            step()
-        torch.cuda.synchronize()
+        warm_up(torch, step)
         ms = sorted(time_events(torch, step, iters) for _ in range(3))[1]
         d = out.double() - strict.double()
         res[precision] = {
@@ -313,8 +325,7 @@ def run_sdpa_variants(torch, dev, host, iters=5, ref_parity=False):
          lambda: O.ref_sdpa_q8t512(q_h, kc.cpu().numpy(), vc.cpu().numpy(), None, threads),
          float(vc.abs().max())),
     ):
-        fn()
-        torch.cuda.synchronize()
+        warm_up(torch, fn)
         ms = sorted(time_events(torch, fn, iters) for _ in range(3))[1]
         tf = flop / (ms * 1e-3) / 1e12
         res[name] = {"ms": ms, "tflops": tf, "frac_fp32_mfma_peak": tf / PEAK_FP32_MFMA}
@@ -421,10 +432,7 @@ def run_gemm(torch, dev, iters, ref_parity=False):
 def time_interleaved(torch, fns, iters, rounds=5):
     """Median per-call device time (ms) of each callable, timed in
     interleaved rounds (clocks drift between rounds on these boxes)."""
-    for _ in range(3):
-        for f in fns.values():
-            f()
-    torch.cuda.synchronize()
+    warm_up(torch, lambda: [f() for f in fns.values()])
     ts = {k: [] for k in fns}
     for _ in range(rounds):
         for k, f in fns.items():
