@@ -95,9 +95,9 @@ def test_native_sdpa_f32_symbols(oracle, cuda, hiplib, symbol, B, H, Lq, Lk, bsp
 
 
 def test_blocking_symbols_direct_ctypes(oracle, cuda):
-    """The INTEGRATION.md binding: an unmodified reference ctypes binding
-    (argtypes of scripts/native_sdpa_ctypes.py:18-19) on the library file,
-    device pointers, the reference's `threads` argument."""
+    """The binding a reference user writes: an unmodified reference ctypes
+    binding (argtypes of scripts/native_sdpa_ctypes.py:18-19) on the library
+    file, device pointers, the reference's `threads` argument."""
     import torch
     from tsplat._lib import DEFAULT_LIBRARY
 
