@@ -503,20 +503,27 @@ int tail_rows(int M, int n_count) {
 
 }  // namespace
 
-namespace nf24 {
 int compute_units() {
   static std::atomic<int> cached[64] = {};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  // A failed query falls back to MI355X's 256 CUs (the count only shapes the
+  // launch plan) and leaves no error behind for the caller's next check.
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (dev < 0 || dev >= 64) return 256;
   int n = cached[dev].load(std::memory_order_relaxed);
   if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
       n = 256;
+    }
+    if (n <= 0) n = 256;
     cached[dev].store(n, std::memory_order_relaxed);
   }
   return n;
 }
-}  // namespace nf24
 
 int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
   if (p.precision != kPrecisionFp32 && p.M > 32)

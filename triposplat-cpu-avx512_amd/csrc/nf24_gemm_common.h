@@ -238,9 +238,6 @@ __device__ __forceinline__ void store_result(const GemmArgs& a, floatx16 (&acc)[
     }
 }
 
-// Compute units of the current device (cached per device).
-int compute_units();
-
 // bf16-MFMA GEMM (nf24_gemm_bf16.hip) for p.precision kPrecisionBf16 /
 // kPrecisionBf16x3 and M > 32: epilogue kind epi (kEpi* / kEpilogue*), QKV
 // operands e, gate operands ep, token index of row 0 row0.

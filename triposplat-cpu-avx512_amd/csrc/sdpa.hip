@@ -272,7 +272,7 @@ int launch_shape(const SdpaParams& p, hipStream_t stream, int cus) {
 // softmax (kSplit).
 template <int kLayout, bool kBias>
 int launch_sized(const SdpaParams& p, hipStream_t stream) {
-  const int cus = device_cus();
+  const int cus = compute_units();
   const int64_t wide_tiles = (int64_t)p.B * p.H * ((p.Lq + 511) / 512);
   if (wide_tiles < cus) return launch_shape<kLayout, kBias, 4, 64, false>(p, stream, 0);
   return launch_shape<kLayout, kBias, 16, 64, kBias>(p, stream, cus);

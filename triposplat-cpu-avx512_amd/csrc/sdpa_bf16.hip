@@ -338,7 +338,7 @@ int launch_shape(const SdpaParams& p, hipStream_t stream, int cus) {
 // configs[1]) and none at 8 (3.5 ms).
 template <int kLayout, bool kBias, int kTerms>
 int launch_sized(const SdpaParams& p, hipStream_t stream) {
-  const int cus = device_cus();
+  const int cus = compute_units();
   const int64_t wide_tiles = (int64_t)p.B * p.H * ((p.Lq + 511) / 512);
   if (wide_tiles < cus) return launch_shape<kLayout, kBias, kTerms, 4>(p, stream, 0);
   constexpr int kWide = (kLayout == 1 && kTerms == 3) ? 8 : 16;

@@ -283,13 +283,6 @@ int launch_tiles(SdpaArgs a, const SdpaParams& p, int kBQ, int kBKV, int cus, hi
   return kOk;
 }
 
-inline int device_cus() {
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess)
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  return cus;
-}
-
 }  // namespace
 }  // namespace sdpa
 }  // namespace tsplat

@@ -40,6 +40,11 @@ __device__ __forceinline__ float bf16_roundtrip(float x) {
   return __uint_as_float(u & 0xffff0000u);
 }
 
+// Compute units of the current device, queried once per device (256 on
+// MI355X, also the fallback when the query fails; the count only shapes
+// launch plans).  Defined in nf24_gemm.hip.
+int compute_units();
+
 // Workgroup i of a launch is placed on XCD i % 8.  Renumber so that each XCD
 // receives one contiguous run of tile indices (neighbouring tiles share L2).
 __device__ __forceinline__ int xcd_tile_index(int id, int count) {
