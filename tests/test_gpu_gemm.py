@@ -61,6 +61,8 @@ def _check(oracle, x, c01, q2, s, b, got, start=0):
 SHAPES = [(25, 96, 64), (40, 96, 64), (10, 96, 64), (3, 96, 5), (1, 1024, 3072), (2, 1024, 256),
           (8, 4096, 64), (16, 64, 1024), (33, 130, 48), (129, 257, 200), (200, 64, 129),
           (7, 3, 17), (300, 1024, 96),
+          # vector (buffer-load) path with a partial last K step: K % 4 == 0, K % 16 != 0
+          (70, 100, 96), (300, 1000, 384), (260, 36, 200),
           # few-row (HBM-bound) kernels: every row-count template, split and unsplit K,
           # ragged last K split, narrow and partial 512-column slabs
           (4, 2048, 640), (16, 1024, 3072), (32, 512, 384), (5, 4096, 1024), (12, 1000, 130),
@@ -125,11 +127,12 @@ def test_few_row_mfma_range_and_strides(oracle, cuda, hiplib, K, N, start, count
     assert np.array_equal(got, full[:, start:start + count])
 
 
+@pytest.mark.parametrize("K", [96, 100])
 @pytest.mark.parametrize("start,count", [(0, 16), (16, 32), (48, 80), (5, 7), (100, 28)])
-def test_gemm_range_and_strides(oracle, cuda, hiplib, start, count):
+def test_gemm_range_and_strides(oracle, cuda, hiplib, start, count, K):
     import torch
 
-    M, K, N = 37, 96, 128
+    M, N = 37, 128
     x, w, b = seeded_linear(7, M, K, N)
     c01, q2, s = oracle.quantize_nf24_i16(w)
     got = _run_async(torch, hiplib, cuda, x, c01, q2, s, b, start, count, stride_x=K + 8,

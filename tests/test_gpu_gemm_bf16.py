@@ -67,7 +67,8 @@ def _check_terms(oracle, x, c01, q2, s, b, got, precision):
 @pytest.mark.parametrize("M,K,N", [
     (300, 1024, 3072),   # 256 x 256 tiles, partial row tile
     (64, 256, 512),      # 128 x 128 tiles
-    (520, 96, 200),      # K not a multiple of 32, N below one 256-column tile
+    (520, 96, 200),      # N below one 256-column tile
+    (520, 100, 200),     # K not a multiple of 32: a partial last K step (vector loads)
     (100, 33, 50),       # K, N not multiples of 4: the scalar-load kernel
     (544, 256, 512),     # 512 + 32 tail rows, kept in the 256-row grid (no extra round)
 ])

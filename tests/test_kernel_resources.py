@@ -31,8 +31,6 @@ BUDGET = {
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb0ELi16ELi64ELi1ELi3E"): 40,
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3E"): 88,
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi1E"): 32,
-    # opt-in bf16 GEMM, 256x256 tile with the fused QKV epilogue
-    ("nf24_gemm_bf16", "Bf16CfgILi256ELi256ELi2ELi4EEELi1ELb1ELi1E"): 8,
 }
 
 # kernels that must exist (a rename must update this test, not skip it)

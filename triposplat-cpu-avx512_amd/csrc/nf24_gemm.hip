@@ -66,7 +66,14 @@ struct GemmCfg {
 // C::kLoadThreads loading threads owns fixed X float4 units and W units
 // (column pair, kWK consecutive k).  kVec: x rows 16-byte aligned with
 // K % 4 == 0, and N, n_start, n_count even (a column pair is one 32-bit /
-// 16-bit access).
+// 16-bit access), the code planes and the tile's x rows each below 2^31
+// bytes (vec_buffers_fit).  The kVec path loads through buffer resources --
+// x from the tile's first row, the code planes from their start -- with
+// fixed per-thread byte offsets: rows past M and columns past n_count carry
+// kBufOob, code rows past K lie past the end of the planes, so every bound
+// reads 0 without a branch in the K loop (measured against guarded 64-bit
+// pointer loads: configs[0] 207 -> 198 us, 16384 x 4096 x 1024 1084 -> 1036
+// us, 12294 x 4096 x 1024 1078 -> 937 us, bit-identical).
 template <class C, bool kVec>
 struct TileLoader {
   int t;
@@ -77,6 +84,9 @@ struct TileLoader {
   floatx4 xr[C::kXIter];
   uint32_t cr[C::kWIter][C::kWK];  // two int16 codes (columns lc, lc+1)
   uint32_t qr[C::kWIter][C::kWK];  // two int8 codes in the low 16 bits
+  __amdgpu_buffer_rsrc_t rx, rc, rq;  // kVec: x tile rows, code01 plane, q2 plane
+  uint32_t x_off[C::kXIter];          // byte offset of the x unit at k0 = 0, or kBufOob
+  uint32_t c_off[C::kWIter], q_off[C::kWIter];  // byte offsets of the code row kWK*w_kq at k0 = 0
 
   // The column pairs and their scales are fixed for the whole K loop.
   __device__ __forceinline__ void init(const GemmArgs& a, int t_, int m0_, int c0) {
@@ -95,9 +105,53 @@ struct TileLoader {
       w_sc0[j] = w_ok0[j] ? a.scale[w_nabs[j]] : 0.0f;
       w_sc1[j] = w_ok1[j] ? a.scale[w_nabs[j] + 1] : 0.0f;
     }
+    if constexpr (kVec) {
+      // x: rows m0 .. m0 + rows - 1, the last one K floats long
+      const int rows = min(C::BM, a.M - m0);
+      rx = buffer_rsrc(a.x + (int64_t)m0 * a.stride_x, ((int64_t)(rows - 1) * a.stride_x + a.K) * 4);
+      rc = buffer_rsrc(a.code01, (int64_t)a.K * a.N * 2);
+      rq = buffer_rsrc(a.q2, (int64_t)a.K * a.N);
+#pragma unroll
+      for (int j = 0; j < C::kXIter; ++j) {
+        const int idx = t + j * C::kLoadThreads;
+        const int row = idx / (C::BK / 4);
+        const int kc = idx % (C::BK / 4);
+        const bool live = (C::kXUnits % C::kLoadThreads == 0) || idx < C::kXUnits;
+        x_off[j] = (live && row < rows) ? (uint32_t)(row * a.stride_x + 4 * kc) * 4u : kBufOob;
+      }
+#pragma unroll
+      for (int j = 0; j < C::kWIter; ++j) {
+        // w_ok1 == w_ok0 here: n_start and n_count are even
+        const uint32_t e = (uint32_t)(C::kWK * w_kq[j] * a.N + w_nabs[j]);
+        c_off[j] = w_ok0[j] ? 2u * e : kBufOob;
+        q_off[j] = w_ok0[j] ? e : kBufOob;
+      }
+    }
   }
 
   __device__ __forceinline__ void load(const GemmArgs& a, int k0) {
+    if constexpr (kVec) {
+#pragma unroll
+      for (int j = 0; j < C::kXIter; ++j) {
+        // K % 4 == 0: a float4 unit lies wholly inside or past the row's K floats
+        const int kc = (t + j * C::kLoadThreads) % (C::BK / 4);
+        const uint32_t off = (k0 + 4 * kc < a.K) ? x_off[j] + 4u * (uint32_t)k0 : kBufOob;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+        xr[j] = floatx4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                        __uint_as_float(v[3])};
+      }
+#pragma unroll
+      for (int j = 0; j < C::kWIter; ++j) {
+#pragma unroll
+        for (int i = 0; i < C::kWK; ++i) {
+          // code rows k0 + i + kWK*w_kq >= K lie past the end of the planes: they read 0
+          const uint32_t e = (uint32_t)(k0 + i) * (uint32_t)a.N;
+          cr[j][i] = __builtin_amdgcn_raw_buffer_load_b32(rc, (int)(c_off[j] + 2u * e), 0, 0);
+          qr[j][i] = __builtin_amdgcn_raw_buffer_load_b16(rq, (int)(q_off[j] + e), 0, 0);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < C::kXIter; ++j) {
       const int idx = t + j * C::kLoadThreads;
@@ -107,13 +161,8 @@ struct TileLoader {
       const int gk = k0 + 4 * kc;
       const bool live = (C::kXUnits % C::kLoadThreads == 0) || idx < C::kXUnits;
       const float* src = a.x + (int64_t)gm * a.stride_x + gk;
-      if (kVec) {
-        xr[j] = (live && gm < a.M && gk < a.K) ? *reinterpret_cast<const floatx4*>(src)
-                                                 : floatx4{0, 0, 0, 0};
-      } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xr[j][e] = (live && gm < a.M && gk + e < a.K) ? src[e] : 0.0f;
-      }
+      for (int e = 0; e < 4; ++e) xr[j][e] = (live && gm < a.M && gk + e < a.K) ? src[e] : 0.0f;
     }
 #pragma unroll
     for (int j = 0; j < C::kWIter; ++j) {
@@ -122,18 +171,12 @@ struct TileLoader {
         const int gk = k0 + C::kWK * w_kq[j] + i;
         const int64_t off = (int64_t)gk * a.N + w_nabs[j];
         const bool k_ok = gk < a.K;
-        if (kVec) {
-          const bool ok = w_ok0[j] && k_ok;
-          cr[j][i] = ok ? *reinterpret_cast<const uint32_t*>(a.code01 + off) : 0u;
-          qr[j][i] = ok ? (uint32_t)*reinterpret_cast<const uint16_t*>(a.q2 + off) : 0u;
-        } else {
-          const uint32_t c_lo = (k_ok && w_ok0[j]) ? (uint16_t)a.code01[off] : 0u;
-          const uint32_t c_hi = (k_ok && w_ok1[j]) ? (uint16_t)a.code01[off + 1] : 0u;
-          const uint32_t q_lo = (k_ok && w_ok0[j]) ? (uint8_t)a.q2[off] : 0u;
-          const uint32_t q_hi = (k_ok && w_ok1[j]) ? (uint8_t)a.q2[off + 1] : 0u;
-          cr[j][i] = c_lo | (c_hi << 16);
-          qr[j][i] = q_lo | (q_hi << 8);
-        }
+        const uint32_t c_lo = (k_ok && w_ok0[j]) ? (uint16_t)a.code01[off] : 0u;
+        const uint32_t c_hi = (k_ok && w_ok1[j]) ? (uint16_t)a.code01[off + 1] : 0u;
+        const uint32_t q_lo = (k_ok && w_ok0[j]) ? (uint8_t)a.q2[off] : 0u;
+        const uint32_t q_hi = (k_ok && w_ok1[j]) ? (uint8_t)a.q2[off + 1] : 0u;
+        cr[j][i] = c_lo | (c_hi << 16);
+        qr[j][i] = q_lo | (q_hi << 8);
       }
     }
   }
@@ -371,7 +414,8 @@ int launch_cfg(const GemmParams& p, hipStream_t stream, const QkvArgs& e = QkvAr
   const bool vec = (reinterpret_cast<uintptr_t>(p.x) % 16 == 0) && (p.stride_x % 4 == 0) &&
                    (p.K % 4 == 0) && (p.N % 2 == 0) && (p.n_start % 2 == 0) &&
                    (p.n_count % 2 == 0) && (reinterpret_cast<uintptr_t>(p.code01) % 4 == 0) &&
-                   (reinterpret_cast<uintptr_t>(p.q2) % 2 == 0);
+                   (reinterpret_cast<uintptr_t>(p.q2) % 2 == 0) &&
+                   vec_buffers_fit(p, C::BM, C::BK);
   dim3 grid((unsigned)tiles), block(C::kThreads);
   if (vec)
     hipLaunchKernelGGL((nf24_gemm_kernel<C, true, kEpi>), grid, block, 0, stream, a);

@@ -202,8 +202,56 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
   uint32_t cr[kStages][C::kWIter][4][2];  // k row i: int16 codes of columns 0,1 | 2,3
   uint32_t qr[kStages][C::kWIter][4];     // k row i: int8 codes of columns 0..3
 
+  // kVec: buffer-resource loads from per-thread byte offsets, as in the
+  // strict kernel's TileLoader -- rows past M and columns past n_count carry
+  // kBufOob, code rows past K lie past the end of the planes.
+  __amdgpu_buffer_rsrc_t rx, rc, rq;
+  uint32_t x_off[C::kXIter], c_off[C::kWIter], q_off[C::kWIter];
+  if constexpr (kVec) {
+    const int rows = min(C::BM, a.M - m0);
+    rx = buffer_rsrc(a.x + (int64_t)m0 * a.stride_x, ((int64_t)(rows - 1) * a.stride_x + a.K) * 4);
+    rc = buffer_rsrc(a.code01, (int64_t)a.K * a.N * 2);
+    rq = buffer_rsrc(a.q2, (int64_t)a.K * a.N);
+#pragma unroll
+    for (int j = 0; j < C::kXIter; ++j) {
+      const int idx = tid + j * C::kThreads;
+      const int row = idx / (C::BK / 4);
+      x_off[j] = row < rows ? (uint32_t)(row * a.stride_x + 4 * (idx % (C::BK / 4))) * 4u : kBufOob;
+    }
+#pragma unroll
+    for (int j = 0; j < C::kWIter; ++j) {
+      // all four columns are valid with the first: n_start and n_count are multiples of 4
+      const uint32_t e = (uint32_t)(w_k[j] * a.N + a.n_start + c0 + w_col[j]);
+      c_off[j] = w_ok[j][0] ? 2u * e : kBufOob;
+      q_off[j] = w_ok[j][0] ? e : kBufOob;
+    }
+  }
+
   auto load_tile = [&](auto set_c, int k0) {
     constexpr int S = decltype(set_c)::value;
+    if constexpr (kVec) {
+#pragma unroll
+      for (int j = 0; j < C::kXIter; ++j) {
+        // K % 4 == 0: a float4 unit lies wholly inside or past the row's K floats
+        const int kc = (tid + j * C::kThreads) % (C::BK / 4);
+        const uint32_t off = (k0 + 4 * kc < a.K) ? x_off[j] + 4u * (uint32_t)k0 : kBufOob;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+        xr[S][j] = floatx4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                           __uint_as_float(v[3])};
+      }
+#pragma unroll
+      for (int j = 0; j < C::kWIter; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t e = (uint32_t)(k0 + i) * (uint32_t)a.N;
+          const auto c = __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(c_off[j] + 2u * e), 0, 0);
+          cr[S][j][i][0] = c[0];
+          cr[S][j][i][1] = c[1];
+          qr[S][j][i] = __builtin_amdgcn_raw_buffer_load_b32(rq, (int)(q_off[j] + e), 0, 0);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < C::kXIter; ++j) {
       const int idx = tid + j * C::kThreads;
@@ -404,7 +452,8 @@ int launch_gemm_bf16(const GemmParams& p, int epi, const QkvArgs& e, const GemmE
   const bool vec = (reinterpret_cast<uintptr_t>(p.x) % 16 == 0) && (p.stride_x % 4 == 0) &&
                    (p.K % 4 == 0) && (p.N % 4 == 0) && (p.n_start % 4 == 0) &&
                    (p.n_count % 4 == 0) && (reinterpret_cast<uintptr_t>(p.code01) % 8 == 0) &&
-                   (reinterpret_cast<uintptr_t>(p.q2) % 4 == 0);
+                   (reinterpret_cast<uintptr_t>(p.q2) % 4 == 0) &&
+                   vec_buffers_fit(p, Bf16Large::BM, Bf16Large::BK);
   if (!vec) return launch_shape<Bf16Small, false>(a, terms, epi, stream);
   // 256 x 256 tiles where there are rows and columns to fill them.  Rows
   // past the last multiple of 256 that number at most 32 stay in that grid

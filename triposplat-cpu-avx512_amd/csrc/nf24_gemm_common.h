@@ -238,6 +238,16 @@ __device__ __forceinline__ void store_result(const GemmArgs& a, floatx16 (&acc)[
     }
 }
 
+// The buffer-resource loads of the kernels' vector paths address the code
+// planes (rows up to K + bk) and a tile's bm rows of x with 32-bit byte
+// offsets that must stay below 2^31 (kBufOob); larger operands take the
+// scalar paths.
+inline bool vec_buffers_fit(const GemmParams& p, int bm, int bk) {
+  constexpr int64_t kLimit = 0x7fffffffLL;
+  return ((int64_t)p.K + bk) * p.N * 2 < kLimit &&
+         ((int64_t)(bm - 1) * p.stride_x + p.K + bk) * 4 < kLimit;
+}
+
 // bf16-MFMA GEMM (nf24_gemm_bf16.hip) for p.precision kPrecisionBf16 /
 // kPrecisionBf16x3 and M > 32: epilogue kind epi (kEpi* / kEpilogue*), QKV
 // operands e, gate operands ep, token index of row 0 row0.

@@ -40,6 +40,18 @@ __device__ __forceinline__ float bf16_roundtrip(float x) {
   return __uint_as_float(u & 0xffff0000u);
 }
 
+// Buffer-resource loads.  A raw buffer (stride 0) covers num_records bytes
+// from its base; a lane whose byte offset is >= num_records reads 0 and
+// touches no memory.  Hot loops address their operands as 32-bit offsets
+// from such a base: no 64-bit address arithmetic per load, and bounds that
+// would be exec-mask branches become an offset of kBufOob.  Callers keep
+// every buffer below 2^31 bytes, so kBufOob plus any in-range step stays out
+// of range without wrapping.
+constexpr uint32_t kBufOob = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
 // Compute units of the current device, queried once per device (256 on
 // MI355X, also the fallback when the query fails; the count only shapes
 // launch plans).  Defined in nf24_gemm.hip.
