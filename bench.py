@@ -357,11 +357,9 @@ def run_gemm(torch, dev, iters, ref_parity=False):
     def step():
         nf24_linear(x, codes[0], codes[1], scales[0], bias, out=gout)
 
-    # ~10 ms of warm-up calls: after a short warm-up the first timed batches
-    # still run while the GPU clock ramps (up to 15 % slower)
-    for _ in range(40):
-        step()
-    torch.cuda.synchronize()
+    # 0.5 s of warm-up calls: the clock settles over the first ~100 calls of a
+    # 0.2 ms kernel (a 40-call warm-up left the timed batches 5-10 % slower)
+    warm_up(torch, step, 0.5)
     # median of 5 batches: clocks on these boxes vary by ~10 % between batches
     g_ms = sorted(time_events(torch, step, iters) for _ in range(5))[2]
     g_flop = 2.0 * M * N * K
@@ -373,9 +371,7 @@ def run_gemm(torch, dev, iters, ref_parity=False):
         def step_p(p=precision):
             nf24_linear(x, codes[0], codes[1], scales[0], bias, out=gout, precision=p)
 
-        for _ in range(40):
-            step_p()
-        torch.cuda.synchronize()
+        warm_up(torch, step_p, 0.5)
         p_ms = sorted(time_events(torch, step_p, iters) for _ in range(5))[2]
         d = (gout.double() - strict.double())
         p_tf = g_flop / (p_ms * 1e-3) / 1e12
@@ -432,7 +428,7 @@ def run_gemm(torch, dev, iters, ref_parity=False):
 def time_interleaved(torch, fns, iters, rounds=5):
     """Median per-call device time (ms) of each callable, timed in
     interleaved rounds (clocks drift between rounds on these boxes)."""
-    warm_up(torch, lambda: [f() for f in fns.values()])
+    warm_up(torch, lambda: [f() for f in fns.values()], 0.5)
     ts = {k: [] for k in fns}
     for _ in range(rounds):
         for k, f in fns.items():
