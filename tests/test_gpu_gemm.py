@@ -256,15 +256,20 @@ def test_pointer_checks_within_one_allocation(oracle, cuda, hiplib):
         assert hip.hipFree(base) == 0
 
 
-@pytest.mark.parametrize("M,K,N", [(16385, 1024, 1024), (8194, 1024, 3072)])
+@pytest.mark.parametrize("M,K,N", [(16385, 1024, 1024), (8194, 1024, 3072), (12294, 256, 1024),
+                                   (2818, 256, 3072)])
 def test_gemm_tail_rows(oracle, cuda, hiplib, M, K, N):
     """M = 256 k + r with r <= 32 (e.g. the compressed negative branch, L + 1
-    tokens): 16385 x 1024 runs the tail row as a separate 32-row-tile launch
-    (in the 256-row grid it would add a round), 8194 x 3072 keeps its two tail
-    rows in the grid (their tiles fit the last round).  Either way rows of the
-    256-row part equal a GEMM over exactly those rows and the tail rows equal
-    the same rows computed inside a 256-row tile (a larger M with no tail),
-    bit for bit; sampled rows and the tail against the oracle."""
+    tokens): 16385 x 1024 and 8194 x 3072 run the tail rows as a separate
+    32-row-tile launch (in the main grid they would add a round), 12294 x 1024
+    (the reference's sequence length) runs 12288 rows on 192 x 256 tiles --
+    one round of 256 -- and the 6-row tail as a second launch, 2818 x 3072
+    keeps its two tail rows in its 256 x 192 grid (their tiles fit the last
+    round).  Either way rows
+    of the main part equal a GEMM over exactly those rows, and the same rows
+    of a larger M with no tail (another tile shape), and the tail rows equal
+    the same rows computed inside a 256-row tile, bit for bit; sampled rows
+    and the tail against the oracle."""
     import torch
 
     print(f"gemm tail rows M={M} K={K} N={N}", flush=True)
@@ -276,6 +281,7 @@ def test_gemm_tail_rows(oracle, cuda, hiplib, M, K, N):
     head = _run_async(torch, hiplib, cuda, x[:M - r], c01, q2, s, b)
     full = _run_async(torch, hiplib, cuda, x[:big], c01, q2, s, b)
     assert np.array_equal(got[:M - r].view(np.uint32), head.view(np.uint32))
+    assert np.array_equal(head.view(np.uint32), full[:M - r].view(np.uint32))
     assert np.array_equal(got[M - r:].view(np.uint32), full[M - r:M].view(np.uint32))
     rows = np.concatenate([np.sort(np.random.default_rng(M).choice(M - r, 16, replace=False)),
                            np.arange(M - r, M)])

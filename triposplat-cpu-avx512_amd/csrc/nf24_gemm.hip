@@ -450,6 +450,11 @@ using CfgLarge = GemmCfg<256, 256, 16, 4, 4>;    // 16 waves, 1 workgroup / CU
 // multiplied after its barrier (measured at configs[0]: BK 16 -> 32 -5 %,
 // deferral a further -3 %; with deferral the 256 x 256 tile is 4 % slower)
 using CfgWide = GemmCfg<256, 192, 32, 4, 3, 1, 0, true>;
+// 12 waves, 1 workgroup / CU, the 256 x 192 tile's loop transposed: for
+// row counts whose 256-row bands leave CUs idle but 192-row bands fill whole
+// rounds (the reference's L = 12294 at N = 1024: 196 tiles of 256 x 256 on
+// 256 CUs, against 256 tiles of 192 x 256 plus the 6-row tail launch)
+using CfgTall = GemmCfg<192, 256, 32, 3, 4, 1, 0, true>;
 using CfgSmall = GemmCfg<128, 128, 16, 2, 2, 3>; // 4 waves, 3 workgroups / CU
 using CfgSkinny = GemmCfg<32, 128, 32, 1, 4>;
 using CfgTail = GemmCfg<32, 128, 32, 1, 2>;      // <= 32 rows, QKV epilogue: 64-column waves (a head)
@@ -467,7 +472,8 @@ struct Choice {
   double rate;
 };
 constexpr Choice kChoices[] = {
-    {256, 256, 1, 16, 126.0}, {256, 192, 1, 12, 125.0}, {128, 128, 3, 4, 111.0}};
+    {256, 256, 1, 16, 126.0}, {256, 192, 1, 12, 125.0}, {128, 128, 3, 4, 111.0}, {192, 256, 1, 12, 125.0}};
+constexpr int kNumChoices = sizeof(kChoices) / sizeof(kChoices[0]);
 
 // Modelled time of configuration i (kChoices) over M x n_count outputs.
 double model_time(int i, int M, int n_count) {
@@ -489,7 +495,7 @@ double model_time(int i, int M, int n_count) {
 // Index into kChoices of the configuration with the smallest modelled time.
 int pick_config(int M, int n_count) {
   int best = 0;
-  for (int i = 1; i < 3; ++i)
+  for (int i = 1; i < kNumChoices; ++i)
     if (model_time(i, M, n_count) < model_time(best, M, n_count)) best = i;
   return best;
 }
@@ -523,8 +529,8 @@ int round_split_rows(int M, int n_count) {
 // they would occupy a whole extra round of 256-row tiles (e.g. M = 16385:
 // 1040 tiles = 4 rounds + 16 one-row tiles, ~270 us at K = 1024), run as a
 // second launch of 32-row tiles instead (~30 us).  When they fit in the last
-// round the main launch already has (e.g. M = 12294: 576 + 12 tiles, three
-// rounds either way), they stay in it: the partial tile costs nothing there,
+// round the main launch already has (e.g. M = 2818, N = 3072: 12 bands of
+// 256 x 192 tiles, one round either way), they stay in it: the partial tile costs nothing there,
 // while a second launch would add its own time.  Every MFMA tile shape sums
 // each output in the same order, so the tail rows are bit-identical either way.
 constexpr int kTailRows = 32;
@@ -590,6 +596,7 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
   const int best = pick_config(p.M, p.n_count);
   if (best == 0) return launch_cfg<CfgLarge>(p, stream);
   if (best == 1) return launch_cfg<CfgWide>(p, stream);
+  if (best == 3) return launch_cfg<CfgTall>(p, stream);
   return launch_cfg<CfgSmall>(p, stream);
 }
 
@@ -613,6 +620,7 @@ int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_
   const int best = pick_config(p.M, p.n_count);
   if (best == 0) return launch_cfg<CfgLarge, kEpi>(p, stream, q, e, row0);
   if (best == 1) return launch_cfg<CfgWide, kEpi>(p, stream, q, e, row0);
+  if (best == 3) return launch_cfg<CfgTall, kEpi>(p, stream, q, e, row0);
   return launch_cfg<CfgSmall, kEpi>(p, stream, q, e, row0);
 }
 }  // namespace
