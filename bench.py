@@ -81,6 +81,35 @@ def host_cpu_model():
     return None
 
 
+def host_cpu_topology():
+    """lscpu's description of the host the CPU baselines ran on: model, family
+    / model / stepping, sockets, cores, threads per core, NUMA nodes, L3, the
+    CPUs this process may use and whether AVX-512 F/BW/DQ/VL (what the
+    reference build is compiled for) are present."""
+    import subprocess
+
+    keys = {"Model name": "model", "CPU family": "family", "Model": "model_id", "Stepping": "stepping",
+            "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+            "Thread(s) per core": "threads_per_core", "NUMA node(s)": "numa_nodes",
+            "L3 cache": "l3", "CPU(s)": "cpus", "Hypervisor vendor": "hypervisor"}
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    flags = ""
+    for line in out.splitlines():
+        k, _, v = line.partition(":")
+        k, v = k.strip(), v.strip()
+        if k in keys:
+            info[keys[k]] = v
+        elif k == "Flags":
+            flags = v
+    info["usable_cpus"] = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None
+    info["avx512_f_bw_dq_vl"] = all(f in flags.split() for f in ("avx512f", "avx512bw", "avx512dq", "avx512vl"))
+    return info
+
+
 def warm_up(torch, fn, seconds=0.05):
     """Call fn until `seconds` of device work have run: after the host-side
     reference runs the GPU sits idle and its clock ramps up again over the
@@ -192,6 +221,7 @@ def cpu_baseline_sdpa(q, k, v, budget_s=12.0, gpu_out=None, gpu_fn=None):
         "unit": "TFLOP/s",
         "cores": threads,
         "host_cpu": host_cpu_model(),
+        "host_lscpu": host_cpu_topology(),
         "kind": kind,
         "sample": f"exact SDPA q8t512 (reference AVX-512 build), B=1 H=16 D=64, {rows} of {L} query rows "
                   f"vs all {L} keys; median of 3 = {t_med:.3f} s; {threads} OpenMP threads",
