@@ -286,3 +286,37 @@ def test_gemm_tail_rows(oracle, cuda, hiplib, M, K, N):
     rows = np.concatenate([np.sort(np.random.default_rng(M).choice(M - r, 16, replace=False)),
                            np.arange(M - r, M)])
     _check(oracle, x[rows], c01, q2, s, b, got[rows])
+
+
+@pytest.mark.parametrize("precision", [0, 2])
+def test_gemm_wide_row_stride_scalar_path(oracle, cuda, hiplib, precision):
+    """A row stride so wide that a tile's x rows span 2^31 bytes: the vector
+    path addresses them with 32-bit buffer offsets, so such calls take the
+    scalar-load path.  Its result equals the vector path's on compact rows,
+    bit for bit (strict fp32 and bf16x3), and the strict one the oracle."""
+    import torch
+
+    M, K, N = 40, 96, 128
+    sx = ((1 << 31) // (4 * 127) + 64) // 4 * 4      # (127 * sx + K) * 4 bytes > 2^31
+    x, w, b = seeded_linear(17, M, K, N)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    stream = torch.cuda.current_stream(cuda).cuda_stream
+    d_c01, d_q2, d_s, d_b = (_dev(torch, a, cuda) for a in (c01, q2, s, b))
+
+    def run(xd, stride):
+        out = torch.full((M, N), float("nan"), dtype=torch.float32, device=cuda)
+        st = hiplib.tsplat_nf24_gemm_precision_async(
+            xd.data_ptr(), d_c01.data_ptr(), d_q2.data_ptr(), d_s.data_ptr(), d_b.data_ptr(),
+            out.data_ptr(), M, K, N, 0, N, stride, N, 0, None, 0, 1, precision, stream)
+        assert st == 0, st
+        torch.cuda.synchronize(cuda)
+        return out.cpu().numpy()
+
+    wide = torch.zeros((M, sx), dtype=torch.float32, device=cuda)
+    wide[:, :K] = _dev(torch, x, cuda)
+    got = run(wide, sx)
+    del wide
+    compact = run(_dev(torch, x, cuda), K)
+    assert np.array_equal(got.view(np.uint32), compact.view(np.uint32))
+    if precision == 0:
+        _check(oracle, x, c01, q2, s, b, got)
