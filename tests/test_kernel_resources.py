@@ -31,13 +31,24 @@ BUDGET = {
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb0ELi16ELi64ELi1ELi3E"): 40,
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3E"): 88,
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi1E"): 32,
+    # strict NF24 GEMM, 256x256 tile with K steps of 32 and the deferred last
+    # slice (vector-load path; epilogues store, GELU, gated, QKV, add): values
+    # live across the K loop are stored once before it and reloaded once
+    # after, no scratch access inside the loop; 2-4 % faster at L = 16384
+    # than the spill-free 16-deep step
+    ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi0E"): 12,
+    ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi1E"): 16,
+    ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi2E"): 16,
+    ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi3E"): 24,
+    ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi4E"): 12,
 }
 
 # kernels that must exist (a rename must update this test, not skip it)
 REQUIRED = [
     ("sdpa", "sdpa_kernelILi0ELb0ELi16ELi64ELb0E"),          # configs[1] headline
     ("nf24_gemm", "GemmCfgILi256ELi192ELi32ELi4ELi3ELi1ELi0ELb1EEELb1ELi0E"),  # configs[0]
-    ("nf24_gemm", "GemmCfgILi256ELi256ELi16ELi4ELi4ELi1ELi0ELb0EEELb1ELi1E"),  # fused QKV, L = 16384
+    ("nf24_gemm", "GemmCfgILi256ELi192ELi32ELi4ELi3ELi1ELi0ELb1EEELb1ELi3E"),  # fused QKV, L = 16384
+    ("nf24_gemm", "GemmCfgILi256ELi256ELi16ELi4ELi4ELi1ELi0ELb0EEELb0ELi0E"),  # 256x256 scalar-load path
 ]
 
 

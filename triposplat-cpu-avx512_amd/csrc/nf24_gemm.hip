@@ -400,6 +400,13 @@ void xcd_blocking(int tiles_m, int tiles_n, int bm, int bn, int K, int& pm, int&
   }
 }
 
+// Tile configuration of the scalar-load path for configuration C (C itself
+// unless specialised below).
+template <class C>
+struct ScalarPathCfg {
+  using type = C;
+};
+
 template <class C, int kEpi = kEpiStore>
 int launch_cfg(const GemmParams& p, hipStream_t stream, const QkvArgs& e = QkvArgs{},
                const GemmEpilogueParams& ep = GemmEpilogueParams{kEpilogueStore, nullptr, 0, 1},
@@ -420,7 +427,8 @@ int launch_cfg(const GemmParams& p, hipStream_t stream, const QkvArgs& e = QkvAr
   if (vec)
     hipLaunchKernelGGL((nf24_gemm_kernel<C, true, kEpi>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((nf24_gemm_kernel<C, false, kEpi>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((nf24_gemm_kernel<typename ScalarPathCfg<C>::type, false, kEpi>), grid, block, 0,
+                       stream, a);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
@@ -448,7 +456,11 @@ __global__ __launch_bounds__(kTailThreads) void packed_tail_zero_kernel(float* p
 // workgroup then runs alone on its CU (one wave per SIMD hides less latency).
 // Against measurement (M = 2048..32768, N = 1024..4096) the model picks the
 // fastest configuration or one within 3 % of it.
-using CfgLarge = GemmCfg<256, 256, 16, 4, 4>;    // 16 waves, 1 workgroup / CU
+// 16 waves, 1 workgroup / CU, K steps of 32 with the deferred last slice
+// (since the buffer-resource loads left room: 16384 x 4096 x 1024 1033 ->
+// 990 us against K steps of 16; two live-range values spill once per
+// workgroup, outside the K loop)
+using CfgLarge = GemmCfg<256, 256, 32, 4, 4, 1, 0, true>;
 // 12 waves, 1 workgroup / CU, K steps of 32, the last k-slice of each step
 // multiplied after its barrier (measured at configs[0]: BK 16 -> 32 -5 %,
 // deferral a further -3 %; with deferral the 256 x 256 tile is 4 % slower)
@@ -459,6 +471,14 @@ using CfgWide = GemmCfg<256, 192, 32, 4, 3, 1, 0, true>;
 // 256 CUs, against 256 tiles of 192 x 256 plus the 6-row tail launch)
 using CfgTall = GemmCfg<192, 256, 32, 3, 4, 1, 0, true>;
 using CfgSmall = GemmCfg<128, 128, 16, 2, 2, 3>; // 4 waves, 3 workgroups / CU
+// The scalar-load path (unaligned or odd operands) runs the 256 x 256 tile at
+// K steps of 16: the guarded per-element loads need the registers that the
+// 32-deep step and its deferred slice take, and spill inside the K loop.
+// Same tile, same per-output order: the same results.
+template <>
+struct ScalarPathCfg<CfgLarge> {
+  using type = GemmCfg<256, 256, 16, 4, 4>;
+};
 using CfgSkinny = GemmCfg<32, 128, 32, 1, 4>;
 using CfgTail = GemmCfg<32, 128, 32, 1, 2>;      // <= 32 rows, QKV epilogue: 64-column waves (a head)
 // <= 32 rows otherwise: each wave's cost is its chain of K/2 MFMAs per 32
