@@ -47,7 +47,7 @@ BUDGET = {
 REQUIRED = [
     ("sdpa", "sdpa_kernelILi0ELb0ELi16ELi64ELb0E"),          # configs[1] headline
     ("nf24_gemm", "GemmCfgILi256ELi192ELi32ELi4ELi3ELi1ELi0ELb1EEELb1ELi0E"),  # configs[0]
-    ("nf24_gemm", "GemmCfgILi256ELi192ELi32ELi4ELi3ELi1ELi0ELb1EEELb1ELi3E"),  # fused QKV, L = 16384
+    ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi3E"),  # fused QKV, L = 16384
     ("nf24_gemm", "GemmCfgILi256ELi256ELi16ELi4ELi4ELi1ELi0ELb0EEELb0ELi0E"),  # 256x256 scalar-load path
 ]
 

@@ -447,9 +447,9 @@ __global__ __launch_bounds__(kTailThreads) void packed_tail_zero_kernel(float* p
 
 // Tile configurations and the rates they sustain on MI355X when the grid is
 // many rounds deep (fp32 TFLOP/s, measured over M = 16384..32768 shapes; the
-// 256 x 192 tile's K steps of 32 with the deferred last slice make it 1-2 %
-// faster than 256 x 256 where both fill whole rounds: 16384 x 1024 x 3072
-// 789 -> 776 us, 32768 x 1024 x 3072 1571 -> 1554 us).
+// order of the rates is what the choices rest on: where 256 x 256 and
+// 256 x 192 both fill whole rounds, 256 x 256 is 2-3 % faster, e.g.
+// 16384 x 1024 x 3072 754 against 775 us).
 // The launcher picks the one with the smallest modelled time: full rounds of
 // CUs * wgs_per_cu tiles cost wgs_per_cu * BM * BN / rate each; a partial
 // last round costs ceil(rest / CUs) tiles' worth, 25 % more when a 4-wave
@@ -495,7 +495,7 @@ struct Choice {
   double rate;
 };
 constexpr Choice kChoices[] = {
-    {256, 256, 1, 16, 126.0}, {256, 192, 1, 12, 127.0}, {128, 128, 3, 4, 111.0}, {192, 256, 1, 12, 125.0}};
+    {256, 256, 1, 16, 126.0}, {256, 192, 1, 12, 125.0}, {128, 128, 3, 4, 111.0}, {192, 256, 1, 12, 125.0}};
 constexpr int kNumChoices = sizeof(kChoices) / sizeof(kChoices[0]);
 
 // Modelled time of configuration i (kChoices) over M x n_count outputs.
