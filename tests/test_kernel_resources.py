@@ -27,8 +27,9 @@ BUDGET = {
     # spill into the key-bias or bf16 kernels instead.
     ("sdpa", "sdpa_kernelILi1ELb0ELi16ELi64ELb0E"): 8,
     # opt-in bf16x3 / bf16 SDPA at 16 waves ([B,H,L,64] k/v): 8 waves spill
-    # nothing but run 6 % slower
-    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb0ELi16ELi64ELi1ELi3E"): 40,
+    # nothing but run 6 % slower (with a key bias 5 % slower: 3.40 against
+    # 3.24 ms at configs[2])
+    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb0ELi16ELi64ELi1ELi3E"): 8,
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3E"): 88,
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi1E"): 32,
     # strict NF24 GEMM, 256x256 tile with K steps of 32 and the deferred last
