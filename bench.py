@@ -754,21 +754,23 @@ def run_flow(torch, dev, steps, with_cpu, validate):
 
 def run_flow_joint(torch, dev, steps):
     """The reference-faithful single-stream graph (tsplat/flow_joint.py): one
-    block over 18432 = 16384 latent + 2048 condition tokens (1.855 TFLOP), and
-    one 28-block CFG Euler step computed in full and with the reference's
+    block over 18433 = 16384 latent + 2048 condition + 1 camera tokens
+    (1.855 TFLOP), and one 28-block CFG Euler step of the latent and the
+    camera state computed in full and with the reference's
     exactness-preserving reductions (negative branch with one condition row +
     log(M) key bias, selected-rows final block)."""
     from tsplat.flow import FlowConfig
-    from tsplat.flow_joint import JointFlowModel
+    from tsplat.flow_joint import JointFlowModel, camera_state
 
     cfg = FlowConfig()
     C, L, Lc, H = cfg.hidden, cfg.latent_tokens, cfg.cond_tokens, cfg.heads
     model = JointFlowModel(cfg, dev)
     z_h, c_h = flow_inputs(cfg)
     z, c = torch.from_numpy(z_h).to(dev), torch.from_numpy(c_h).to(dev)
-    Lt = L + Lc
+    cam = torch.from_numpy(camera_state(cfg, SEEDS["flow_camera"])).to(dev)
+    Lt = L + Lc + 1
     _, t_mod = model.timestep(torch.full((1,), 1000.0, device=dev))
-    x = torch.cat((z, c), 0)[None].contiguous()
+    x = torch.cat((z, c, model.cam_refiner(cam)), 0)[None].contiguous()
     for _ in range(2):
         model.block_forward(model.blocks[0], x, t_mod, L)
     torch.cuda.synchronize()
@@ -776,25 +778,26 @@ def run_flow_joint(torch, dev, steps):
     blk_flop = 2.0 * Lt * C * 12 * C + 4.0 * H * Lt * Lt * 64
 
     def step_time(reduce):
-        model.euler_cfg_step(z, c, reduce_work=reduce)
+        model.euler_cfg_step(z, c, cam, reduce_work=reduce)
         torch.cuda.synchronize()
         ts = []
         for _ in range(max(1, steps)):
             t0 = time.perf_counter()
-            zn, _ = model.euler_cfg_step(z, c, reduce_work=reduce)
+            zn, _, cn, _ = model.euler_cfg_step(z, c, cam, reduce_work=reduce)
             torch.cuda.synchronize()
             ts.append(time.perf_counter() - t0)
-        return sorted(ts)[len(ts) // 2], zn
+        return sorted(ts)[len(ts) // 2], zn, cn
 
-    full_s, zf = step_time(False)
-    red_s, zr = step_time(True)
-    d = (zr - zf).double()
+    full_s, zf, cf = step_time(False)
+    red_s, zr, cr = step_time(True)
     return {
-        "workload": "single-stream graph: 28 blocks over 16384 latent + 2048 condition tokens, CFG pair, one Euler step",
+        "workload": "single-stream graph: 28 blocks over 16384 latent + 2048 condition + 1 camera tokens, "
+                    "CFG pair, one Euler step of latent and camera state",
         "block_ms": blk_ms, "block_tflops": blk_flop / (blk_ms * 1e-3) / 1e12,
         "s_per_denoise_step_full": full_s, "s_per_denoise_step_reduced": red_s,
         "speedup_from_reduction": full_s / red_s,
-        "reduced_vs_full_latent_rmse": float(d.square().mean().sqrt()),
+        "reduced_vs_full_latent_rmse": float((zr - zf).double().square().mean().sqrt()),
+        "reduced_vs_full_camera_rmse": float((cr - cf).double().square().mean().sqrt()),
     }
 
 

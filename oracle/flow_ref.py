@@ -223,24 +223,34 @@ class CpuJointFlow(CpuFlow):
         h = self._gelu(self.linear(h.reshape(Lt, C), bp["fc1"]))
         return self._gated(x, self.linear(h, bp["fc2"]).reshape(1, Lt, C), g2)
 
-    def joint_velocity(self, z, cond, t):
+    def joint_velocity(self, z, cond, cam, t):
+        """(v [L, C], v_cam [1, cam_channels]) over the sequence
+        [latent ; condition ; camera]."""
         L, C = z.shape
         t_emb, t_mod = self.timestep(t)
-        x = np.concatenate((self.linear(z, self.p["input_layer"]), cond), 0)[None].astype(np.float32)
+        x = np.concatenate((self.linear(z, self.p["input_layer"]), cond,
+                            self.linear(cam, self.p["cam_refiner"])), 0)[None].astype(np.float32)
         for bp in self.p["blocks"]:
             x = self.joint_block(bp, x, t_mod, L)
         fs = (self.p["final_shift_table"][None] + t_emb[:, None, :]).astype(np.float32)
-        h = self._modulate(self._ln(np.ascontiguousarray(x[:, :L]), self.cfg.final_ln_eps),
-                           np.ascontiguousarray(fs[:, 1]), np.ascontiguousarray(fs[:, 0]))
-        return self.linear(h.reshape(L, C), self.p["out_layer"])
+        rows = np.ascontiguousarray(np.concatenate((x[:, :L], x[:, -1:]), 1))
+        h = self._modulate(self._ln(rows, self.cfg.final_ln_eps),
+                           np.ascontiguousarray(fs[:, 1]), np.ascontiguousarray(fs[:, 0])).reshape(L + 1, C)
+        return (self.linear(h[:L], self.p["out_layer"]),
+                self.linear(np.ascontiguousarray(h[L:]), self.p["cam_out_layer"]))
 
-    def joint_euler_cfg_step(self, z, cond, step=0):
+    def joint_euler_cfg_step(self, z, cond, cam, step=0):
+        """(z_next, v_cfg, cam_next, v_cam_cfg) of one CFG Euler step."""
         ts = self.schedule()
         t = np.full(1, ts[step] * 1000.0, np.float32)
         dt = np.float32(ts[step] - ts[step + 1])
-        v_pos = np.ascontiguousarray(self.joint_velocity(z, cond, t))
-        v_neg = np.ascontiguousarray(self.joint_velocity(z, np.zeros_like(cond), t))
-        self._ew("cfg_combine_inplace", v_pos, v_neg, np.array([self.cfg.guidance], np.float32), 1, v_pos.size)
-        z_next = np.array(z, np.float32, copy=True)
-        self._ew("euler_update_inplace", z_next, v_pos, np.array([dt], np.float32), 1, z_next.size)
-        return z_next, v_pos
+        v_pos, vc_pos = self.joint_velocity(z, cond, cam, t)
+        v_neg, vc_neg = self.joint_velocity(z, np.zeros_like(cond), cam, t)
+        out = []
+        for vp, vn, state in ((v_pos, v_neg, z), (vc_pos, vc_neg, cam)):
+            vp, vn = np.ascontiguousarray(vp), np.ascontiguousarray(vn)
+            self._ew("cfg_combine_inplace", vp, vn, np.array([self.cfg.guidance], np.float32), 1, vp.size)
+            nxt = np.array(state, np.float32, copy=True)
+            self._ew("euler_update_inplace", nxt, vp, np.array([dt], np.float32), 1, nxt.size)
+            out += [nxt, vp]
+        return tuple(out)

@@ -61,6 +61,8 @@ def _check(oracle, x, c01, q2, s, b, got, start=0):
 SHAPES = [(25, 96, 64), (40, 96, 64), (10, 96, 64), (3, 96, 5), (1, 1024, 3072), (2, 1024, 256),
           (8, 4096, 64), (16, 64, 1024), (33, 130, 48), (129, 257, 200), (200, 64, 129),
           (7, 3, 17), (300, 1024, 96),
+          # the single-stream graph's camera Linears: cam_refiner 5 -> 1024, cam_out_layer 1024 -> 5
+          (1, 5, 1024), (1, 1024, 5),
           # vector (buffer-load) path with a partial last K step: K % 4 == 0, K % 16 != 0
           (70, 100, 96), (300, 1000, 384), (260, 36, 200),
           # few-row (HBM-bound) kernels: every row-count template, split and unsplit K,

@@ -65,6 +65,9 @@ class FlowConfig:
     guidance: float = 3.0
     shift: float = 3.0
     steps: int = 20
+    # camera state width (the single-stream graph's camera token; the
+    # reference's cam_out_layer is a 1024 x 5 Linear, the N = 5 tail GEMM)
+    cam_channels: int = 5
 
     def __post_init__(self):
         if self.hidden != self.heads * self.head_dim or self.head_dim != 64:
