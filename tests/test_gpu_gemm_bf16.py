@@ -65,7 +65,8 @@ def _check_terms(oracle, x, c01, q2, s, b, got, precision):
 
 @pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
 @pytest.mark.parametrize("M,K,N", [
-    (300, 1024, 3072),   # 256 x 256 tiles, partial row tile
+    (300, 1024, 3072),   # 256 x 192 tiles (fewer than one round), partial row tile
+    (768, 1024, 512),    # 256 x 192 tiles with a partial column tile (512 = 2 x 192 + 128)
     (64, 256, 512),      # 128 x 128 tiles
     (520, 96, 200),      # N below one 256-column tile
     (520, 100, 200),     # K not a multiple of 32: a partial last K step (vector loads)
@@ -107,7 +108,9 @@ def test_bf16_few_rows_run_strict(oracle, cuda, hiplib):
 
 @pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
 @pytest.mark.parametrize("M,K,N", [
-    (528, 256, 512),     # 16 tail rows whose partial tiles fit the grid's only round: one launch
+    (528, 256, 512),     # 16 tail rows in a 256 x 192 grid of one round
+    (12294, 64, 3072),   # 6 tail rows kept in a full-chip 256 x 256 grid (588 tiles, 3 rounds);
+                         # its 12288 head rows run as 256 x 192 tiles (768 tiles, 3 rounds)
     (16400, 64, 1024),   # 256 full tiles = one round on 256 CUs; the tail would add one: 128-row launch
 ])
 def test_bf16_tail_rows_bitwise(oracle, cuda, hiplib, precision, M, K, N):

@@ -60,15 +60,25 @@ struct Bf16Cfg {
   static constexpr int kThreads = WM * WN * 64;
   static constexpr int kTM = BM / WM, kTN = BN / WN;
   static constexpr int kMB = kTM / 32, kNB = kTN / 32;
-  // x: float4 units (row, 4 k); W: units of 4 columns x 4 k.
-  static constexpr int kXIter = BM * BK / 4 / kThreads;
-  static constexpr int kWIter = (BN / 4) * (BK / 4) / kThreads;
-  static_assert(kXIter * kThreads == BM * BK / 4, "x units must fill the workgroup");
-  static_assert(kWIter * kThreads == (BN / 4) * (BK / 4), "W units must fill the workgroup");
+  // x: float4 units (row, 4 k); W: units of 4 columns x 4 k.  A last
+  // iteration that not every thread has covers whole waves (the threads
+  // past the units skip it).
+  static constexpr int kXUnits = BM * BK / 4, kWUnits = (BN / 4) * (BK / 4);
+  static constexpr int kXIter = (kXUnits + kThreads - 1) / kThreads;
+  static constexpr int kWIter = (kWUnits + kThreads - 1) / kThreads;
+  static_assert(kXUnits % 64 == 0 && kWUnits % 64 == 0, "a partial iteration must cover whole waves");
   static_assert(kTM % 32 == 0 && kTN % 32 == 0, "wave tile must be 32-aligned");
+  // unit j of this thread exists (uniform over a wave)
+  __device__ static constexpr bool x_unit(int tid, int j) {
+    return kXUnits % kThreads == 0 || j + 1 < kXIter || tid + j * kThreads < kXUnits;
+  }
+  __device__ static constexpr bool w_unit(int tid, int j) {
+    return kWUnits % kThreads == 0 || j + 1 < kWIter || tid + j * kThreads < kWUnits;
+  }
 };
 
 using Bf16Large = Bf16Cfg<256, 256, 2, 4>;  // 8 waves, 128 x 64 per wave
+using Bf16Wide = Bf16Cfg<256, 192, 4, 3>;   // 12 waves, 64 x 64 per wave
 using Bf16Small = Bf16Cfg<128, 128, 2, 2>;  // 4 waves, 64 x 64 per wave
 
 // bf16 element offset of (row r, chunk c) in a 32-k tile row.
@@ -189,7 +199,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int lc = c0 + w_col[j] + e;
-      w_ok[j][e] = lc < a.n_count;
+      w_ok[j][e] = C::w_unit(tid, j) && lc < a.n_count;
       w_sc[j][e] = w_ok[j][e] ? a.scale[a.n_start + lc] : 0.0f;
     }
   }
@@ -232,6 +242,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
     if constexpr (kVec) {
 #pragma unroll
       for (int j = 0; j < C::kXIter; ++j) {
+        if (!C::x_unit(tid, j)) continue;
         // K % 4 == 0: a float4 unit lies wholly inside or past the row's K floats
         const int kc = (tid + j * C::kThreads) % (C::BK / 4);
         const uint32_t off = (k0 + 4 * kc < a.K) ? x_off[j] + 4u * (uint32_t)k0 : kBufOob;
@@ -241,6 +252,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
       }
 #pragma unroll
       for (int j = 0; j < C::kWIter; ++j) {
+        if (!C::w_unit(tid, j)) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t e = (uint32_t)(k0 + i) * (uint32_t)a.N;
@@ -254,6 +266,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
     }
 #pragma unroll
     for (int j = 0; j < C::kXIter; ++j) {
+      if (!C::x_unit(tid, j)) continue;
       const int idx = tid + j * C::kThreads;
       const int row = idx / (C::BK / 4);
       const int gm = m0 + row;
@@ -269,6 +282,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
     }
 #pragma unroll
     for (int j = 0; j < C::kWIter; ++j) {
+      if (!C::w_unit(tid, j)) continue;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int gk = k0 + w_k[j] + i;
@@ -300,6 +314,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
     constexpr int buf = decltype(buf_c)::value;
 #pragma unroll
     for (int j = 0; j < C::kXIter; ++j) {
+      if (!C::x_unit(tid, j)) continue;
       const int idx = tid + j * C::kThreads;
       const int row = idx / (C::BK / 4);
       const int kc = idx % (C::BK / 4);  // 4-k unit: chunk kc/2, half kc%2
@@ -311,6 +326,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
     }
 #pragma unroll
     for (int j = 0; j < C::kWIter; ++j) {
+      if (!C::w_unit(tid, j)) continue;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float pw[4];
@@ -463,10 +479,19 @@ int launch_gemm_bf16(const GemmParams& p, int epi, const QkvArgs& e, const GemmE
   // the same order.
   if (p.M < 256 || p.n_count < 256) return launch_shape<Bf16Small, true>(a, terms, epi, stream);
   const int rem = p.M % 256;
-  const int64_t bands = (p.n_count + 255) / 256, cus = compute_units();
+  const int64_t cus = compute_units();
+  auto rounds = [cus](int64_t tiles) { return (tiles + cus - 1) / cus; };
+  const int64_t bands = (p.n_count + 255) / 256, row_bands = (p.M + 255) / 256;
   const int64_t base = (int64_t)(p.M / 256) * bands;
-  if (rem == 0 || rem > 32 || (base + bands + cus - 1) / cus == (base + cus - 1) / cus)
-    return launch_shape<Bf16Large, true>(a, terms, epi, stream);
+  const bool split = rem != 0 && rem <= 32 && rounds(base + bands) > rounds(base);
+  // 256 x 192 tiles when their rounds of the chip, each 3/4 as long, take
+  // less time than the 256 x 256 plan (a split-off tail counted as a
+  // quarter round): M = 4096, N = 3072 gives 256 tiles, every CU once,
+  // where 256 x 256 leaves 64 of 256 idle.  A tie keeps 256 x 256.
+  const int64_t large_cost = split ? 4 * rounds(base) + 1 : 4 * rounds(row_bands * bands);
+  if (3 * rounds(row_bands * ((p.n_count + 191) / 192)) < large_cost)
+    return launch_shape<Bf16Wide, true>(a, terms, epi, stream);
+  if (!split) return launch_shape<Bf16Large, true>(a, terms, epi, stream);
   const int st = launch_shape<Bf16Large, true>(rows_of(a, 0, p.M - rem), terms, epi, stream);
   return st != kOk ? st : launch_shape<Bf16Small, true>(rows_of(a, p.M - rem, rem), terms, epi, stream);
 }
