@@ -53,17 +53,19 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
-template <int BM_, int BN_, int WM_, int WN_>
+template <int BM_, int BN_, int WM_, int WN_, int WK_ = 4>
 struct Bf16Cfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int WK = WK_;  // k rows of a W staging unit
   static constexpr int BK = 32;
   static constexpr int kThreads = WM * WN * 64;
   static constexpr int kTM = BM / WM, kTN = BN / WN;
   static constexpr int kMB = kTM / 32, kNB = kTN / 32;
-  // x: float4 units (row, 4 k); W: units of 4 columns x 4 k.  A last
+  // x: float4 units (row, 4 k); W: units of 4 columns x WK k.  A last
   // iteration that not every thread has covers whole waves (the threads
   // past the units skip it).
-  static constexpr int kXUnits = BM * BK / 4, kWUnits = (BN / 4) * (BK / 4);
+  static_assert(WK == 2 || WK == 4, "W units are 2 or 4 k rows deep");
+  static constexpr int kXUnits = BM * BK / 4, kWUnits = (BN / 4) * (BK / WK);
   static constexpr int kXIter = (kXUnits + kThreads - 1) / kThreads;
   static constexpr int kWIter = (kWUnits + kThreads - 1) / kThreads;
   static_assert(kXUnits % 64 == 0 && kWUnits % 64 == 0, "a partial iteration must cover whole waves");
@@ -78,7 +80,10 @@ struct Bf16Cfg {
 };
 
 using Bf16Large = Bf16Cfg<256, 256, 2, 4>;  // 8 waves, 128 x 64 per wave
-using Bf16Wide = Bf16Cfg<256, 192, 4, 3>;   // 12 waves, 64 x 64 per wave
+// 12 waves, 64 x 64 per wave; 2-deep W units give every thread one, so the
+// decode is spread over all twelve waves (4-deep units would leave it to six,
+// two on each of two SIMDs and one on each of the others)
+using Bf16Wide = Bf16Cfg<256, 192, 4, 3, 2>;
 using Bf16Small = Bf16Cfg<128, 128, 2, 2>;  // 4 waves, 64 x 64 per wave
 
 // bf16 element offset of (row r, chunk c) in a 32-k tile row.
@@ -135,17 +140,18 @@ __device__ __forceinline__ float w_payload(const uint32_t (&c)[2], uint32_t q, i
   return (float)(code * 256 + q2);
 }
 
-// Four weights w = fp32(p * s) of one column -- the reference's decode
-// (scripts/gemm_nf24_i16_avx512.c:26-33) -- split: hi = bf16(w), and with
-// three terms lo = bf16 of fma(p, s, -hi), the exact p * s minus hi rounded
-// once to fp32.  Spelled out so that the result does not depend on whether
-// the compiler contracts w - hi with the product that made w.
-template <int kTerms>
-__device__ __forceinline__ void split_w4(const float (&p)[4], float s, bf16x4& hi, bf16x4& lo) {
+// WK weights w = fp32(p * s) of one column -- the reference's decode
+// (scripts/gemm_nf24_i16_avx512.c:26-33) -- split into bf16 pairs: hi =
+// bf16(w), and with three terms lo = bf16 of fma(p, s, -hi), the exact
+// p * s minus hi rounded once to fp32.  Spelled out so that the result does
+// not depend on whether the compiler contracts w - hi with the product
+// that made w.
+template <int kTerms, int WK>
+__device__ __forceinline__ void split_w(const float (&p)[WK], float s, unsigned (&h)[WK / 2],
+                                        unsigned (&l)[WK / 2]) {
 #pragma clang fp contract(off)
-  unsigned h[2], l[2] = {0, 0};
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
+  for (int q = 0; q < WK / 2; ++q) {
     const float w0 = p[2 * q] * s, w1 = p[2 * q + 1] * s;
     h[q] = __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{w0, w1}, bf16x2));
     if constexpr (kTerms == 3) {
@@ -156,8 +162,13 @@ __device__ __forceinline__ void split_w4(const float (&p)[4], float s, bf16x4& h
                                               bf16x2));
     }
   }
-  hi = __builtin_bit_cast(bf16x4, uintx2{h[0], h[1]});
-  if constexpr (kTerms == 3) lo = __builtin_bit_cast(bf16x4, uintx2{l[0], l[1]});
+}
+
+// WK / 2 bf16 pairs stored at dst (8- or 4-byte aligned).
+template <int NW>
+__device__ __forceinline__ void store_pairs(__bf16* dst, const unsigned (&w)[NW]) {
+  if constexpr (NW == 2) *reinterpret_cast<uintx2*>(dst) = uintx2{w[0], w[1]};
+  else *reinterpret_cast<unsigned*>(dst) = w[0];
 }
 
 __device__ __forceinline__ floatx16 mfma_bf16(const bf16x8& a, const bf16x8& b, floatx16 c) {
@@ -187,7 +198,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
   const int c0 = (tile % tiles_n) * C::BN;
 
   // W units of this thread: columns w_col .. w_col+3 of the tile, k rows
-  // w_k .. w_k+3 of each step; the columns and their scales are fixed.
+  // w_k .. w_k+WK-1 of each step; the columns and their scales are fixed.
   int w_col[C::kWIter], w_k[C::kWIter];
   float w_sc[C::kWIter][4];
   bool w_ok[C::kWIter][4];
@@ -195,7 +206,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
   for (int j = 0; j < C::kWIter; ++j) {
     const int u = tid + j * C::kThreads;
     w_col[j] = 4 * (u % (C::BN / 4));
-    w_k[j] = 4 * (u / (C::BN / 4));
+    w_k[j] = C::WK * (u / (C::BN / 4));
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int lc = c0 + w_col[j] + e;
@@ -209,8 +220,8 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
   // term; three terms have no registers for a second set.
   constexpr int kStages = kTerms == 3 ? 1 : 2;
   floatx4 xr[kStages][C::kXIter];
-  uint32_t cr[kStages][C::kWIter][4][2];  // k row i: int16 codes of columns 0,1 | 2,3
-  uint32_t qr[kStages][C::kWIter][4];     // k row i: int8 codes of columns 0..3
+  uint32_t cr[kStages][C::kWIter][C::WK][2];  // k row i: int16 codes of columns 0,1 | 2,3
+  uint32_t qr[kStages][C::kWIter][C::WK];     // k row i: int8 codes of columns 0..3
 
   // kVec: buffer-resource loads from per-thread byte offsets, as in the
   // strict kernel's TileLoader -- rows past M and columns past n_count carry
@@ -254,7 +265,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
       for (int j = 0; j < C::kWIter; ++j) {
         if (!C::w_unit(tid, j)) continue;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < C::WK; ++i) {
           const uint32_t e = (uint32_t)(k0 + i) * (uint32_t)a.N;
           const auto c = __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(c_off[j] + 2u * e), 0, 0);
           cr[S][j][i][0] = c[0];
@@ -284,7 +295,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
     for (int j = 0; j < C::kWIter; ++j) {
       if (!C::w_unit(tid, j)) continue;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < C::WK; ++i) {
         const int gk = k0 + w_k[j] + i;
         const int64_t off = (int64_t)gk * a.N + a.n_start + c0 + w_col[j];
         if (kVec) {
@@ -329,14 +340,14 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
       if (!C::w_unit(tid, j)) continue;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float pw[4];
+        float pw[C::WK];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pw[i] = w_payload(cr[S][j][i], qr[S][j][i], e);
-        bf16x4 hi, lo;
-        split_w4<kTerms>(pw, w_sc[j][e], hi, lo);
+        for (int i = 0; i < C::WK; ++i) pw[i] = w_payload(cr[S][j][i], qr[S][j][i], e);
+        unsigned hi[C::WK / 2], lo[C::WK / 2];
+        split_w<kTerms, C::WK>(pw, w_sc[j][e], hi, lo);
         const int off = chunk_offset<kSwz>(w_row<kSwz>(w_col[j] + e), w_k[j] >> 3) + (w_k[j] & 7);
-        *reinterpret_cast<bf16x4*>(&ws[buf][0][off]) = hi;
-        if constexpr (kTerms == 3) *reinterpret_cast<bf16x4*>(&ws[buf][kPlanes - 1][off]) = lo;
+        store_pairs(&ws[buf][0][off], hi);
+        if constexpr (kTerms == 3) store_pairs(&ws[buf][kPlanes - 1][off], lo);
       }
     }
   };
