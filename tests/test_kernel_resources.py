@@ -24,7 +24,9 @@ BUDGET = {
     # loop and reloaded for the final store, i.e. one scratch store and one
     # load per lane per workgroup, none inside the loop.  Variants that keep
     # it in registers (wave index in an SGPR, 32-bit K/V offsets) move a
-    # spill into the key-bias or bf16 kernels instead.
+    # spill into the key-bias or bf16 kernels instead; buffer-resource K/V
+    # loads from one shared 32-bit offset keep these 8 bytes and add 8 to the
+    # key-bias form.
     ("sdpa", "sdpa_kernelILi1ELb0ELi16ELi64ELb0E"): 8,
     # opt-in bf16x3 / bf16 SDPA at 16 waves ([B,H,L,64] k/v): 8 waves spill
     # nothing but run 6 % slower (with a key bias 5 % slower: 3.40 against
