@@ -790,14 +790,68 @@ def run_flow_joint(torch, dev, steps):
 
     full_s, zf, cf = step_time(False)
     red_s, zr, cr = step_time(True)
+    rmse_lat = float((zr - zf).double().square().mean().sqrt())
+    rmse_cam = float((cr - cf).double().square().mean().sqrt())
+    del model, x, zf, cf, zr, cr
     return {
         "workload": "single-stream graph: 28 blocks over 16384 latent + 2048 condition + 1 camera tokens, "
                     "CFG pair, one Euler step of latent and camera state",
         "block_ms": blk_ms, "block_tflops": blk_flop / (blk_ms * 1e-3) / 1e12,
         "s_per_denoise_step_full": full_s, "s_per_denoise_step_reduced": red_s,
         "speedup_from_reduction": full_s / red_s,
-        "reduced_vs_full_latent_rmse": float((zr - zf).double().square().mean().sqrt()),
-        "reduced_vs_full_camera_rmse": float((cr - cf).double().square().mean().sqrt()),
+        "reduced_vs_full_latent_rmse": rmse_lat,
+        "reduced_vs_full_camera_rmse": rmse_cam,
+        "reference_shapes": run_flow_joint_reference_shapes(torch, dev, steps),
+    }
+
+
+# The reference's published s20 run (docs/triposplat_cpu_p0_p1_validation_20260722_ja.md:139-143):
+# 2747.270 s for 20 denoise steps on 4 EPYC 9654 cores, of which NF24 Linear 1008.472 s and exact SDPA 1432.319 s.
+PUBLISHED_S20 = {"s_per_denoise_step": 2747.270 / 20, "hot_path_s_per_denoise_step": (1008.472 + 1432.319) / 20,
+                 "cpus": 4, "host": "AMD EPYC 9654"}
+
+
+def run_flow_joint_reference_shapes(torch, dev, steps):
+    """The single-stream graph at the reference model's real sequence lengths:
+    8192 latent + 4101 condition + 1 camera tokens, 28 blocks, CFG pair with
+    both reductions -- positive branch L = 12294, compressed negative branch
+    L = 8194, final block 8193 selected queries against 12294 keys, the
+    shapes of the reference's published s20 step.  (The real model runs 4 of
+    its 28 blocks as refiners over the latent or the condition rows only, so
+    28 joint blocks are an upper bound of its block work.)"""
+    from tsplat.flow import FlowConfig
+    from tsplat.flow_joint import JointFlowModel, camera_state
+
+    cfg = FlowConfig(latent_tokens=8192, cond_tokens=4101)
+    model = JointFlowModel(cfg, dev)
+    z_h, c_h = flow_inputs(cfg)
+    z, c = torch.from_numpy(z_h).to(dev), torch.from_numpy(c_h).to(dev)
+    cam = torch.from_numpy(camera_state(cfg, SEEDS["flow_camera"])).to(dev)
+
+    def step_time():
+        model.euler_cfg_step(z, c, cam, reduce_work=True)
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(max(1, steps)):
+            t0 = time.perf_counter()
+            model.euler_cfg_step(z, c, cam, reduce_work=True)
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2]
+
+    strict = step_time()
+    model.set_precision("bf16x3", include=("blocks", "attention"))
+    fast = step_time()
+    model.set_precision("fp32")
+    return {
+        "workload": "single-stream graph at the reference's real lengths: 28 blocks over 8192 latent + 4101 condition "
+                    "+ 1 camera tokens, CFG pair with negative-branch compression (L = 12294 / 8194) and the "
+                    "selected final block (8193 x 12294), one Euler step",
+        "s_per_denoise_step": strict,
+        "opt_in_bf16x3_block_linears_and_attention_s_per_denoise_step": fast,
+        "published_reference_cpu": PUBLISHED_S20,
+        "speedup_vs_published_cpu_step": PUBLISHED_S20["s_per_denoise_step"] / strict,
+        "speedup_vs_published_cpu_hot_path": PUBLISHED_S20["hot_path_s_per_denoise_step"] / strict,
     }
 
 
