@@ -322,3 +322,42 @@ def test_gemm_wide_row_stride_scalar_path(oracle, cuda, hiplib, precision):
     assert np.array_equal(got.view(np.uint32), compact.view(np.uint32))
     if precision == 0:
         _check(oracle, x, c01, q2, s, b, got)
+
+
+def _sweep_shapes(seed, n, max_work=1.5e8):
+    """Seeded random calls: ragged and aligned M, K, N (vector and scalar
+    load paths, few-row kernels, row tails), an output range on 16-column
+    boundaries (the reference's range contract) for some, and padded x /
+    output row strides for some."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        M = int([r.integers(1, 33), r.integers(33, 300), r.integers(256, 900)][r.integers(0, 3)])
+        K = int(4 * r.integers(1, 300) if r.random() < 0.5 else r.integers(1, 1200))
+        N = int(16 * r.integers(1, 50) if r.random() < 0.5 else r.integers(1, 800))
+        if M * K * N > max_work:
+            continue
+        start, count = 0, N
+        if N % 16 == 0 and N >= 32 and r.random() < 0.5:
+            start = 16 * int(r.integers(0, N // 16))
+            count = 16 * int(r.integers(1, (N - start) // 16 + 1))
+        sx = K + (int(r.integers(1, 9)) if r.random() < 0.3 else 0)
+        so = count + (int(r.integers(1, 9)) if r.random() < 0.3 else 0)
+        out.append((M, K, N, start, count, sx, so))
+    return out
+
+
+@pytest.mark.parametrize("M,K,N,start,count,sx,so", _sweep_shapes(2026, 40))
+def test_gemm_random_shape_sweep(oracle, cuda, hiplib, M, K, N, start, count, sx, so):
+    """Random shapes, ranges and strides against the oracle within the
+    summation-order bound; the padding columns of the output rows stay
+    unwritten."""
+    import torch
+
+    print(f"gemm sweep M={M} K={K} N={N} start={start} count={count} sx={sx} so={so}", flush=True)
+    x, w, b = seeded_linear(M * 131 + K * 7 + N, M, K, N)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    got = _run_async(torch, hiplib, cuda, x, c01, q2, s, b, start=start, count=count, stride_x=sx,
+                     stride_out=so)
+    assert np.all(np.isnan(got[:, count:]))
+    _check(oracle, x, c01, q2, s, b, np.ascontiguousarray(got[:, :count]), start=start)

@@ -224,3 +224,33 @@ def test_bf16_rejects_unknown_precision(cuda, hiplib):
                                                  v.data_ptr(), out.data_ptr(), 64, 64, 64, 0, 64, 64, 64,
                                                  0, None, 0, 1, 3, None)
     assert st == -2
+
+
+def _sweep_shapes(seed, n, max_work=1.5e8):
+    """Seeded random calls of the opt-in modes: M from the strict few-row
+    range to several 256-row tiles, K and N aligned (vector loads, every tile
+    shape) or ragged (scalar loads), some with a padded x row stride."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        M = int([r.integers(33, 300), r.integers(256, 1100)][r.integers(0, 2)])
+        K = int(4 * r.integers(1, 300) if r.random() < 0.7 else r.integers(1, 1200))
+        N = int(4 * r.integers(1, 200) if r.random() < 0.7 else r.integers(1, 800))
+        if M * K * N > max_work:
+            continue
+        sx = K + (4 * int(r.integers(1, 3)) if r.random() < 0.3 else 0)
+        out.append((M, K, N, sx))
+    return out
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+@pytest.mark.parametrize("M,K,N,sx", _sweep_shapes(2027, 16))
+def test_bf16_random_shape_sweep(oracle, cuda, hiplib, precision, M, K, N, sx):
+    import torch
+
+    print(f"bf16 gemm sweep {precision} M={M} K={K} N={N} sx={sx}", flush=True)
+    x, w, b = seeded_linear(M * 17 + K * 5 + N, M, K, N, w_scale=0.02)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    got = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision, stride_x=sx)
+    e = _check_terms(oracle, x, c01, q2, s, b, got, precision)
+    assert e["rel_rmse"] < 1e-6, e

@@ -257,3 +257,35 @@ def test_sdpa_tail_split_sampled_rows(oracle, cuda, L, packed, bias):
         ref = oracle.sdpa_q8t512(np.ascontiguousarray(q[:, h:h + 1, rows]), np.ascontiguousarray(k[:, h:h + 1]),
                                  np.ascontiguousarray(v[:, h:h + 1]), kb)
         _assert_close(np.ascontiguousarray(got[:, h:h + 1, rows]), ref, v[:, h:h + 1])
+
+
+def _sweep_cases(seed, n, max_work=4e8):
+    """Seeded random calls: batch, heads, ragged Lq / Lk (partial query and
+    key tiles, one key, more keys than queries and fewer), no bias, a
+    uniform shared bias or log M on one key, [B,H,L,64] or packed K/V, BHLD
+    or BLHD output."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        B, H = int(r.integers(1, 3)), int(r.integers(1, 4))
+        Lq = int([r.integers(1, 64), r.integers(64, 700)][r.integers(0, 2)])
+        Lk = int([r.integers(1, 80), r.integers(80, 1400)][r.integers(0, 2)])
+        if B * H * Lq * Lk * 128 > max_work:
+            continue
+        bias = [None, ("uniform",), ("one", int(r.integers(0, Lk)), math.log(float(r.integers(2, 5000))))][
+            r.integers(0, 3)]
+        out.append((B, H, Lq, Lk, bias, bool(r.random() < 0.5), bool(r.random() < 0.5)))
+    return out
+
+
+@pytest.mark.parametrize("B,H,Lq,Lk,bspec,packed,blhd", _sweep_cases(2028, 32))
+def test_sdpa_random_case_sweep(oracle, cuda, B, H, Lq, Lk, bspec, packed, blhd):
+    import torch
+
+    print(f"sdpa sweep B={B} H={H} Lq={Lq} Lk={Lk} bias={bspec} packed={packed} blhd={blhd}", flush=True)
+    q, k, v = _qkv(Lq * 7 + Lk * 3 + B + H, B, H, Lq, Lk)
+    bias = _bias(bspec, Lk, H, Lk + 1)
+    got = _run(torch, cuda, q, k, v, bias, packed=packed, blhd=blhd)
+    if blhd:
+        got = got.transpose(0, 2, 1, 3)
+    _assert_close(got, oracle.sdpa_q8t512(q, k, v, bias), v)

@@ -225,3 +225,32 @@ def test_packed_kv_layout_matches(cuda, precision, B, H, Lq, Lk, bias):
         assert tail <= 1e-5 * float(vd.abs().max()), tail
     else:
         assert torch.equal(packed, rows)
+
+
+def _sweep_cases(seed, n, max_work=2e8):
+    """Seeded random calls of the opt-in modes: ragged Lq / Lk, no bias or
+    a shared or per-head bias, [B,H,L,64] or packed K/V, BHLD or BLHD."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        B, H = int(r.integers(1, 3)), int(r.integers(1, 4))
+        Lq, Lk = int(r.integers(1, 600)), int(r.integers(1, 1200))
+        if B * H * Lq * Lk * 128 > max_work:
+            continue
+        out.append((B, H, Lq, Lk, [None, "shared", "per_head"][r.integers(0, 3)], bool(r.random() < 0.5),
+                    bool(r.random() < 0.5)))
+    return out
+
+
+@pytest.mark.parametrize("precision", PRECISIONS)
+@pytest.mark.parametrize("B,H,Lq,Lk,bias,packed,blhd", _sweep_cases(2029, 12))
+def test_sdpa_bf16_random_case_sweep(oracle, cuda, precision, B, H, Lq, Lk, bias, packed, blhd):
+    import torch
+
+    print(f"sdpa bf16 sweep {precision} B={B} H={H} Lq={Lq} Lk={Lk} bias={bias} packed={packed} "
+          f"blhd={blhd}", flush=True)
+    q, k, v = _inputs(Lq * 5 + Lk + B + H, B, H, Lq, Lk)
+    b = _bias(bias, H, Lk, Lq + Lk)
+    got = _run(torch, cuda, q, k, v, precision, bias=b, per_head=bias == "per_head", packed=packed, blhd=blhd)
+    ref, bound = _bound(oracle, q, k, v, b, precision)
+    _check(got, ref, bound)
