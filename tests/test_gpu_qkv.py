@@ -302,3 +302,49 @@ def test_kv_bf16_round_probe(oracle, cuda, hiplib, mode):
     assert torch.equal(exact_fused[0], fused[0])
     assert not torch.equal(exact_fused[1 if rk else 2], fused[1 if rk else 2])
     assert hiplib.triposplat_qkv_postprocess_bf16_probe_mode() == 0
+
+
+def _sweep_cases(seed, n):
+    """Seeded random fused projections: batch, odd and tail-row lengths, head
+    counts from 1 to 16, K aligned or ragged, one shared or per-batch
+    frequency table, strict or bf16x3 products."""
+    r = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        B = int(r.integers(1, 4))
+        H = int(r.choice([1, 2, 3, 4, 16]))
+        L = int([r.integers(1, 40), r.integers(40, 700), r.integers(700, 3000)][r.integers(0, 3)])
+        if B * L * H > 40000:
+            L = max(1, 40000 // (B * H))
+        L = max(L, -(-33 // B))  # M = B * L > 32: the plain GEMM takes the tile kernels too
+        K = int(r.choice([64, 100, 256, 1024, 36]))
+        out.append((B, L, H, K, int(r.choice([1, B])), str(r.choice(["fp32", "bf16x3"]))))
+    return out
+
+
+@pytest.mark.parametrize("B,L,H,K,fb,precision", _sweep_cases(2030, 16))
+def test_qkv_fused_random_sweep(cuda, B, L, H, K, fb, precision):
+    """Fused projection == the same precision's NF24 GEMM then the
+    postprocess kernel, bit for bit, at seeded random shapes (M > 32: fewer
+    rows go to the few-row kernels, checked against the oracle instead)."""
+    import torch
+    from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
+    from tsplat.qkv import gemm_nf24_qkv_direct, qkv_rope_rmsnorm_pack
+
+    print(f"qkv sweep B={B} L={L} H={H} K={K} fb={fb} {precision}", flush=True)
+    C = H * 64
+    g = torch.Generator(device=cuda).manual_seed(B * 1000 + L + K)
+    x = torch.randn((B * L, K), generator=g, device=cuda)
+    w = torch.randn((3 * C, K), generator=g, device=cuda) * 0.02
+    bias = torch.randn((3 * C,), generator=g, device=cuda) * 0.01
+    codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+    fr = torch.from_numpy(_freqs(fb, L, H, L + 1)).to(cuda)
+    qg, kg = (torch.from_numpy(a).to(cuda) for a in _gammas(H, H + 2))
+    fused = gemm_nf24_qkv_direct(x, codes[0], codes[1], scales[0], bias, fr, qg, kg, B, L, H,
+                                 precision=precision)
+    proj = nf24_linear(x, codes[0], codes[1], scales[0], bias, precision=precision)
+    unfused = qkv_rope_rmsnorm_pack(proj, fr, qg, kg, B, L, H)
+    torch.cuda.synchronize(cuda)
+    for a_, b_ in zip(fused, unfused):
+        assert bool(torch.isfinite(a_).all())
+        assert torch.equal(a_, b_)
