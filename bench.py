@@ -748,11 +748,11 @@ def run_flow(torch, dev, steps, with_cpu, validate):
             out["config4_step"]["latent_rmse_vs_cpu"] = combined_rmse(zn.cpu().numpy(), zc)
             out["config4_step"]["velocity_rmse_vs_cpu"] = combined_rmse(v.cpu().numpy(), vc)
     del model
-    out["joint"] = run_flow_joint(torch, dev, steps)
+    out["joint"] = run_flow_joint(torch, dev, steps, with_cpu)
     return out
 
 
-def run_flow_joint(torch, dev, steps):
+def run_flow_joint(torch, dev, steps, with_cpu=False):
     """The reference-faithful single-stream graph (tsplat/flow_joint.py): one
     block over 18433 = 16384 latent + 2048 condition + 1 camera tokens
     (1.855 TFLOP), and one 28-block CFG Euler step of the latent and the
@@ -801,7 +801,7 @@ def run_flow_joint(torch, dev, steps):
         "speedup_from_reduction": full_s / red_s,
         "reduced_vs_full_latent_rmse": rmse_lat,
         "reduced_vs_full_camera_rmse": rmse_cam,
-        "reference_shapes": run_flow_joint_reference_shapes(torch, dev, steps),
+        "reference_shapes": run_flow_joint_reference_shapes(torch, dev, steps, with_cpu),
     }
 
 
@@ -811,14 +811,19 @@ PUBLISHED_S20 = {"s_per_denoise_step": 2747.270 / 20, "hot_path_s_per_denoise_st
                  "cpus": 4, "host": "AMD EPYC 9654"}
 
 
-def run_flow_joint_reference_shapes(torch, dev, steps):
+def run_flow_joint_reference_shapes(torch, dev, steps, with_cpu=False):
     """The single-stream graph at the reference model's real sequence lengths:
     8192 latent + 4101 condition + 1 camera tokens, 28 blocks, CFG pair with
     both reductions -- positive branch L = 12294, compressed negative branch
     L = 8194, final block 8193 selected queries against 12294 keys, the
     shapes of the reference's published s20 step.  (The real model runs 4 of
     its 28 blocks as refiners over the latent or the condition rows only, so
-    28 joint blocks are an upper bound of its block work.)"""
+    28 joint blocks are an upper bound of its block work.)  With with_cpu and
+    the reference's AVX-512 build on the host, the same step is computed in
+    full (both branches over all 12294 rows, all 28 blocks) by the
+    reference's kernels on the host cores: its wall time, and the latent and
+    camera RMSE of the device's reduced step against it (the north star's
+    full-sampler-step gate, compare_latent_npz.py:22-71)."""
     from tsplat.flow import FlowConfig
     from tsplat.flow_joint import JointFlowModel, camera_state
 
@@ -840,9 +845,39 @@ def run_flow_joint_reference_shapes(torch, dev, steps):
         return sorted(ts)[len(ts) // 2]
 
     strict = step_time()
+    zn, _, cn, _ = model.euler_cfg_step(z, c, cam, reduce_work=True)
+    zn, cn = zn.cpu().numpy(), cn.cpu().numpy()
     model.set_precision("bf16x3", include=("blocks", "attention"))
     fast = step_time()
+    zn3, _, cn3, _ = model.euler_cfg_step(z, c, cam, reduce_work=True)
+    zn3, cn3 = zn3.cpu().numpy(), cn3.cpu().numpy()
     model.set_precision("fp32")
+    cpu_res = None
+    if with_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+        from flow_ref import CpuJointFlow, combined_rmse
+
+        if O.ref_available():
+            cpu = CpuJointFlow(model.host(), cfg, backend="reference", threads=HOST_THREADS)
+            t0 = time.perf_counter()
+            cpu.progress = lambda i: print(f"cpu joint step: block {i + 1}/{cfg.blocks} "
+                                           f"({time.perf_counter() - t0:.0f} s)", file=sys.stderr, flush=True)
+            zc, _, cc, _ = cpu.joint_euler_cfg_step(z_h, c_h, camera_state(cfg, SEEDS["flow_camera"]))
+            cpu_s = time.perf_counter() - t0
+            cpu_res = {
+                "kind": "reference", "cores": HOST_THREADS, "host_cpu": host_cpu_model(),
+                "sample": "the whole step (28 blocks, both CFG branches over all 12294 rows, no reduction) "
+                          "through the reference's own AVX-512 kernels",
+                "s_per_denoise_step": cpu_s, "speedup_gpu_vs_cpu": cpu_s / strict,
+                "speedup_gpu_bf16x3_vs_cpu": cpu_s / fast,
+                "latent_rmse_vs_cpu": combined_rmse(zn, zc), "camera_rmse_vs_cpu": combined_rmse(cn, cc),
+                "bf16x3_latent_rmse_vs_cpu": combined_rmse(zn3, zc),
+                "bf16x3_camera_rmse_vs_cpu": combined_rmse(cn3, cc), "gate_rmse": 1e-4,
+            }
+            cpu_res["within_gate"] = bool(max(cpu_res["latent_rmse_vs_cpu"], cpu_res["camera_rmse_vs_cpu"],
+                                              cpu_res["bf16x3_latent_rmse_vs_cpu"],
+                                              cpu_res["bf16x3_camera_rmse_vs_cpu"]) <= 1e-4)
     return {
         "workload": "single-stream graph at the reference's real lengths: 28 blocks over 8192 latent + 4101 condition "
                     "+ 1 camera tokens, CFG pair with negative-branch compression (L = 12294 / 8194) and the "
@@ -852,6 +887,7 @@ def run_flow_joint_reference_shapes(torch, dev, steps):
         "published_reference_cpu": PUBLISHED_S20,
         "speedup_vs_published_cpu_step": PUBLISHED_S20["s_per_denoise_step"] / strict,
         "speedup_vs_published_cpu_hot_path": PUBLISHED_S20["hot_path_s_per_denoise_step"] / strict,
+        "cpu_reference_full_step": cpu_res,
     }
 
 

@@ -230,8 +230,10 @@ class CpuJointFlow(CpuFlow):
         t_emb, t_mod = self.timestep(t)
         x = np.concatenate((self.linear(z, self.p["input_layer"]), cond,
                             self.linear(cam, self.p["cam_refiner"])), 0)[None].astype(np.float32)
-        for bp in self.p["blocks"]:
+        for i, bp in enumerate(self.p["blocks"]):
             x = self.joint_block(bp, x, t_mod, L)
+            if self.progress is not None:
+                self.progress(i)
         fs = (self.p["final_shift_table"][None] + t_emb[:, None, :]).astype(np.float32)
         rows = np.ascontiguousarray(np.concatenate((x[:, :L], x[:, -1:]), 1))
         h = self._modulate(self._ln(rows, self.cfg.final_ln_eps),
