@@ -23,18 +23,22 @@ struct SdpaArgs {
   int64_t bias_head_stride;
   int out_blhd;
   // Tail split: workgroups [0, full_tiles) each own one query tile over all
-  // keys; the rest take one of `splits` key ranges (keys_per_split keys, a
-  // multiple of the key tile) of tile full_tiles + j / splits and write the
-  // unnormalised output rows and (max, sum) to part_o / part_ml, which
-  // sdpa_combine_kernel merges.
+  // keys; the rest are pieces, each one key range of a tail tile, writing
+  // the unnormalised output rows and (max, sum) to part_o / part_ml (piece
+  // j: rows j * kBQ ..), which sdpa_combine_kernel merges.  The first
+  // pieces_full pieces split their tiles into `splits` ranges of
+  // keys_per_split keys (a multiple of the key tile); the pieces after them
+  // split the partial query tiles (numbered last) into splits_p ranges of
+  // keys_per_split_p keys.
   int full_tiles, splits, keys_per_split;
+  int pieces_full, splits_p, keys_per_split_p;
   float* part_o;   // [split item][query][64]
   float* part_ml;  // [split item][query][2]
 };
 
 inline SdpaArgs make_args(const SdpaParams& p) {
   return SdpaArgs{p.q,   p.k,  p.v,  p.bias, p.out, p.B, p.H, p.Lq, p.Lk, p.Lkp, p.bias_head_stride,
-                  p.out_blhd, 0, 1, p.Lk, nullptr, nullptr};
+                  p.out_blhd, 0, 1, p.Lk, 0, 1, p.Lk, nullptr, nullptr};
 }
 
 namespace {
@@ -117,11 +121,17 @@ __device__ __forceinline__ TileWork tile_work(const SdpaArgs& a) {
   TileWork w{0, -1, 0, a.Lk};
   if ((int)blockIdx.x < a.full_tiles) {
     w.tile = xcd_tile_index(blockIdx.x, a.full_tiles);
-  } else {  // tail: one key range of a query tile
+  } else if ((int)blockIdx.x - a.full_tiles < a.pieces_full) {  // tail: a key range of a tile
     w.part = blockIdx.x - a.full_tiles;
     w.tile = a.full_tiles + w.part / a.splits;
     w.k_begin = (w.part % a.splits) * a.keys_per_split;
     w.k_end = min(a.Lk, w.k_begin + a.keys_per_split);
+  } else {  // tail: a key range of a partial query tile
+    w.part = blockIdx.x - a.full_tiles;
+    const int pp = w.part - a.pieces_full;
+    w.tile = a.full_tiles + a.pieces_full / a.splits + pp / a.splits_p;
+    w.k_begin = (pp % a.splits_p) * a.keys_per_split_p;
+    w.k_end = min(a.Lk, w.k_begin + a.keys_per_split_p);
   }
   return w;
 }
@@ -190,11 +200,15 @@ __global__ __launch_bounds__(kCombineThreads) void sdpa_combine_kernel(SdpaArgs 
   tile_coords(a, tile, q_per_tile, bh, qb);
   const int qrow = qb * q_per_tile + qi;
   if (qrow >= a.Lq) return;
-  const int64_t base = (int64_t)ptile * a.splits * q_per_tile + qi;
+  const int tail_full = a.pieces_full / a.splits;  // tail tiles split `splits` ways
+  const int nsplit = ptile < tail_full ? a.splits : a.splits_p;
+  const int64_t piece0 = ptile < tail_full ? (int64_t)ptile * a.splits
+                                           : a.pieces_full + (int64_t)(ptile - tail_full) * a.splits_p;
+  const int64_t base = piece0 * q_per_tile + qi;
   float m = -INFINITY;
-  for (int s = 0; s < a.splits; ++s) m = fmaxf(m, a.part_ml[2 * (base + (int64_t)s * q_per_tile)]);
+  for (int s = 0; s < nsplit; ++s) m = fmaxf(m, a.part_ml[2 * (base + (int64_t)s * q_per_tile)]);
   float l = 0.0f, o = 0.0f;
-  for (int s = 0; s < a.splits; ++s) {
+  for (int s = 0; s < nsplit; ++s) {
     const int64_t row = base + (int64_t)s * q_per_tile;
     const float w = __builtin_amdgcn_exp2f(a.part_ml[2 * row] - m);
     l = fmaf(a.part_ml[2 * row + 1], w, l);
@@ -206,23 +220,19 @@ __global__ __launch_bounds__(kCombineThreads) void sdpa_combine_kernel(SdpaArgs 
   dst[d] = o * (1.0f / l);
 }
 
-// Key ranges for each of the `rest` tiles of a partial last round.  Modelled
-// in units of one full tile over all keys: with s ranges the rest's full
-// tiles make ceil(full * s / cus) rounds of 1/s each, plus a fixed cost per
-// piece (its prologue, Q load and partial store) of 2 % of a tile; partial
-// tiles (numbered last, see tile_coords) cost little and are not counted.
-// rest * s stays within 2 * cus, so the partials need at most
-// (2 * cus - 1) * kBQ rows of workspace; s <= 16.
-inline int choose_splits(const SdpaParams& p, int kBQ, int64_t rest, int cus) {
-  const int64_t partial = (p.Lq % kBQ != 0) ? (int64_t)p.B * p.H : 0;
-  const int64_t full = rest > partial ? rest - partial : 0;
-  if (full == 0) {  // only partial tiles: spread them over the CUs
-    const int64_t s = (cus + rest - 1) / rest;
-    return (int)(s < 16 ? s : 16);
-  }
+// Key ranges for the tiles of a partial last round.  Modelled in units of
+// one full tile over all keys: `full` full tiles split s ways make
+// ceil(full * s / cus) rounds of 1/s each, plus a fixed cost per piece (its
+// prologue, Q load and partial store) of 2 % of a tile.  The `partial` query
+// tiles (numbered last, see tile_coords; their few live waves still stream
+// every key tile, at a few us each) take the slots left after the full
+// tiles' pieces and are split by the same model into s_p ranges of their
+// own.  All pieces together stay within 2 * cus - 1, so the partials need
+// at most (2 * cus - 1) * kBQ rows of workspace; s, s_p <= 16.
+inline int choose_splits(int64_t full, int64_t reserve, int cus) {
   int best = 1;
   double best_t = 1e30;
-  for (int s = 1; s <= 16 && rest * s <= 2 * (int64_t)cus; ++s) {
+  for (int s = 1; s <= 16 && full * s + reserve <= 2 * (int64_t)cus - 1; ++s) {
     const double t = (double)((full * s + cus - 1) / cus) * (1.0 / s + 0.02);
     if (t < best_t - 1e-9) {
       best_t = t;
@@ -230,6 +240,12 @@ inline int choose_splits(const SdpaParams& p, int kBQ, int64_t rest, int cus) {
     }
   }
   return best;
+}
+
+// Keys per range (a multiple of the key tile) and the resulting range count.
+inline void key_ranges(int Lk, int kBKV, int s0, int& kps, int& splits) {
+  kps = ((Lk + s0 - 1) / s0 + kBKV - 1) / kBKV * kBKV;
+  splits = (Lk + kps - 1) / kps;
 }
 
 // Launches `main(grid, args)` over the query tiles of kBQ queries.  A last
@@ -249,11 +265,19 @@ int launch_tiles(SdpaArgs a, const SdpaParams& p, int kBQ, int kBKV, int cus, hi
   a.keys_per_split = p.Lk;
   const int64_t rest = cus > 0 ? tiles % cus : 0;
   if (cus > 0 && tiles >= cus && rest != 0) {
-    const int splits0 = choose_splits(p, kBQ, rest, cus);
-    const int kps = ((p.Lk + splits0 - 1) / splits0 + kBKV - 1) / kBKV * kBKV;
-    const int splits = (p.Lk + kps - 1) / kps;
-    if (splits >= 2) {
-      const size_t items = (size_t)rest * splits * kBQ;
+    const int64_t partial_all = (p.Lq % kBQ != 0) ? (int64_t)p.B * p.H : 0;
+    const int64_t partial = partial_all < rest ? partial_all : rest;
+    const int64_t full = rest - partial;
+    int kps = p.Lk, splits = 1, kps_p = p.Lk, splits_p = 1;
+    if (full > 0) key_ranges(p.Lk, kBKV, choose_splits(full, partial, cus), kps, splits);
+    const int64_t pieces_full = splits >= 2 ? full * splits : 0;
+    if (partial > 0) key_ranges(p.Lk, kBKV, choose_splits(partial, pieces_full, cus), kps_p, splits_p);
+    // Tail tiles: the `full` ones when they split, then the partial ones when
+    // either kind splits (a partial tile kept whole is one piece).
+    const int64_t tail_tiles = (splits >= 2 ? full : 0) + ((splits >= 2 || splits_p >= 2) ? partial : 0);
+    if (tail_tiles > 0) {
+      const int64_t pieces = pieces_full + partial * splits_p;
+      const size_t items = (size_t)pieces * kBQ;
       const size_t need = items * (kD + 2) * 4;
       float* ws;
       if (p.scratch != nullptr) {
@@ -263,17 +287,20 @@ int launch_tiles(SdpaArgs a, const SdpaParams& p, int kBQ, int kBKV, int cus, hi
         ws = static_cast<float*>(stream_workspace(stream, need, kSlotSdpaPartial));
         if (ws == nullptr) return kErrWorkspace;
       }
-      a.full_tiles = (int)(tiles - rest);
+      a.full_tiles = (int)(tiles - tail_tiles);
       a.splits = splits;
       a.keys_per_split = kps;
+      a.pieces_full = (int)pieces_full;
+      a.splits_p = splits_p;
+      a.keys_per_split_p = kps_p;
       a.part_o = ws;
       a.part_ml = ws + items * kD;
-      grid_n = a.full_tiles + rest * splits;
+      grid_n = a.full_tiles + pieces;
     }
   }
   main(dim3((unsigned)grid_n), a);
   if (hipGetLastError() != hipSuccess) return kErrLaunch;
-  if (a.splits > 1) {
+  if (a.full_tiles < tiles) {
     const int64_t rows = (tiles - a.full_tiles) * (int64_t)kBQ;
     hipLaunchKernelGGL(sdpa_combine_kernel,
                        dim3((unsigned)((rows * kD + kCombineThreads - 1) / kCombineThreads)),

@@ -4,9 +4,9 @@
 // a file-scope device array instead of the library's per-stream workspace.
 //
 // Scratch bound.  A launch splits the keys only for the partial last round
-// of query tiles: `rest` = tiles mod CUs tiles (rest < CUs) into `splits` =
-// ceil(CUs / rest) key ranges (at most 16), each writing kBQ <= 512 query
-// rows of 64 outputs + (max, sum) in fp32.  rest * splits < CUs + rest <=
+// of query tiles: its tiles (tiles mod CUs of them) become pieces of at most
+// 16 key ranges each, every piece writing kBQ <= 512 query rows of 64
+// outputs + (max, sum) in fp32, and the plan keeps all pieces within
 // 2 * CUs - 1, so on a 256-CU MI355X a plan needs at most 511 * 512 * 66 * 4
 // = 69,074,944 bytes.  The array holds 66 MiB (69,206,016 bytes): every plan
 // of a 256-CU device fits; a call whose plan needs more (a device with more
