@@ -229,13 +229,18 @@ def test_sdpa_config2_sampled_rows(oracle, cuda):
     print("config2 sampled rows", s)
 
 
-@pytest.mark.parametrize("L,packed,bias", [(18432, True, False), (16385, True, True), (8704, False, False)])
+@pytest.mark.parametrize("L,packed,bias", [(18432, True, False), (16385, True, True), (8704, False, False),
+                                            (12294, False, False), (18433, True, True)])
 def test_sdpa_tail_split_sampled_rows(oracle, cuda, L, packed, bias):
     """Tile counts that are not a multiple of the CU count (the joint
     sequence 16384 + 2048 = 18432 -> 576 tiles; the compressed negative
     branch 16385 keys with the log(M) bias -> 528; 8704 -> 272) run the
-    remainder tiles split along the keys plus a merge kernel.  Sampled rows
-    of the last head (the split tiles) and of head 0 against the oracle."""
+    remainder tiles split along the keys plus a merge kernel.  With a partial
+    query tile per head in the remainder (the reference's L = 12294: 128 full
+    tiles in 2 key ranges and 16 six-query tiles in 15; 18433: 64 full tiles
+    in 4 and 16 one-query tiles in 15) the two kinds of tile have splits of
+    their own.  Sampled rows (the last row sits in a partial tile) of the
+    last head and of head 0 against the oracle."""
     import torch
 
     print(f"sdpa tail split L={L} packed={packed} bias={bias}", flush=True)
