@@ -960,7 +960,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=("sdpa", "gemm", "copy", "flow", "skinny", "gemm16k", "refshapes"),
+    ap.add_argument("--only", choices=("sdpa", "gemm", "copy", "flow", "skinny", "gemm16k", "refshapes",
+                                       "joint_ref"),
                     default=None,
                     help="run one workload alone (for profiler runs) and print its figures")
     ap.add_argument("--no-flow", action="store_true", help="skip configs[3]/[4] (flow block / step)")
@@ -1001,6 +1002,9 @@ def main():
         return 0
     if args.only == "flow":
         print(json.dumps(run_flow(torch, dev, 3, not args.no_cpu_baseline, args.validate_flow)))
+        return 0
+    if args.only == "joint_ref":
+        print(json.dumps(run_flow_joint_reference_shapes(torch, dev, 3, not args.no_cpu_baseline)))
         return 0
 
     host = sdpa_inputs(torch, dev)
