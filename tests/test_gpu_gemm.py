@@ -262,16 +262,17 @@ def test_pointer_checks_within_one_allocation(oracle, cuda, hiplib):
                                    (2818, 256, 3072)])
 def test_gemm_tail_rows(oracle, cuda, hiplib, M, K, N):
     """M = 256 k + r with r <= 32 (e.g. the compressed negative branch, L + 1
-    tokens): 16385 x 1024 and 8194 x 3072 run the tail rows as a separate
-    32-row-tile launch (in the main grid they would add a round), 12294 x 1024
-    (the reference's sequence length) runs 12288 rows on 192 x 256 tiles --
-    one round of 256 -- and the 6-row tail as a second launch, 2818 x 3072
+    tokens): 16385 x 1024 and 8194 x 3072 run the tail rows on the few-row
+    kernels (in the main grid they would add a round), 12294 x 1024 (the
+    reference's sequence length) runs 12288 rows on 192 x 256 tiles -- one
+    round of 256 -- and the 6-row tail on the few-row kernels, 2818 x 3072
     keeps its two tail rows in its 256 x 192 grid (their tiles fit the last
-    round).  Either way rows
-    of the main part equal a GEMM over exactly those rows, and the same rows
-    of a larger M with no tail (another tile shape), and the tail rows equal
-    the same rows computed inside a 256-row tile, bit for bit; sampled rows
-    and the tail against the oracle."""
+    round).  Either way rows of the main part equal a GEMM over exactly those
+    rows, and the same rows of a larger M with no tail (another tile shape),
+    bit for bit; the tail rows equal a GEMM over exactly the tail rows bit for
+    bit (split-off tails) or the same rows inside a tile (kept tails), repeat
+    bit for bit, and lie within the summation-order bound of the same rows
+    inside a 256-row tile; sampled rows and the tail against the oracle."""
     import torch
 
     print(f"gemm tail rows M={M} K={K} N={N}", flush=True)
@@ -280,11 +281,19 @@ def test_gemm_tail_rows(oracle, cuda, hiplib, M, K, N):
     r = M % 256
     big = M - r + 256                                             # a multiple of 256: no tail split
     got = _run_async(torch, hiplib, cuda, x[:M], c01, q2, s, b)
+    again = _run_async(torch, hiplib, cuda, x[:M], c01, q2, s, b)
     head = _run_async(torch, hiplib, cuda, x[:M - r], c01, q2, s, b)
+    tail = _run_async(torch, hiplib, cuda, x[M - r:M], c01, q2, s, b)
     full = _run_async(torch, hiplib, cuda, x[:big], c01, q2, s, b)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
     assert np.array_equal(got[:M - r].view(np.uint32), head.view(np.uint32))
     assert np.array_equal(head.view(np.uint32), full[:M - r].view(np.uint32))
-    assert np.array_equal(got[M - r:].view(np.uint32), full[M - r:M].view(np.uint32))
+    split_off = (M, N) != (2818, 3072)
+    same = tail if split_off else full[M - r:M]
+    assert np.array_equal(got[M - r:].view(np.uint32), same.view(np.uint32))
+    # two fp32 evaluation orders of the same sums
+    bound = gemm_order_bound(x[M - r:M], oracle.decode_nf24(c01, q2, s), b)
+    assert np.all(np.abs(got[M - r:].astype(np.float64) - full[M - r:M]) <= bound)
     rows = np.concatenate([np.sort(np.random.default_rng(M).choice(M - r, 16, replace=False)),
                            np.arange(M - r, M)])
     _check(oracle, x[rows], c01, q2, s, b, got[rows])

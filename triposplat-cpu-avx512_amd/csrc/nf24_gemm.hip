@@ -432,6 +432,33 @@ int launch_cfg(const GemmParams& p, hipStream_t stream, const QkvArgs& e = QkvAr
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
+// Epilogue of the row-tail rows (M <= kTailRows, see tail_rows): `raw`
+// holds bias + x W of those rows ([M, n_count], from the few-row kernels);
+// each wave loads a 32 x 64 block of it into the MFMA accumulator layout and
+// runs the same epilogue code as the tile kernels (one head per wave for
+// the QKV epilogue), so the tail rows get the same elementwise arithmetic.
+template <class C, int kEpi>
+__global__ __launch_bounds__(64) void tail_epilogue_kernel(GemmArgs a, const float* raw) {
+  static_assert(C::kMB == 1 && C::kNB == 2, "one 32 x 64 block per wave");
+  const int lane = threadIdx.x;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int colw = blockIdx.x * 64;
+  floatx16 acc[1][2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int col = colw + nb * 32 + l32;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = 8 * (r / 4) + 4 * g + (r % 4);
+      acc[0][nb][r] = (row < a.M && col < a.n_count) ? raw[(int64_t)row * a.n_count + col] : 0.0f;
+    }
+  }
+  if constexpr (kEpi == kEpiQkv)
+    qkv_epilogue<C>(a, acc, 0, colw, g, l32);
+  else
+    store_result<1, 2, kEpi>(a, acc, 0, colw, g, l32);
+}
+
 // Packed k/v tokens L..Lpad-1 of every (b, h, dim) row are zero.
 constexpr int kTailThreads = 256;
 __global__ __launch_bounds__(kTailThreads) void packed_tail_zero_kernel(float* pk, float* pv,
@@ -481,10 +508,10 @@ struct ScalarPathCfg<CfgLarge> {
 };
 using CfgSkinny = GemmCfg<32, 128, 32, 1, 4>;
 using CfgTail = GemmCfg<32, 128, 32, 1, 2>;      // <= 32 rows, QKV epilogue: 64-column waves (a head)
-// <= 32 rows otherwise: each wave's cost is its chain of K/2 MFMAs per 32
-// columns (one wave per SIMD, nothing to overlap), so 32-column waves -- twice
-// the waves of 64-column ones -- finish in ~0.55x the time (e.g. one row
-// at K = 4096, N = 1024: 148 against 270 us).
+// <= 32 rows otherwise (whole calls of that size with an epilogue): each
+// wave's cost is its chain of K/2 MFMAs per 32 columns (one wave per SIMD,
+// nothing to overlap), so 32-column waves -- twice the waves of 64-column
+// ones -- finish in ~0.55x the time.
 using CfgTailNarrow = GemmCfg<32, 32, 32, 1, 1>;
 
 template <int kEpi>
@@ -550,12 +577,16 @@ int round_split_rows(int M, int n_count) {
 
 // Rows past the last multiple of 256 that number at most kTailRows, when
 // they would occupy a whole extra round of 256-row tiles (e.g. M = 16385:
-// 1040 tiles = 4 rounds + 16 one-row tiles, ~270 us at K = 1024), run as a
-// second launch of 32-row tiles instead (~30 us).  When they fit in the last
-// round the main launch already has (e.g. M = 2818, N = 3072: 12 bands of
-// 256 x 192 tiles, one round either way), they stay in it: the partial tile costs nothing there,
-// while a second launch would add its own time.  Every MFMA tile shape sums
-// each output in the same order, so the tail rows are bit-identical either way.
+// 1040 tiles = 4 rounds + 16 one-row tiles, ~270 us at K = 1024), run on the
+// few-row kernels instead (launch_tail_rows: the K range split over the
+// whole chip, partial sums merged in a fixed order).  When they fit in the
+// last round the main launch already has (e.g. M = 2818, N = 3072: 12 bands
+// of 256 x 192 tiles, one round either way), they stay in it: the partial
+// tile costs nothing there, while a second launch would add its own time.
+// The tile shapes all sum each output in one order; the few-row kernels sum
+// in another (deterministic) one, so a tail row equals the same row of a
+// call over exactly the tail rows, bit for bit, and a row inside a tile to
+// within the fp32 summation-order bound.
 constexpr int kTailRows = 32;
 
 GemmParams rows_slice(const GemmParams& p, int first, int count) {
@@ -610,7 +641,7 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
   }
   if (const int rem = tail_rows(p.M, p.n_count)) {
     const int st = launch_nf24_gemm(rows_slice(p, 0, p.M - rem), stream);
-    return st != kOk ? st : launch_cfg<CfgTailNarrow>(rows_slice(p, p.M - rem, rem), stream);
+    return st != kOk ? st : launch_nf24_gemv(rows_slice(p, p.M - rem, rem), stream);
   }
   if (const int m1 = round_split_rows(p.M, p.n_count)) {
     const int st = launch_nf24_gemm(rows_slice(p, 0, m1), stream);
@@ -624,6 +655,28 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
 }
 
 namespace {
+// The row tail t (at most kTailRows rows, token index of its row 0 row0) of
+// an epilogue GEMM: bias + x W of its rows by the few-row kernels into the
+// per-stream workspace, then tail_epilogue_kernel.
+template <int kEpi>
+int launch_tail_rows(const GemmParams& t, const GemmEpilogueParams& e, const QkvArgs& q, int row0,
+                     hipStream_t stream) {
+  float* raw = static_cast<float*>(
+      stream_workspace(stream, (size_t)t.M * t.n_count * sizeof(float), kSlotGemmTail));
+  if (raw == nullptr) return kErrWorkspace;
+  GemmParams r = t;
+  r.out = raw;
+  r.stride_out = t.n_count;
+  const int st = launch_nf24_gemv(r, stream);
+  if (st != kOk) return st;
+  GemmArgs a{t.x, t.code01, t.q2, t.scale, t.bias, t.out,
+             t.M, t.K, t.N, t.n_start, t.n_count, t.stride_x, t.stride_out, q,
+             e.gate, e.gate_stride, e.rows_per_batch, row0, 0, 0};
+  hipLaunchKernelGGL((tail_epilogue_kernel<CfgTail, kEpi>), dim3((unsigned)((t.n_count + 63) / 64)),
+                     dim3(64), 0, stream, a, raw);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
 template <int kEpi>
 int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_t stream,
                     const QkvArgs& q = QkvArgs{}, int row0 = 0) {
@@ -631,8 +684,8 @@ int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_
   if (const int rem = tail_rows(p.M, p.n_count)) {
     const int st = launch_epi_kind<kEpi>(rows_slice(p, 0, p.M - rem), e, stream, q, row0);
     return st != kOk ? st
-                     : launch_cfg<TailCfg<kEpi>, kEpi>(rows_slice(p, p.M - rem, rem), stream, q, e,
-                                                 row0 + p.M - rem);
+                     : launch_tail_rows<kEpi>(rows_slice(p, p.M - rem, rem), e, q, row0 + p.M - rem,
+                                              stream);
   }
   // Few rows: the 32-row tile (the epilogues live in the MFMA kernels).
   if (p.M <= 32) return launch_cfg<TailCfg<kEpi>, kEpi>(p, stream, q, e, row0);

@@ -34,7 +34,8 @@ struct HipOps {
 };
 
 using Pool = WorkspacePool<hipStream_t, HipOps>;
-static_assert(kSlotSdpaPartial < Pool::kSlots, "workspace slot out of range");
+static_assert(kSlotSdpaPartial < Pool::kSlots && kSlotGemmTail < Pool::kSlots,
+              "workspace slot out of range");
 
 std::mutex g_mu;
 // Never destroyed: retired buffers stay valid for graphs until the process
