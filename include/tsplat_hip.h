@@ -107,7 +107,15 @@ int triposplat_sdpa_f32_avx512_exact_q8t512_packed_blhd(
 /* q8t512.c:51-100 and packed.c:160-162 metadata/profile probes.  Key tile
  * and query block report this library's tiles (64 keys, 128 queries).
  * Profile: calls and wall time of the blocking calls (allocate/pack/free
- * report 0: there is no per-call workspace or pack step). */
+ * report 0: there is no per-call workspace or pack step).
+ * Workspace: the SDPA's key-split partials live in grow-only device buffers,
+ * one per (device, stream); stats report their allocations and bytes.
+ * Release frees, after its stream, the buffer of every stream on the current
+ * device that is idle, and keeps (until the process ends) the buffers a HIP
+ * graph captured, those of a stream under capture at that moment (waiting on
+ * it would end the capture) and those of streams already destroyed (they
+ * cannot be waited on): a stream's buffer is reclaimed only by a release
+ * made before the stream is destroyed. */
 int triposplat_sdpa_key_tile(void);
 int triposplat_sdpa_query_block(void);
 int triposplat_sdpa_packed_output_is_blhd(void);
@@ -147,7 +155,11 @@ int tsplat_sdpa_precision_async(const float* q, const float* k, const float* v,
  * plan of a 256-CU device; a call that would need more returns -8 before any
  * launch.  The array is per GPU and shared by all calls on it, whatever the
  * stream: calls that overlap in time on one GPU race and must be ordered by
- * the caller. */
+ * the caller.  The array is part of the library's code object: every process
+ * that loads the library holds 66 MiB of device memory on each GPU it uses,
+ * whether or not it calls this entry.  The array's device address is looked
+ * up on the first call on each device; that call may itself be under graph
+ * capture. */
 int tsplat_sdpa_noalloc_async(const float* q, const float* k, const float* v,
                               const float* key_bias_or_null, float* out, int B, int H, int Lq,
                               int Lk, int D, int has_key_bias, int key_bias_len,

@@ -46,6 +46,19 @@ def test_every_declared_symbol_is_exported(lib):
     assert set(SIGNATURES) == set(declared)
 
 
+def test_loader_checks_abi_version(lib, monkeypatch):
+    """The bindings' argument lists are those of ABI_VERSION; a library that
+    reports another version is refused at load time, not called with shifted
+    arguments."""
+    from tsplat import _lib
+
+    assert lib.tsplat_abi_version() == _lib.ABI_VERSION
+    monkeypatch.setattr(_lib, "ABI_VERSION", _lib.ABI_VERSION - 1)
+    monkeypatch.setattr(_lib, "_CACHE", {})
+    with pytest.raises(RuntimeError, match="ABI version"):
+        _lib.load_library()
+
+
 def test_query_symbols(lib):
     assert lib.triposplat_gemm_rnf8_avx512_residual_mode() == 4
     assert lib.triposplat_gemm_nf24_qkv_direct_residual_mode() == 4

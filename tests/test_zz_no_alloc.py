@@ -27,12 +27,23 @@ def _inputs(torch, cuda, seed, H, Lq, Lk, bias):
     return q, k, v, b
 
 
-def _call(lib, fn, torch, cuda, q, k, v, b, out, precision, blhd):
+def _packed(torch, t):
+    """[1, H, Lk, 64] -> key-contiguous [1, H, 64, Lkp], Lkp = roundup16(Lk), tail keys zero."""
+    _, H, Lk, _ = t.shape
+    Lkp = -(-Lk // 16) * 16
+    p = torch.zeros((1, H, 64, Lkp), device=t.device)
+    p[..., :Lk] = t.transpose(2, 3)
+    return p
+
+
+def _call(lib, fn, torch, cuda, q, k, v, b, out, precision, blhd, Lk_packed=0):
+    """Lk_packed > 0: k and v are key-contiguous [1, H, 64, Lkp] of Lk_packed keys."""
     _, H, Lq, _ = q.shape
-    Lk = k.shape[2]
+    Lk = Lk_packed if Lk_packed else k.shape[2]
+    Lkp = k.shape[3] if Lk_packed else 0
     return getattr(lib, fn)(q.data_ptr(), k.data_ptr(), v.data_ptr(), None if b is None else b.data_ptr(),
                             out.data_ptr(), 1, H, Lq, Lk, 64, int(b is not None), Lk if b is not None else 0,
-                            Lk if b is not None else 0, 0, 0, int(blhd), precision,
+                            Lk if b is not None else 0, int(bool(Lk_packed)), Lkp, int(blhd), precision,
                             torch.cuda.current_stream(cuda).cuda_stream)
 
 
@@ -42,12 +53,15 @@ def _allocations(lib):
     return vals[0].value
 
 
-# (H, Lq, Lk, bias, precision, blhd): the first two of each pair need the
-# key split (16 heads x 17 tiles of 512 queries on 256 CUs), the second
-# smaller than the first
+# (H, Lq, Lk, bias, precision, blhd, packed k/v): the first of each pair
+# needs the key split (16 heads x 17 tiles of 512 queries on 256 CUs), the
+# second is smaller than the first; every precision (0 fp32, 1 bf16,
+# 2 bf16x3) and both K/V layouts
 CALLS = [
-    [(16, 8704, 1024, True, 0, True), (16, 8292, 512, False, 0, False)],
-    [(16, 8704, 1024, False, 2, False), (16, 8500, 320, True, 2, True)],
+    [(16, 8704, 1024, True, 0, True, False), (16, 8292, 512, False, 0, False, False)],
+    [(16, 8704, 1024, False, 2, False, False), (16, 8500, 320, True, 2, True, False)],
+    [(16, 8704, 1024, False, 1, True, True), (16, 8292, 520, True, 1, False, True)],
+    [(16, 8704, 1000, True, 0, False, True), (16, 8500, 700, False, 2, True, True)],
 ]
 
 
@@ -60,20 +74,24 @@ def test_noalloc_matches_precision_entry(cuda, hiplib, pair):
         pytest.skip(f"the split shapes assume 256 CUs, the device has {props.multi_processor_count}")
     before = _allocations(hiplib)
     got_all, want_all = [], []
-    for i, (H, Lq, Lk, bias, precision, blhd) in enumerate(CALLS[pair]):
+    for i, (H, Lq, Lk, bias, precision, blhd, packed) in enumerate(CALLS[pair]):
         print(f"noalloc pair {pair} call {i}: H={H} Lq={Lq} Lk={Lk} bias={bias} precision={precision} "
-              f"blhd={blhd}", flush=True)
+              f"blhd={blhd} packed={packed}", flush=True)
         q, k, v, b = _inputs(torch, cuda, 100 * pair + i, H, Lq, Lk, bias)
+        if packed:
+            k, v = _packed(torch, k), _packed(torch, v)
         shape = (1, Lq, H, 64) if blhd else (1, H, Lq, 64)
         got = torch.full(shape, float("nan"), device=cuda)
-        assert _call(hiplib, "tsplat_sdpa_noalloc_async", torch, cuda, q, k, v, b, got, precision, blhd) == 0
+        assert _call(hiplib, "tsplat_sdpa_noalloc_async", torch, cuda, q, k, v, b, got, precision, blhd,
+                     Lk if packed else 0) == 0
         torch.cuda.synchronize(cuda)
         got_all.append(got)
-        want_all.append((q, k, v, b, shape, precision, blhd))
+        want_all.append((q, k, v, b, shape, precision, blhd, Lk if packed else 0))
     assert _allocations(hiplib) == before          # no workspace allocation
-    for got, (q, k, v, b, shape, precision, blhd) in zip(got_all, want_all):
+    for got, (q, k, v, b, shape, precision, blhd, lkp) in zip(got_all, want_all):
         want = torch.full(shape, float("nan"), device=cuda)
-        assert _call(hiplib, "tsplat_sdpa_precision_async", torch, cuda, q, k, v, b, want, precision, blhd) == 0
+        assert _call(hiplib, "tsplat_sdpa_precision_async", torch, cuda, q, k, v, b, want, precision, blhd,
+                     lkp) == 0
         torch.cuda.synchronize(cuda)
         assert bool(torch.isfinite(got).all())
         assert torch.equal(got, want)
@@ -115,6 +133,64 @@ def test_noalloc_captured_without_warmup(cuda, hiplib):
         assert _call(hiplib, "tsplat_sdpa_noalloc_async", torch, cuda, *other, other_out, 0, False) == 0
         torch.cuda.synchronize(cuda)
     assert _allocations(hiplib) == before
+
+
+_FIRST_CALL_CAPTURED = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+import torch
+dev = torch.device("cuda", 0)
+torch.cuda.set_device(dev)
+g = torch.Generator(device=dev).manual_seed(5)
+q = torch.nn.functional.normalize(torch.randn((1, 16, 8704, 64), generator=g, device=dev), dim=-1) * 8
+k = torch.nn.functional.normalize(torch.randn((1, 16, 1024, 64), generator=g, device=dev), dim=-1) * 8
+v = torch.randn((1, 16, 1024, 64), generator=g, device=dev)
+out = torch.full_like(q, float("nan"))
+want = torch.full_like(q, float("nan"))
+s = torch.cuda.Stream(device=dev)
+torch.cuda.synchronize(dev)
+from tsplat import load_library
+lib = load_library()
+def call(fn, o, stream):
+    return getattr(lib, fn)(q.data_ptr(), k.data_ptr(), v.data_ptr(), None, o.data_ptr(), 1, 16, 8704, 1024,
+                            64, 0, 0, 0, 0, 0, 0, 0, stream)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=s):
+    st = call("tsplat_sdpa_noalloc_async", out, s.cuda_stream)
+print("captured status", st, flush=True)
+assert st == 0, st
+for _ in range(2):
+    out.fill_(float("nan"))
+    graph.replay()
+    torch.cuda.synchronize(dev)
+    assert bool(torch.isfinite(out).all())
+assert call("tsplat_sdpa_precision_async", want, torch.cuda.current_stream(dev).cuda_stream) == 0
+torch.cuda.synchronize(dev)
+assert torch.equal(out, want)
+print("first call captured: ok", flush=True)
+"""
+
+
+def test_noalloc_first_library_call_captured(cuda):
+    """A fresh process whose first call into the library is a captured
+    no-allocation SDPA (so the per-device scratch address is looked up
+    inside the capture, with global capture mode), replayed twice: the
+    capture succeeds and every replay equals the eager result bit for bit."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    import torch
+
+    props = torch.cuda.get_device_properties(cuda)
+    if props.multi_processor_count != 256:
+        pytest.skip(f"the split shape assumes 256 CUs, the device has {props.multi_processor_count}")
+    pkg = Path(__file__).resolve().parents[1] / "triposplat-cpu-avx512_amd"
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED, str(pkg)], capture_output=True, text=True,
+                       timeout=100)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0
+    assert "first call captured: ok" in r.stdout
 
 
 def test_noalloc_argument_errors(cuda, hiplib):

@@ -19,30 +19,51 @@ struct Log {
   int next = 1;
   bool fail_sync = false;
   bool fail_alloc = false;
+  bool fail_free = false;
+  bool pending_error = false;  // what a failed runtime call leaves behind
+  std::set<int> capturing, gone;
   uint64_t clock = 0;
 };
 
 struct FakeOps {
   Log* log;
   void* alloc(size_t bytes) {
-    if (log->fail_alloc) return nullptr;
+    if (log->fail_alloc) {
+      log->pending_error = true;
+      return nullptr;
+    }
     void* p = reinterpret_cast<void*>((uintptr_t)(log->next++) << 32);
     log->live.insert(p);
     log->events.push_back("alloc " + std::to_string(bytes));
     return p;
   }
-  void free(void* p) {
+  bool free(void* p) {
     if (!log->live.count(p)) {
       std::printf("FAIL: free of a pointer that is not live\n");
       std::exit(1);
     }
+    if (log->fail_free) {
+      log->pending_error = true;
+      return false;
+    }
     log->live.erase(p);
     log->events.push_back("free");
+    return true;
   }
   bool sync(int stream) {
+    if (log->capturing.count(stream) || log->gone.count(stream)) {
+      std::printf("FAIL: wait on a stream that is capturing or gone\n");
+      std::exit(1);
+    }
     log->events.push_back("sync " + std::to_string(stream));
+    if (log->fail_sync) log->pending_error = true;
     return !log->fail_sync;
   }
+  tsplat::StreamState state(int stream) {
+    if (log->gone.count(stream)) return tsplat::StreamState::kGone;
+    return log->capturing.count(stream) ? tsplat::StreamState::kCapturing : tsplat::StreamState::kIdle;
+  }
+  void clear_error() { log->pending_error = false; }
   uint64_t now_ns() { return log->clock += 10; }
 };
 
@@ -149,12 +170,38 @@ int main() {
     log.fail_sync = true;
     check(pool.acquire(0, 1, 0, 2 * kMin, false) == nullptr, "failed stream wait fails the request");
     check(log.live.count(a) == 1 && log.live.size() == 1, "old kept, the fresh buffer freed");
+    check(!log.pending_error, "a failed stream wait leaves no runtime error for the next launch check");
     log.fail_sync = false;
     log.fail_alloc = true;
     check(pool.acquire(0, 1, 0, 2 * kMin, false) == nullptr, "failed alloc fails the request");
     check(log.live.count(a) == 1, "old kept after a failed alloc");
+    check(!log.pending_error, "a failed alloc leaves no runtime error");
     log.fail_alloc = false;
     check(pool.acquire(0, 1, 0, kMin, false) == a, "the old buffer still serves fitting requests");
+    log.fail_free = true;
+    void* b = pool.acquire(0, 1, 0, 2 * kMin, false);
+    check(b != nullptr && b != a, "growth succeeds when the old buffer's free fails");
+    check(!log.pending_error, "a failed free leaves no runtime error");
+    log.fail_free = false;
+  }
+
+  {  // release never waits on a stream under capture or one that is gone
+    Log log;
+    Pool pool(FakeOps{&log});
+    void* idle = pool.acquire(0, 1, 1, kMin, false);
+    void* cap = pool.acquire(0, 2, 1, kMin, false);
+    void* gone = pool.acquire(0, 3, 1, kMin, false);
+    log.capturing.insert(2);
+    log.gone.insert(3);
+    pool.release(0, 1);
+    check(!log.live.count(idle), "idle stream: buffer freed after its stream");
+    check(log.live.count(cap) && log.live.count(gone), "capturing / gone streams: buffers kept");
+    check(pool.retired().size() == 2, "both retired");
+    check(pool.stats(1).live_bytes == 0 && pool.stats(1).retired_bytes == 2 * kMin,
+          "retired bytes accounted");
+    log.capturing.clear();
+    void* again = pool.acquire(0, 2, 1, kMin, false);
+    check(again != nullptr && again != cap, "the stream gets a fresh buffer after release");
   }
 
   if (failures == 0) std::printf("ok\n");

@@ -4,6 +4,7 @@
 // that splits the last, partial round of query tiles along the keys.
 #pragma once
 
+#include "sdpa_plan.h"
 #include "tsplat_common.h"
 #include "tsplat_launch.h"
 
@@ -220,34 +221,6 @@ __global__ __launch_bounds__(kCombineThreads) void sdpa_combine_kernel(SdpaArgs 
   dst[d] = o * (1.0f / l);
 }
 
-// Key ranges for the tiles of a partial last round.  Modelled in units of
-// one full tile over all keys: `full` full tiles split s ways make
-// ceil(full * s / cus) rounds of 1/s each, plus a fixed cost per piece (its
-// prologue, Q load and partial store) of 2 % of a tile.  The `partial` query
-// tiles (numbered last, see tile_coords; their few live waves still stream
-// every key tile, at a few us each) take the slots left after the full
-// tiles' pieces and are split by the same model into s_p ranges of their
-// own.  All pieces together stay within 2 * cus - 1, so the partials need
-// at most (2 * cus - 1) * kBQ rows of workspace; s, s_p <= 16.
-inline int choose_splits(int64_t full, int64_t reserve, int cus) {
-  int best = 1;
-  double best_t = 1e30;
-  for (int s = 1; s <= 16 && full * s + reserve <= 2 * (int64_t)cus - 1; ++s) {
-    const double t = (double)((full * s + cus - 1) / cus) * (1.0 / s + 0.02);
-    if (t < best_t - 1e-9) {
-      best_t = t;
-      best = s;
-    }
-  }
-  return best;
-}
-
-// Keys per range (a multiple of the key tile) and the resulting range count.
-inline void key_ranges(int Lk, int kBKV, int s0, int& kps, int& splits) {
-  kps = ((Lk + s0 - 1) / s0 + kBKV - 1) / kBKV * kBKV;
-  splits = (Lk + kps - 1) / kps;
-}
-
 // Launches `main(grid, args)` over the query tiles of kBQ queries.  A last
 // round that would leave CUs idle (tiles % CUs workgroups of a
 // one-workgroup-per-CU shape) is split along the keys instead, so that the
@@ -256,52 +229,32 @@ inline void key_ranges(int Lk, int kBKV, int s0, int& kps, int& splits) {
 template <class Main>
 int launch_tiles(SdpaArgs a, const SdpaParams& p, int kBQ, int kBKV, int cus, hipStream_t stream,
                  Main&& main) {
-  const int64_t tiles = (int64_t)p.B * p.H * ((p.Lq + kBQ - 1) / kBQ);
-  if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
+  TilePlan pl;
+  if (!plan_tiles(p.B, p.H, p.Lq, p.Lk, kBQ, kBKV, kD, cus, pl)) return kErrDims;
   note_sdpa_query_tile(kBQ);
-  int64_t grid_n = tiles;
-  a.full_tiles = (int)tiles;
-  a.splits = 1;
-  a.keys_per_split = p.Lk;
-  const int64_t rest = cus > 0 ? tiles % cus : 0;
-  if (cus > 0 && tiles >= cus && rest != 0) {
-    const int64_t partial_all = (p.Lq % kBQ != 0) ? (int64_t)p.B * p.H : 0;
-    const int64_t partial = partial_all < rest ? partial_all : rest;
-    const int64_t full = rest - partial;
-    int kps = p.Lk, splits = 1, kps_p = p.Lk, splits_p = 1;
-    if (full > 0) key_ranges(p.Lk, kBKV, choose_splits(full, partial, cus), kps, splits);
-    const int64_t pieces_full = splits >= 2 ? full * splits : 0;
-    if (partial > 0) key_ranges(p.Lk, kBKV, choose_splits(partial, pieces_full, cus), kps_p, splits_p);
-    // Tail tiles: the `full` ones when they split, then the partial ones when
-    // either kind splits (a partial tile kept whole is one piece).
-    const int64_t tail_tiles = (splits >= 2 ? full : 0) + ((splits >= 2 || splits_p >= 2) ? partial : 0);
-    if (tail_tiles > 0) {
-      const int64_t pieces = pieces_full + partial * splits_p;
-      const size_t items = (size_t)pieces * kBQ;
-      const size_t need = items * (kD + 2) * 4;
-      float* ws;
-      if (p.scratch != nullptr) {
-        if (need > p.scratch_bytes) return kErrScratch;
-        ws = p.scratch;
-      } else {
-        ws = static_cast<float*>(stream_workspace(stream, need, kSlotSdpaPartial));
-        if (ws == nullptr) return kErrWorkspace;
-      }
-      a.full_tiles = (int)(tiles - tail_tiles);
-      a.splits = splits;
-      a.keys_per_split = kps;
-      a.pieces_full = (int)pieces_full;
-      a.splits_p = splits_p;
-      a.keys_per_split_p = kps_p;
-      a.part_o = ws;
-      a.part_ml = ws + items * kD;
-      grid_n = a.full_tiles + pieces;
+  a.full_tiles = (int)pl.full_tiles;
+  a.splits = pl.splits;
+  a.keys_per_split = pl.keys_per_split;
+  a.pieces_full = (int)pl.pieces_full;
+  a.splits_p = pl.splits_p;
+  a.keys_per_split_p = pl.keys_per_split_p;
+  if (pl.pieces > 0) {
+    float* ws;
+    if (p.scratch != nullptr) {
+      if (!scratch_fits(pl, p.scratch_bytes)) return kErrScratch;
+      ws = p.scratch;
+    } else {
+      ws = static_cast<float*>(stream_workspace(stream, pl.scratch_bytes, kSlotSdpaPartial));
+      if (ws == nullptr) return kErrWorkspace;
     }
+    a.part_o = ws;
+    a.part_ml = ws + (size_t)pl.pieces * kBQ * kD;
   }
+  const int64_t grid_n = pl.grid();
   main(dim3((unsigned)grid_n), a);
   if (hipGetLastError() != hipSuccess) return kErrLaunch;
-  if (a.full_tiles < tiles) {
-    const int64_t rows = (tiles - a.full_tiles) * (int64_t)kBQ;
+  if (pl.full_tiles < pl.tiles) {
+    const int64_t rows = (pl.tiles - pl.full_tiles) * (int64_t)kBQ;
     hipLaunchKernelGGL(sdpa_combine_kernel,
                        dim3((unsigned)((rows * kD + kCombineThreads - 1) / kCombineThreads)),
                        dim3(kCombineThreads), 0, stream, a, kBQ, rows);

@@ -15,17 +15,24 @@
 namespace tsplat {
 namespace {
 
+// The pool clears the error a failed call leaves (clear_error), so the
+// caller's next hipGetLastError() check sees only its own launch.
 struct HipOps {
   void* alloc(size_t bytes) {
     void* p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess) {
-      (void)hipGetLastError();
-      return nullptr;
-    }
-    return p;
+    return hipMalloc(&p, bytes) == hipSuccess ? p : nullptr;
   }
-  void free(void* p) { (void)hipFree(p); }
+  bool free(void* p) { return hipFree(p) == hipSuccess; }
   bool sync(hipStream_t s) { return hipStreamSynchronize(s) == hipSuccess; }
+  void clear_error() { (void)hipGetLastError(); }
+  StreamState state(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+      (void)hipGetLastError();
+      return StreamState::kGone;
+    }
+    return st == hipStreamCaptureStatusNone ? StreamState::kIdle : StreamState::kCapturing;
+  }
   uint64_t now_ns() {
     return (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
                std::chrono::steady_clock::now().time_since_epoch())
@@ -51,7 +58,10 @@ Pool& pool() {
 
 void* stream_workspace(hipStream_t stream, size_t bytes, int slot) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
     (void)hipGetLastError();
@@ -63,7 +73,10 @@ void* stream_workspace(hipStream_t stream, size_t bytes, int slot) {
 
 void release_workspace(int slot) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return;
+  }
   std::lock_guard<std::mutex> lock(g_mu);
   pool().release(dev, slot);
 }

@@ -15,11 +15,19 @@
 //     after the stream has finished with it -- unless a capture recorded it:
 //     then it is retired (kept allocated until the process ends), because a
 //     graph replayed later still writes to it.
-//   - release() frees every uncaptured buffer of a slot on the current
-//     device and retires the captured ones.
+//   - release() frees, after its stream, every buffer of a slot on the
+//     current device whose stream is idle (not under capture), and retires
+//     the others: buffers a capture recorded, buffers of a stream under
+//     capture right now (waiting on such a stream would end its capture),
+//     and buffers of a stream that no longer exists (it cannot be waited
+//     on).  A destroyed stream's buffer is therefore reclaimed only by a
+//     release() made before the stream is destroyed.
 // Calls on one stream are ordered by the stream and share its buffer; a
 // graph must be replayed on the stream it was captured on (or ordered with
-// that stream's eager work), since both use the same buffer.
+// that stream's eager work), since both use the same buffer.  Streams are
+// keyed by handle: a new stream that reuses a destroyed stream's handle
+// value takes over its buffers, which is safe because the runtime releases
+// a stream's handle only once the work queued on it has finished.
 #pragma once
 
 #include <stddef.h>
@@ -45,8 +53,15 @@ struct WorkspaceSlotStats {
   uint64_t free_ns = 0;         // host time waiting for streams and in free
 };
 
-// Ops: void* alloc(size_t); void free(void*); bool sync(Stream);
-//      uint64_t now_ns();
+// What a stream is doing when release() looks at it.
+enum class StreamState { kIdle, kCapturing, kGone };
+
+// Ops: void* alloc(size_t); bool free(void*); bool sync(Stream);
+//      StreamState state(Stream); void clear_error(); uint64_t now_ns();
+// alloc / free / sync report failure by null / false and may leave a
+// runtime error pending; the pool clears it (clear_error) right away, so a
+// caller that checks the runtime's last error after its own launch sees only
+// that launch's.  Stream must be ordered (operator<): it is part of the map key.
 template <class Stream, class Ops>
 class WorkspacePool {
  public:
@@ -74,9 +89,12 @@ class WorkspacePool {
     const uint64_t t0 = ops_.now_ns();
     void* fresh = ops_.alloc(want);
     stats_[slot].alloc_ns += ops_.now_ns() - t0;
-    if (fresh == nullptr) return nullptr;
+    if (fresh == nullptr) {
+      ops_.clear_error();
+      return nullptr;
+    }
     if (b.ptr != nullptr && !drop(b, stream, slot)) {
-      ops_.free(fresh);
+      if (!ops_.free(fresh)) ops_.clear_error();
       return nullptr;
     }
     b.ptr = fresh;
@@ -87,13 +105,22 @@ class WorkspacePool {
     return fresh;
   }
 
-  // Frees (after its stream) or retires every buffer of `slot` on `device`.
+  // Frees (after its stream) or retires every buffer of `slot` on `device`;
+  // buffers of streams that are capturing or gone are retired, never waited on.
   void release(int device, int slot) {
     if (slot < 0 || slot >= kSlots) return;
-    for (auto& kv : buffers_) {
-      if (std::get<0>(kv.first) != device || std::get<2>(kv.first) != slot) continue;
-      WorkspaceBuffer& b = kv.second;
-      if (b.ptr != nullptr && drop(b, std::get<1>(kv.first), slot)) b = WorkspaceBuffer{};
+    for (auto it = buffers_.begin(); it != buffers_.end();) {
+      if (std::get<0>(it->first) != device || std::get<2>(it->first) != slot) {
+        ++it;
+        continue;
+      }
+      WorkspaceBuffer& b = it->second;
+      const Stream stream = std::get<1>(it->first);
+      if (b.ptr != nullptr && !b.captured && ops_.state(stream) != StreamState::kIdle) b.captured = true;
+      if (b.ptr == nullptr || drop(b, stream, slot))
+        it = buffers_.erase(it);
+      else
+        ++it;
     }
   }
 
@@ -112,9 +139,12 @@ class WorkspacePool {
     } else {
       const uint64_t t0 = ops_.now_ns();
       const bool ok = ops_.sync(stream);
-      if (ok) ops_.free(b.ptr);
+      if (ok && !ops_.free(b.ptr)) ops_.clear_error();
       stats_[slot].free_ns += ops_.now_ns() - t0;
-      if (!ok) return false;
+      if (!ok) {
+        ops_.clear_error();
+        return false;
+      }
     }
     stats_[slot].live_bytes -= b.bytes;
     b.ptr = nullptr;

@@ -96,6 +96,12 @@ STATUS_TEXT = {
     -8: "needs more scratch than the no-allocation entry point's static buffer",
 }
 
+# tsplat_abi_version() of the library these bindings describe: an entry's
+# argument list changed whenever it moved (ABI 3 put kv_round before the
+# stream argument of the asynchronous QKV entries), so a library reporting
+# another version would read its arguments shifted.
+ABI_VERSION = 3
+
 _CACHE: dict[str, ctypes.CDLL] = {}
 
 
@@ -125,6 +131,12 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = argtypes
         fn.restype = restype
+    found = lib.tsplat_abi_version()
+    if found != ABI_VERSION:
+        raise RuntimeError(
+            f"{resolved} reports ABI version {found}, these bindings expect {ABI_VERSION}; "
+            "rebuild it with `make -C triposplat-cpu-avx512_amd`"
+        )
     _CACHE[key] = lib
     return lib
 
