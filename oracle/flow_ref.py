@@ -31,6 +31,9 @@ class CpuFlow:
         self.backend = backend
         self.threads = threads
         self.progress = None  # optional callable(block index) after each block
+        # optional callable(i, x): the hidden state entering block i, and
+        # (len(blocks), x) the state the final layer receives
+        self.observe = None
         if backend == "reference" and not O.ref_available():
             raise RuntimeError("oracle/_ref not built")
 
@@ -160,36 +163,96 @@ class CpuFlow:
         t_emb, t_mod = self.timestep(t)
         x = self.linear(z.reshape(B * L, C), self.p["input_layer"]).reshape(B, L, C)
         for i, bp in enumerate(self.p["blocks"]):
+            if self.observe is not None:
+                self.observe(i, x)
             x = self.block(bp, x, cond, t_mod)
             if self.progress is not None:
                 self.progress(i)
+        if self.observe is not None:
+            self.observe(len(self.p["blocks"]), x)
+        return self.final_layer(x, t_emb)
+
+    def final_layer(self, x, t_emb):
+        """Final LayerNorm, modulation by (shift table + t_emb), output Linear:
+        the hidden state after the last block [B, L, C] -> velocity."""
+        B, L, C = x.shape
         fs = (self.p["final_shift_table"][None] + t_emb[:, None, :]).astype(np.float32)
         shift, scale = np.ascontiguousarray(fs[:, 0]), np.ascontiguousarray(fs[:, 1])
         h = self._modulate(self._ln(x, self.cfg.final_ln_eps), scale, shift)
         return self.linear(h.reshape(B * L, C), self.p["out_layer"]).reshape(B, L, C)
 
     def schedule(self):
+        """t_i = s u / (1 + (s - 1) u), u = linspace(1, 0, steps + 1) in float64
+        (scripts/triposplat_quantized_sampler.py:398-400)."""
         s = self.cfg.shift
         u = np.linspace(1.0, 0.0, self.cfg.steps + 1, dtype=np.float64)
         return s * u / (1.0 + (s - 1.0) * u)
 
-    def euler_cfg_step(self, z, cond, step=0):
+    def step_times(self, step=0):
+        """(t * 1000, dt) of a step as the sampler passes them: float32 of the
+        float64 schedule values (sampler.py:413-414)."""
         ts = self.schedule()
-        t = np.full(2, ts[step] * 1000.0, np.float32)
-        dt = np.float32(ts[step] - ts[step + 1])
-        v = self.velocity(np.stack((z, z)), np.stack((cond, np.zeros_like(cond))), t)
-        v_cfg = np.ascontiguousarray(v[0])
-        self._ew("cfg_combine_inplace", v_cfg, np.ascontiguousarray(v[1]),
+        return np.float32(ts[step] * 1000.0), np.float32(ts[step] - ts[step + 1])
+
+    def cfg_euler(self, v_pos, v_neg, z, dt):
+        """v = g v_c - (g - 1) v_u, z - dt v (native_sampler_avx512.c:41-49,
+        78-84): (z_next, v_cfg)."""
+        v_cfg = np.array(v_pos, np.float32, copy=True)
+        self._ew("cfg_combine_inplace", v_cfg, np.ascontiguousarray(v_neg, np.float32),
                  np.array([self.cfg.guidance], np.float32), 1, v_cfg.size)
         z_next = np.array(z, np.float32, copy=True)
         self._ew("euler_update_inplace", z_next, v_cfg, np.array([dt], np.float32), 1, z_next.size)
         return z_next, v_cfg
+
+    def euler_cfg_step(self, z, cond, step=0):
+        t1000, dt = self.step_times(step)
+        t = np.full(2, t1000, np.float32)
+        v = self.velocity(np.stack((z, z)), np.stack((cond, np.zeros_like(cond))), t)
+        return self.cfg_euler(v[0], v[1], z, dt)
 
 
 def combined_rmse(a, b):
     """RMSE as scripts/compare_latent_npz.py:22-48 reports it (float64)."""
     d = np.asarray(a, np.float64) - np.asarray(b, np.float64)
     return float(np.sqrt(np.mean(d * d)))
+
+
+def latent_stats(ref, cand):
+    """The per-key statistics of scripts/compare_latent_npz.py:22-48 (float64):
+    RMSE, MAE, max-abs, mean relative error against max(|ref|, 1e-8), the
+    50/95/99th percentiles of |diff|, and the finite / NaN / +Inf / -Inf counts
+    of the difference."""
+    ref = np.asarray(ref, np.float64)
+    d = np.asarray(cand, np.float64) - ref
+    ad = np.abs(d)
+    mse = float(np.mean(d * d))
+    return {
+        "mse": mse,
+        "rmse": float(np.sqrt(mse)),
+        "mae": float(np.mean(ad)),
+        "max_abs": float(np.max(ad)),
+        "mean_relative_abs": float(np.mean(ad / np.maximum(np.abs(ref), 1e-8))),
+        "p50_abs": float(np.percentile(ad, 50)),
+        "p95_abs": float(np.percentile(ad, 95)),
+        "p99_abs": float(np.percentile(ad, 99)),
+        "finite_count": int(np.isfinite(d).sum()),
+        "nan_count": int(np.isnan(d).sum()),
+        "posinf_count": int(np.isposinf(d).sum()),
+        "neginf_count": int(np.isneginf(d).sum()),
+    }
+
+
+def combined_rmse_from_key_mse(per_key):
+    """sqrt of the mean of the per-key MSEs (compare_latent_npz.py:67-71):
+    the score that combines e.g. the latent and the camera keys."""
+    mses = [v["mse"] for v in per_key.values()]
+    return float(np.sqrt(np.mean(mses)))
+
+
+def non_finite(stats):
+    """NaN + Inf count of a latent_stats() record (the reference's promotion
+    gates require 0 beside the RMSE)."""
+    return stats["nan_count"] + stats["posinf_count"] + stats["neginf_count"]
 
 
 class CpuJointFlow(CpuFlow):
@@ -243,9 +306,8 @@ class CpuJointFlow(CpuFlow):
 
     def joint_euler_cfg_step(self, z, cond, cam, step=0):
         """(z_next, v_cfg, cam_next, v_cam_cfg) of one CFG Euler step."""
-        ts = self.schedule()
-        t = np.full(1, ts[step] * 1000.0, np.float32)
-        dt = np.float32(ts[step] - ts[step + 1])
+        t1000, dt = self.step_times(step)
+        t = np.full(1, t1000, np.float32)
         v_pos, vc_pos = self.joint_velocity(z, cond, cam, t)
         v_neg, vc_neg = self.joint_velocity(z, np.zeros_like(cond), cam, t)
         out = []

@@ -9,9 +9,11 @@ gated residual, GELU, RMSNorm) on the same packed weights, inputs and
 timestep modulation.  Metric: scripts/compare_latent_npz.py:22-71 (RMSE of
 the difference) plus max-abs, relative to the output's RMS.
 
-The whole 28-block CFG Euler step is the same graph repeated; its latent
-RMSE against this CPU path is gated at 1e-4 by tests/test_gpu_flow.py at
-reduced sizes and reported at full size by `bench.py --validate-flow`.
+The whole 28-block CFG Euler step is the same graph repeated: it is checked
+stage by stage at full size by tests/test_gpu_flow_step_fullsize.py, gated
+end to end at reduced sizes by tests/test_gpu_flow.py, and compared end to
+end at full size against this CPU path by bench.py
+(flow.config4_step.cpu_reference_full_step).
 """
 from __future__ import annotations
 

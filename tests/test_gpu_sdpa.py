@@ -229,6 +229,51 @@ def test_sdpa_config2_sampled_rows(oracle, cuda):
     print("config2 sampled rows", s)
 
 
+@pytest.mark.parametrize("variant", ["keybias_per_head", "keybias_shared_log2048", "cross_16384x2048"])
+def test_sdpa_config3_variants_sampled_rows(oracle, cuda, variant):
+    """BASELINE configs[2] at its stated size (configs/workloads.json): the
+    configs[1] q/k/v (B=1, H=16, L=16384, RoPE+RMSNorm q/k) with
+    * a per-head key bias [16, 16384] ~ U(-2, 0) (seed c3_key_bias = 13), the
+      benchmark's extension of the reference's [Lk] bias
+      (native_sdpa_avx512_exact_q8t512.c:257-260 adds bias[j] per key);
+    * the reference-faithful shared [Lk] bias, log(2048) on key 4096;
+    * cross attention of the 16384 queries to 2048 keys/values ~ N(0,1)
+      (seeds 14, 15).
+    Full GPU call; the oracle on 24 sampled query rows of every head (rows
+    are independent), each head with its own bias row."""
+    import torch
+
+    B, H, L, Lc = 1, 16, 16384, 2048
+    print(f"config3 {variant} L={L}", flush=True)
+    q = _rope_rmsnorm(np.random.default_rng(10).standard_normal((B, H, L, 64), dtype=np.float32))
+    if variant == "cross_16384x2048":
+        k = np.random.default_rng(14).standard_normal((B, H, Lc, 64), dtype=np.float32)
+        v = np.random.default_rng(15).standard_normal((B, H, Lc, 64), dtype=np.float32)
+    else:
+        k = _rope_rmsnorm(np.random.default_rng(11).standard_normal((B, H, L, 64), dtype=np.float32))
+        v = np.random.default_rng(12).standard_normal((B, H, L, 64), dtype=np.float32)
+    bias, per_head = None, False
+    if variant == "keybias_per_head":
+        bias = np.random.default_rng(13).uniform(-2.0, 0.0, (H, L)).astype(np.float32)
+        per_head = True
+    elif variant == "keybias_shared_log2048":
+        bias = np.zeros(L, np.float32)
+        bias[4096] = np.float32(math.log(2048.0))
+    got = _run(torch, cuda, q, k, v, bias, per_head=per_head)
+    rows = np.sort(np.random.default_rng(16).choice(L, 24, replace=False))
+    rows[0], rows[-1] = 0, L - 1
+    if per_head:
+        ref = oracle.sdpa_q8t512(q[:, :, rows], k, v, bias, bias_head_stride=L)
+        for h in (0, 5, 15):   # the per-head form equals the reference's shared form run per head
+            ref_h = oracle.sdpa_q8t512(q[:, h:h + 1, rows[:4]], k[:, h:h + 1], v[:, h:h + 1], bias[h])
+            assert np.array_equal(ref_h, ref[:, h:h + 1, :4])
+    else:
+        ref = oracle.sdpa_q8t512(q[:, :, rows], k, v, bias)
+    s = _assert_close(got[:, :, rows], ref, v)
+    assert stats(got[:, :, rows[:2]], sdpa_f64(q[:, :, rows[:2]], k, v, bias))["max_abs"] < 1e-4
+    print(f"config3 {variant} sampled rows", s)
+
+
 @pytest.mark.parametrize("L,packed,bias", [(18432, True, False), (16385, True, True), (8704, False, False),
                                             (12294, False, False), (18433, True, True)])
 def test_sdpa_tail_split_sampled_rows(oracle, cuda, L, packed, bias):

@@ -254,14 +254,22 @@ class FlowModel:
         lin["fc2"].epilogue(h, bo.EPILOGUE_GATED, out=x2, gate=gate_mlp)
         return x
 
-    def velocity(self, z, cond, t):
-        """z [B, L, C], cond [B, Lc, C], t [B] (already x1000) -> v [B, L, C]."""
+    def velocity(self, z, cond, t, observe=None):
+        """z [B, L, C], cond [B, Lc, C], t [B] (already x1000) -> v [B, L, C].
+        observe(i, x), when given, sees the hidden state x entering block i,
+        and observe(len(blocks), x) the state the final layer receives (for
+        checks that recompute single blocks elsewhere; x is updated in place
+        afterwards, so keep a copy)."""
         torch = self.torch
         B, L, C = (int(s) for s in z.shape)
         t_emb, t_mod = self.timestep(t)
         x = self.input_layer(z.reshape(B * L, C)).view(B, L, C)
-        for blk in self.blocks:
+        for i, blk in enumerate(self.blocks):
+            if observe is not None:
+                observe(i, x)
             x = self.block_forward(blk, x, cond, t_mod)
+        if observe is not None:
+            observe(len(self.blocks), x)
         fs = t_emb[:, None, :].expand(B, 2, C).contiguous()  # [B, (shift, scale), C]
         for b in range(B):
             bo.add_inplace(fs[b], self.final_shift_table)
@@ -269,19 +277,22 @@ class FlowModel:
         return self.out_layer(h.view(B * L, C)).view(B, L, C)
 
     def schedule(self):
+        """t_i = s u / (1 + (s - 1) u), u = 1 - i / steps, in float64
+        (scripts/triposplat_quantized_sampler.py:398-400)."""
         s = self.cfg.shift
         u = [1.0 - i / self.cfg.steps for i in range(self.cfg.steps + 1)]
         return [s * x / (1.0 + (s - 1.0) * x) for x in u]
 
-    def euler_cfg_step(self, z, cond, step=0):
-        """One sampler step with CFG: z [L, C], cond [Lc, C] -> (z_next, v)."""
+    def euler_cfg_step(self, z, cond, step=0, observe=None):
+        """One sampler step with CFG: z [L, C], cond [Lc, C] -> (z_next, v).
+        observe: as in velocity(), over the CFG batch of 2."""
         torch = self.torch
         ts = self.schedule()
         t = torch.full((2,), ts[step] * 1000.0, dtype=torch.float32, device=self.device)
         dt = float(ts[step] - ts[step + 1])
         zz = torch.stack((z, z))
         cc = torch.stack((cond, torch.zeros_like(cond)))
-        v = self.velocity(zz, cc, t)
+        v = self.velocity(zz, cc, t, observe=observe)
         v_cfg, z_next = v[0:1].clone(), z[None].clone()
         g = torch.full((1,), self.cfg.guidance, dtype=torch.float32, device=self.device)
         d = torch.full((1,), dt, dtype=torch.float32, device=self.device)
