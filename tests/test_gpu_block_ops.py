@@ -51,23 +51,32 @@ def test_reference_named_symbols_bit_exact(oracle, cuda, hiplib, name):
         assert np.array_equal(_bits(got[k]), _bits(gold[f"{name}/out/{k}"])), (name, k)
 
 
-def test_layernorm_full_size_bit_exact(oracle, cuda, hiplib):
-    """L = 16384 rows of C = 1024 (the block's LayerNorm), and a ragged width."""
+@pytest.mark.parametrize("rows,cols,offset", [(16384, 1024, 0), (513, 1000, 0), (64, 2100, 0), (7, 100, 0),
+                                             (33, 36, 0), (300, 1024, 1), (129, 1000, 1)])
+def test_layernorm_full_size_bit_exact(oracle, cuda, hiplib, rows, cols, offset):
+    """L = 16384 rows of C = 1024 (the block's LayerNorm) and ragged widths.
+    Widths that are a multiple of 4 up to 1024 with 16-byte aligned rows take
+    the LDS-staged 128-bit kernel (cols 1000, 100, 36: a partial last 16-column
+    chunk, whose padded lanes the reference's variance counts); offset = 1
+    misaligns the rows by one float and 2100 columns exceed the staged width,
+    both taking the per-column kernel.  Every path equals the oracle bit for
+    bit."""
     import torch
 
-    for rows, cols in ((16384, 1024), (513, 1000), (64, 2100)):
-        print(f"layernorm {rows}x{cols}", flush=True)
-        r = np.random.default_rng(rows + cols)
-        x = (r.standard_normal((rows, cols)) * 1.5 + 0.3).astype(np.float32)
-        w = (1 + 0.1 * r.standard_normal(cols)).astype(np.float32)
-        b = (0.1 * r.standard_normal(cols)).astype(np.float32)
-        exp = np.empty_like(x)
-        assert oracle.ew("layernorm", x, w, b, exp, rows, cols, np.float32(1e-6), 1) == 0
-        dx, dw, db = (torch.from_numpy(a).to(cuda) for a in (x, w, b))
-        out = torch.empty_like(dx)
-        assert hiplib.triposplat_layernorm_f32_avx512(dx.data_ptr(), dw.data_ptr(), db.data_ptr(),
-                                                      out.data_ptr(), rows, cols, 1e-6, 1, 0) == 0
-        assert np.array_equal(_bits(out.cpu().numpy()), _bits(exp))
+    print(f"layernorm {rows}x{cols} offset {offset}", flush=True)
+    r = np.random.default_rng(rows + cols)
+    x = (r.standard_normal((rows, cols)) * 1.5 + 0.3).astype(np.float32)
+    w = (1 + 0.1 * r.standard_normal(cols)).astype(np.float32)
+    b = (0.1 * r.standard_normal(cols)).astype(np.float32)
+    exp = np.empty_like(x)
+    assert oracle.ew("layernorm", x, w, b, exp, rows, cols, np.float32(1e-6), 1) == 0
+    dx = torch.zeros(rows * cols + offset, device=cuda)
+    dx[offset:] = torch.from_numpy(x.reshape(-1)).to(cuda)
+    dw, db = (torch.from_numpy(a).to(cuda) for a in (w, b))
+    out = torch.full((rows * cols + offset,), float("nan"), device=cuda)
+    assert hiplib.triposplat_layernorm_f32_avx512(dx.data_ptr() + 4 * offset, dw.data_ptr(), db.data_ptr(),
+                                                  out.data_ptr() + 4 * offset, rows, cols, 1e-6, 1, 0) == 0
+    assert np.array_equal(_bits(out[offset:].cpu().numpy().reshape(rows, cols)), _bits(exp))
 
 
 def test_fused_layernorm_modulate_and_head_norm(oracle, cuda):
