@@ -28,12 +28,12 @@ BUDGET = {
     # loads from one shared 32-bit offset keep these 8 bytes and add 8 to the
     # key-bias form.
     ("sdpa", "sdpa_kernelILi1ELb0ELi16ELi64ELb0E"): 8,
-    # opt-in bf16x3 / bf16 SDPA at 16 waves ([B,H,L,64] k/v): 8 waves spill
-    # nothing but run 6 % slower (with a key bias 5 % slower: 3.40 against
-    # 3.24 ms at configs[2])
+    # opt-in bf16x3 SDPA at 16 waves ([B,H,L,64] k/v): 8 waves spill nothing
+    # but run 6 % slower.  With a key bias the bias row is the accumulators'
+    # starting value (no registers of its own): 88 -> 52 bytes, and the
+    # one-term bf16 form 32 -> 0 (configs[2] bf16x3 3.43 -> 2.88 ms).
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb0ELi16ELi64ELi1ELi3E"): 8,
-    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3E"): 88,
-    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi1E"): 32,
+    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3E"): 52,
     # strict NF24 GEMM, 256x256 tile with K steps of 32 and the deferred last
     # slice (vector-load path; epilogues store, GELU, gated, QKV, add): values
     # live across the K loop are stored once before it and reloaded once

@@ -232,11 +232,25 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
     if (wave_live) {
 #pragma unroll
     for (int kb0 = 0; kb0 < kNKB; kb0 += kGB) {
+      // The key bias (in log2 units) is the accumulators' starting value, so
+      // it is summed with the score terms and needs no registers of its own
+      // (the order of an fp32 sum of the terms and the bias, as bounded).
       floatx16 s[kGB];
 #pragma unroll
-      for (int i = 0; i < kGB; ++i)
+      for (int i = 0; i < kGB; ++i) {
+        if constexpr (kBias) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[i][r] = 0.0f;
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const floatx4 bb =
+                *reinterpret_cast<const floatx4*>(&bbuf[buf][(kb0 + i) * 32 + 8 * r4 + 4 * g]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[i][4 * r4 + e] = bb[e];
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[i][r] = 0.0f;
+        }
+      }
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -251,17 +265,6 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
           }
         }
 
-      if (kBias) {
-#pragma unroll
-        for (int i = 0; i < kGB; ++i)
-#pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) {
-            const floatx4 bb =
-                *reinterpret_cast<const floatx4*>(&bbuf[buf][(kb0 + i) * 32 + 8 * r4 + 4 * g]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s[i][4 * r4 + e] += bb[e];
-          }
-      }
       if (tail) {
         const int valid = a.Lk - key0 - 4 * g;
 #pragma unroll
