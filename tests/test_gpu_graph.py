@@ -61,6 +61,84 @@ def test_graph_few_row_gemm(cuda, M, K, N):
     _replays_match(torch, cuda, g, out, expected, lambda: nf24_linear(*args))
 
 
+@pytest.mark.parametrize("kind", ["gelu", "gated", "qkv"])
+def test_graph_epilogue_gemm_row_tail(cuda, kind):
+    """An epilogue GEMM whose <= 32-row tail runs on the few-row kernels
+    through the workspace (16385 rows = 64 x 256 + 1): captured before its
+    stream has a workspace it fails with -5 and enqueues nothing (the tail
+    goes first), after one eager call it captures, and every replay equals
+    the eager result bit for bit."""
+    import torch
+    from tsplat import block_ops as bo
+    from tsplat.nf24 import quantize_nf24_i16_per_output_channel
+    from tsplat.qkv import gemm_nf24_qkv_direct
+
+    M, K = 16385, 1024
+    N = 3 * 1024 if kind == "qkv" else 1024
+    print(f"graph epilogue gemm {kind} M={M} K={K} N={N}", flush=True)
+    g0 = torch.Generator(device=cuda).manual_seed(5)
+    x = torch.randn((M, K), generator=g0, device=cuda)
+    w = torch.randn((N, K), generator=g0, device=cuda) * 0.02
+    b = torch.randn((N,), generator=g0, device=cuda) * 0.01
+    codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+    args = (x, codes[0], codes[1], scales[0], b)
+    base = torch.randn((M, N), generator=g0, device=cuda)
+    gate = torch.randn((1, N), generator=g0, device=cuda)
+    if kind == "qkv":
+        H = 16
+        i = torch.arange(32, dtype=torch.float64, device=cuda)
+        ang = torch.arange(M, dtype=torch.float64, device=cuda)[:, None] * 1e4 ** (-2.0 * i / 64.0)[None, :]
+        fr = torch.stack((ang.cos(), ang.sin()), -1).reshape(M, 64).float()[None, :, None, :].expand(1, M, H, 64)
+        fr = fr.contiguous()
+        qg = torch.ones((H, 64), device=cuda)
+        outs = gemm_nf24_qkv_direct(*args, fr, qg, qg, 1, M, H)
+
+        def call():
+            q_, k_, v_ = gemm_nf24_qkv_direct(*args, fr, qg, qg, 1, M, H)
+            for dst, src in zip(outs, (q_, k_, v_)):
+                dst.copy_(src)
+        expected = [t.clone() for t in outs]
+        out = outs[0]
+    else:
+        out = base.clone()
+
+        def call():
+            if kind == "gelu":
+                bo.nf24_linear_epilogue(*args, bo.EPILOGUE_GELU, out=out)
+            else:
+                out.copy_(base)
+                bo.nf24_linear_epilogue(*args, bo.EPILOGUE_GATED, out=out, gate=gate)
+        call()
+        expected = [out.clone()]
+    s = torch.cuda.Stream(device=cuda)
+    torch.cuda.synchronize(cuda)
+
+    if kind != "qkv":   # the QKV wrapper allocates its outputs, which a capture cannot hold here
+        g = torch.cuda.CUDAGraph()
+        with pytest.raises(RuntimeError, match="-5"):
+            with torch.cuda.graph(g, stream=s, capture_error_mode="relaxed"):
+                call()
+        torch.cuda.synchronize(cuda)
+
+    with torch.cuda.stream(s):
+        call()                                   # eager call: the stream's buffers exist
+    torch.cuda.synchronize(cuda)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s, capture_error_mode="relaxed"):
+        call()
+    torch.cuda.synchronize(cuda)
+    results = outs if kind == "qkv" else [out]
+    for _ in range(3):
+        for t in results:
+            t.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize(cuda)
+        for got, want in zip(results, expected):
+            assert torch.equal(got, want)
+        call()                                   # eager work between replays
+        torch.cuda.synchronize(cuda)
+
+
 def test_graph_sdpa_key_split_tail(cuda):
     import torch
     from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex

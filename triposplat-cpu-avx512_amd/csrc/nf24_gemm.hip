@@ -639,9 +639,11 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
     if (p.M > 8 && p.K <= 256) return launch_cfg<CfgSkinny>(p, stream);
     return launch_nf24_gemv(p, stream);
   }
+  // The row tail goes first: its workspace is the only thing that can fail
+  // (e.g. under graph capture), and then nothing has been enqueued.
   if (const int rem = tail_rows(p.M, p.n_count)) {
-    const int st = launch_nf24_gemm(rows_slice(p, 0, p.M - rem), stream);
-    return st != kOk ? st : launch_nf24_gemv(rows_slice(p, p.M - rem, rem), stream);
+    const int st = launch_nf24_gemv(rows_slice(p, p.M - rem, rem), stream);
+    return st != kOk ? st : launch_nf24_gemm(rows_slice(p, 0, p.M - rem), stream);
   }
   if (const int m1 = round_split_rows(p.M, p.n_count)) {
     const int st = launch_nf24_gemm(rows_slice(p, 0, m1), stream);
@@ -681,11 +683,10 @@ template <int kEpi>
 int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_t stream,
                     const QkvArgs& q = QkvArgs{}, int row0 = 0) {
   if (p.precision != kPrecisionFp32 && p.M > 32) return launch_gemm_bf16(p, kEpi, q, e, row0, stream);
+  // The row tail first (as in launch_nf24_gemm: only its workspace can fail).
   if (const int rem = tail_rows(p.M, p.n_count)) {
-    const int st = launch_epi_kind<kEpi>(rows_slice(p, 0, p.M - rem), e, stream, q, row0);
-    return st != kOk ? st
-                     : launch_tail_rows<kEpi>(rows_slice(p, p.M - rem, rem), e, q, row0 + p.M - rem,
-                                              stream);
+    const int st = launch_tail_rows<kEpi>(rows_slice(p, p.M - rem, rem), e, q, row0 + p.M - rem, stream);
+    return st != kOk ? st : launch_epi_kind<kEpi>(rows_slice(p, 0, p.M - rem), e, stream, q, row0);
   }
   // Few rows: the 32-row tile (the epilogues live in the MFMA kernels).
   if (p.M <= 32) return launch_cfg<TailCfg<kEpi>, kEpi>(p, stream, q, e, row0);
@@ -719,6 +720,12 @@ int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream) {
   if (gp.n_start != 0 || gp.n_count != gp.N || gp.N != 3 * p.H * 64 ||
       (int64_t)p.B * p.L != gp.M || p.L_padded < p.L)
     return kErrDims;
+  const QkvArgs e{p.freqs, p.q_gamma, p.k_gamma, p.q, p.packed_k, p.packed_v,
+                  p.L, p.H, p.L_padded, p.freq_batches, p.kv_bhld, p.kv_round};
+  const GemmEpilogueParams none{kEpilogueStore, nullptr, 0, 1};
+  const int st = launch_epi_kind<kEpiQkv>(gp, none, stream, e);
+  if (st != kOk) return st;
+  // tokens L .. Lpad - 1 of the packed k / v (disjoint from what the GEMM writes)
   if (!p.kv_bhld && p.L_padded > p.L) {
     const int64_t rows = (int64_t)p.B * p.H * 64;
     const int64_t n = rows * (p.L_padded - p.L);
@@ -727,10 +734,7 @@ int launch_nf24_gemm_qkv(const QkvFusedParams& p, hipStream_t stream) {
                        0, stream, p.packed_k, p.packed_v, rows, p.L, p.L_padded);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
   }
-  const QkvArgs e{p.freqs, p.q_gamma, p.k_gamma, p.q, p.packed_k, p.packed_v,
-                  p.L, p.H, p.L_padded, p.freq_batches, p.kv_bhld, p.kv_round};
-  const GemmEpilogueParams none{kEpilogueStore, nullptr, 0, 1};
-  return launch_epi_kind<kEpiQkv>(gp, none, stream, e);
+  return kOk;
 }
 
 }  // namespace tsplat
