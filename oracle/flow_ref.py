@@ -226,15 +226,17 @@ def latent_stats(ref, cand):
     d = np.asarray(cand, np.float64) - ref
     ad = np.abs(d)
     mse = float(np.mean(d * d))
+    with np.errstate(invalid="ignore"):  # non-finite differences are counted below
+        p50, p95, p99 = (float(np.percentile(ad, q)) for q in (50, 95, 99))
     return {
         "mse": mse,
         "rmse": float(np.sqrt(mse)),
         "mae": float(np.mean(ad)),
         "max_abs": float(np.max(ad)),
         "mean_relative_abs": float(np.mean(ad / np.maximum(np.abs(ref), 1e-8))),
-        "p50_abs": float(np.percentile(ad, 50)),
-        "p95_abs": float(np.percentile(ad, 95)),
-        "p99_abs": float(np.percentile(ad, 99)),
+        "p50_abs": p50,
+        "p95_abs": p95,
+        "p99_abs": p99,
         "finite_count": int(np.isfinite(d).sum()),
         "nan_count": int(np.isnan(d).sum()),
         "posinf_count": int(np.isposinf(d).sum()),
