@@ -115,7 +115,8 @@ def test_fused_layernorm_modulate_and_head_norm(oracle, cuda):
 
 @pytest.mark.parametrize("M,K,N", [(600, 256, 1024), (16384, 1024, 4096), (3000, 4096, 1024), (20, 128, 96),
                                    (18432, 1024, 1024),   # whole-round split inside the second gate batch
-                                   (16386, 1024, 1024)])  # 2-row tail tile inside the second gate batch
+                                   (16386, 1024, 1024),   # 2-row tail tile inside the second gate batch
+                                   (8194, 1024, 1024)])   # 256 x 128 tiles + the 2-row tail
 def test_gemm_epilogues(oracle, cuda, M, K, N):
     """GELU / gated-residual / add epilogues == NF24 Linear then the separate
     elementwise kernel (bit for bit when both use the same GEMM tile, M > 32);

@@ -164,12 +164,14 @@ def test_gemm_config1_sampled_rows(oracle, cuda, hiplib):
 
 
 @pytest.mark.parametrize("M,K,N", [(16384, 1024, 1024), (32768, 1002, 1024), (2048, 1024, 2048),
-                                   (9000, 998, 1030), (18432, 1024, 3072)])
+                                   (9000, 998, 1030), (18432, 1024, 3072), (4096, 1024, 2048),
+                                   (8192, 1002, 1024)])
 def test_gemm_large_tiles_sampled_rows(oracle, cuda, hiplib, M, K, N):
     """Shapes that route to each tile configuration (256x256, 256x192,
-    128x128, and 18432 rows: 256x256 over 16384 rows plus 128x128 over the
-    rest), with the vectorised and the scalar-load paths (K % 4 != 0 or odd
-    N); the oracle checks 32 sampled rows."""
+    128x128, 256x128 for 4096 x 2048 and 8192 x 1024, and 18432 rows:
+    256x256 over 16384 rows plus 256x128 over the rest), with the vectorised
+    and the scalar-load paths (K % 4 != 0 or odd N); the oracle checks 32
+    sampled rows."""
     import torch
 
     print(f"gemm large M={M} K={K} N={N}", flush=True)
@@ -259,11 +261,12 @@ def test_pointer_checks_within_one_allocation(oracle, cuda, hiplib):
 
 
 @pytest.mark.parametrize("M,K,N", [(16385, 1024, 1024), (8194, 1024, 3072), (12294, 256, 1024),
-                                   (2818, 256, 3072)])
+                                   (2818, 256, 3072), (8194, 1024, 1024)])
 def test_gemm_tail_rows(oracle, cuda, hiplib, M, K, N):
     """M = 256 k + r with r <= 32 (e.g. the compressed negative branch, L + 1
-    tokens): 16385 x 1024 and 8194 x 3072 run the tail rows on the few-row
-    kernels (in the main grid they would add a round), 12294 x 1024 (the
+    tokens): 16385 x 1024, 8194 x 3072 and 8194 x 1024 (main rows on 256 x
+    128 tiles, the 8448-row call on 256 x 192) run the tail rows on the
+    few-row kernels (in the main grid they would add a round), 12294 x 1024 (the
     reference's sequence length) runs 12288 rows on 192 x 256 tiles -- one
     round of 256 -- and the 6-row tail on the few-row kernels, 2818 x 3072
     keeps its two tail rows in its 256 x 192 grid (their tiles fit the last

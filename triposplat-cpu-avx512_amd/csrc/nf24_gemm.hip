@@ -482,7 +482,8 @@ __global__ __launch_bounds__(kTailThreads) void packed_tail_zero_kernel(float* p
 // last round costs ceil(rest / CUs) tiles' worth, 25 % more when a 4-wave
 // workgroup then runs alone on its CU (one wave per SIMD hides less latency).
 // Against measurement (M = 2048..32768, N = 1024..4096) the model picks the
-// fastest configuration or one within 3 % of it.
+// fastest configuration or one within 3 % of it.  The 256 x 128 rate (119)
+// is fitted to its one-round calls against 128 x 128 (M = 2048..8192).
 // 16 waves, 1 workgroup / CU, K steps of 32 with the deferred last slice
 // (since the buffer-resource loads left room: 16384 x 4096 x 1024 1033 ->
 // 990 us against K steps of 16; two live-range values spill once per
@@ -498,6 +499,12 @@ using CfgWide = GemmCfg<256, 192, 32, 4, 3, 1, 0, true>;
 // 256 CUs, against 256 tiles of 192 x 256 plus the 6-row tail launch)
 using CfgTall = GemmCfg<192, 256, 32, 3, 4, 1, 0, true>;
 using CfgSmall = GemmCfg<128, 128, 16, 2, 2, 3>; // 4 waves, 3 workgroups / CU
+// 8 waves (two per SIMD), 1 workgroup / CU: for calls whose 256 x 256 /
+// 256 x 192 tiles leave CUs idle and whose 128 x 128 tiles would share CUs
+// two or three to one (the compressed negative branch's 8192 x 1024 GEMMs:
+// 256 tiles, one per CU; 152 -> 141 us at K = 1024, 568 -> 533 us at
+// K = 4096 against 512 tiles of 128 x 128)
+using CfgHalf = GemmCfg<256, 128, 32, 4, 2, 1, 0, true>;
 // The scalar-load path (unaligned or odd operands) runs the 256 x 256 tile at
 // K steps of 16: the guarded per-element loads need the registers that the
 // 32-deep step and its deferred slice take, and spill inside the K loop.
@@ -522,7 +529,8 @@ struct Choice {
   double rate;
 };
 constexpr Choice kChoices[] = {
-    {256, 256, 1, 16, 126.0}, {256, 192, 1, 12, 125.0}, {128, 128, 3, 4, 111.0}, {192, 256, 1, 12, 125.0}};
+    {256, 256, 1, 16, 126.0}, {256, 192, 1, 12, 125.0}, {128, 128, 3, 4, 111.0}, {192, 256, 1, 12, 125.0},
+    {256, 128, 1, 8, 119.0}};
 constexpr int kNumChoices = sizeof(kChoices) / sizeof(kChoices[0]);
 
 // Modelled time of configuration i (kChoices) over M x n_count outputs.
@@ -653,6 +661,7 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
   if (best == 0) return launch_cfg<CfgLarge>(p, stream);
   if (best == 1) return launch_cfg<CfgWide>(p, stream);
   if (best == 3) return launch_cfg<CfgTall>(p, stream);
+  if (best == 4) return launch_cfg<CfgHalf>(p, stream);
   return launch_cfg<CfgSmall>(p, stream);
 }
 
@@ -698,6 +707,7 @@ int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_
   if (best == 0) return launch_cfg<CfgLarge, kEpi>(p, stream, q, e, row0);
   if (best == 1) return launch_cfg<CfgWide, kEpi>(p, stream, q, e, row0);
   if (best == 3) return launch_cfg<CfgTall, kEpi>(p, stream, q, e, row0);
+  if (best == 4) return launch_cfg<CfgHalf, kEpi>(p, stream, q, e, row0);
   return launch_cfg<CfgSmall, kEpi>(p, stream, q, e, row0);
 }
 }  // namespace
