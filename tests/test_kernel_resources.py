@@ -42,8 +42,13 @@ BUDGET = {
     ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi0E"): 12,
     ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi1E"): 16,
     ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi2E"): 16,
-    ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi3E"): 24,
-    ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi4E"): 12,
+    ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi3E"): 16,
+    ("nf24_gemm", "GemmCfgILi256ELi256ELi32ELi4ELi4ELi1ELi0ELb1EEELb1ELi4E"): 20,
+    # 256x256 scalar-load path (unaligned or odd operands), gated epilogue:
+    # the block's 16 old values and gates read ahead of its stores take
+    # registers the 128-register budget lacks; three values are stored
+    # after the K loop and reloaded for the epilogue
+    ("nf24_gemm", "GemmCfgILi256ELi256ELi16ELi4ELi4ELi1ELi0ELb0EEELb0ELi3E"): 12,
 }
 
 # kernels that must exist (a rename must update this test, not skip it)

@@ -210,6 +210,58 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs& a, floatx16 (&acc)[
 template <int kMB, int kNB, int kEpi>
 __device__ __forceinline__ void store_result(const GemmArgs& a, floatx16 (&acc)[kMB][kNB],
                                              int row_base, int col_base, int g, int l32) {
+  if constexpr (kEpi == kEpilogueGated || kEpi == kEpilogueAdd) {
+    // Read-modify-write epilogues: each 32 x 32 block reads all of its old
+    // values (and, when its 32 rows lie in one gate batch, its gate value
+    // once) before it stores any, so that the loads are in flight together;
+    // element by element, every load would wait behind the previous store,
+    // which might alias it.  The same arithmetic per element.
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < kNB; ++nb) {
+        const int col = col_base + nb * 32 + l32;
+        const int rb = row_base + mb * 32;
+        if (col >= a.n_count || rb >= a.M) continue;
+        float* dst = a.out + (int64_t)rb * a.stride_out + col;
+        float old[16], gt[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dr = 8 * (r / 4) + 4 * g + (r % 4);
+          old[r] = rb + dr < a.M ? dst[(int64_t)dr * a.stride_out] : 0.0f;
+        }
+        if constexpr (kEpi == kEpilogueGated) {
+          const int t0 = a.row0 + rb;
+          const int b0 = t0 / a.rows_per_batch;
+          if (b0 == (t0 + 31) / a.rows_per_batch) {  // uniform over the wave
+            const float gv = a.gate[(int64_t)b0 * a.gate_stride + a.n_start + col];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) gt[r] = gv;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int dr = 8 * (r / 4) + 4 * g + (r % 4);
+              gt[r] = rb + dr < a.M
+                          ? a.gate[(int64_t)((t0 + dr) / a.rows_per_batch) * a.gate_stride +
+                                   a.n_start + col]
+                          : 0.0f;
+            }
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dr = 8 * (r / 4) + 4 * g + (r % 4);
+          if (rb + dr >= a.M) continue;
+          if constexpr (kEpi == kEpilogueGated)
+            // h = acc * gate, x = x + h: two roundings, as the reference's
+            // native_block_elementwise_avx512.c:24-35
+            dst[(int64_t)dr * a.stride_out] = gated_residual_ref(old[r], acc[mb][nb][r], gt[r]);
+          else
+            dst[(int64_t)dr * a.stride_out] = old[r] + acc[mb][nb][r];
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
@@ -224,13 +276,6 @@ __device__ __forceinline__ void store_result(const GemmArgs& a, floatx16 (&acc)[
         const float v = acc[mb][nb][r];
         if constexpr (kEpi == kEpilogueGelu) {
           *dst = gelu_tanh_ref(v);
-        } else if constexpr (kEpi == kEpilogueGated) {
-          // h = acc * gate, x = x + h: two roundings, as the reference's
-          // native_block_elementwise_avx512.c:24-35
-          const float* gate = a.gate + (int64_t)((a.row0 + row) / a.rows_per_batch) * a.gate_stride;
-          *dst = gated_residual_ref(*dst, v, gate[a.n_start + col]);
-        } else if constexpr (kEpi == kEpilogueAdd) {
-          *dst = *dst + v;
         } else {
           *dst = v;
         }
