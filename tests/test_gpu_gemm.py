@@ -165,11 +165,12 @@ def test_gemm_config1_sampled_rows(oracle, cuda, hiplib):
 
 @pytest.mark.parametrize("M,K,N", [(16384, 1024, 1024), (32768, 1002, 1024), (2048, 1024, 2048),
                                    (9000, 998, 1030), (18432, 1024, 3072), (4096, 1024, 2048),
-                                   (8192, 1002, 1024)])
+                                   (8192, 1002, 1024), (2600, 1024, 3072), (2048, 1002, 1024)])
 def test_gemm_large_tiles_sampled_rows(oracle, cuda, hiplib, M, K, N):
-    """Shapes that route to each tile configuration (256x256, 256x192,
-    128x128, 256x128 for 4096 x 2048 and 8192 x 1024, and 18432 rows:
-    256x256 over 16384 rows plus 256x128 over the rest), with the vectorised
+    """Shapes that route to each tile configuration (256x256: 16384 and
+    32768 rows; 256x192: 9000 x 1030; 256x128: 4096 x 2048 and 8192 x 1024;
+    128x128: 2600 x 3072; 128x64: 2048 x 2048 and 2048 x 1024; 18432 rows:
+    256x256 over 16384 rows plus 128x64 over the rest), with the vectorised
     and the scalar-load paths (K % 4 != 0 or odd N); the oracle checks 32
     sampled rows."""
     import torch

@@ -100,13 +100,14 @@ def test_qkv_direct(oracle, cuda, B, L, H, fb, Lp):
 @pytest.mark.parametrize("B,L,H,fb", [(1, 16384, 16, 1), (1, 4096, 16, 1), (2, 300, 4, 2), (3, 257, 2, 1),
                                      (1, 5000, 16, 1), (1, 8194, 16, 1), (1, 3000, 16, 1),
                                      (1, 18432, 16, 1),   # split into whole-round row launches
-                                     (1, 2048, 16, 1), (1, 16385, 16, 1)])
+                                     (1, 2048, 16, 1), (1, 16385, 16, 1), (1, 2200, 16, 1),
+                                     (1, 2600, 16, 1)])
 def test_qkv_fused_matches_unfused(oracle, cuda, B, L, H, fb):
     """Fused epilogue == NF24 GEMM then the postprocess kernel, at shapes that
     route to each tile configuration (256x256: L=16384, 5000, 16385 (plus its
     1-row tail); 256x192: L=4096, 3000, 8194 (plus its 2-row tail); 256x128:
-    L=2048 and the last 2048 rows of L=18432; 128x128: the rest), with
-    partial row tiles and odd L.
+    L=2200; 128x128: L=2600; 128x64: L=2048, the last 2048 rows of L=18432
+    and the small shapes), with partial row tiles and odd L.
     Both paths run the same GEMM main loop and the same postprocess
     arithmetic, so all three outputs are bit-identical."""
     import torch

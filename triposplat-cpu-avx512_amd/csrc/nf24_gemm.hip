@@ -483,7 +483,8 @@ __global__ __launch_bounds__(kTailThreads) void packed_tail_zero_kernel(float* p
 // workgroup then runs alone on its CU (one wave per SIMD hides less latency).
 // Against measurement (M = 2048..32768, N = 1024..4096) the model picks the
 // fastest configuration or one within 3 % of it.  The 256 x 128 rate (119)
-// is fitted to its one-round calls against 128 x 128 (M = 2048..8192).
+// is fitted to its one-round calls against 128 x 128 (M = 2048..8192), the
+// 128 x 64 rate (100) to M = 512..8192 at N = 1024..4096.
 // 16 waves, 1 workgroup / CU, K steps of 32 with the deferred last slice
 // (since the buffer-resource loads left room: 16384 x 4096 x 1024 1033 ->
 // 990 us against K steps of 16; two live-range values spill once per
@@ -505,6 +506,12 @@ using CfgSmall = GemmCfg<128, 128, 16, 2, 2, 3>; // 4 waves, 3 workgroups / CU
 // 256 tiles, one per CU; 152 -> 141 us at K = 1024, 568 -> 533 us at
 // K = 4096 against 512 tiles of 128 x 128)
 using CfgHalf = GemmCfg<256, 128, 32, 4, 2, 1, 0, true>;
+// 4 waves of 32 x 64, 2 workgroups / CU: for calls too small to fill the
+// chip with the larger tiles (the 2048-row remainder of the single-stream
+// graph's 18432 rows: 2048 x 1024 x 1024 90 -> 51 us, 2048 x 4096 x 1024
+// 344 -> 188 us, 4096 x 1024 x 1024 91 -> 81 us, 3000 x 1024 x 1024 93 ->
+// 81 us, against 128 x 128 tiles that left half the CUs idle)
+using CfgNarrow = GemmCfg<128, 64, 32, 4, 1, 2, 0, true>;
 // The scalar-load path (unaligned or odd operands) runs the 256 x 256 tile at
 // K steps of 16: the guarded per-element loads need the registers that the
 // 32-deep step and its deferred slice take, and spill inside the K loop.
@@ -530,7 +537,7 @@ struct Choice {
 };
 constexpr Choice kChoices[] = {
     {256, 256, 1, 16, 126.0}, {256, 192, 1, 12, 125.0}, {128, 128, 3, 4, 111.0}, {192, 256, 1, 12, 125.0},
-    {256, 128, 1, 8, 119.0}};
+    {256, 128, 1, 8, 119.0},  {128, 64, 2, 4, 100.0}};
 constexpr int kNumChoices = sizeof(kChoices) / sizeof(kChoices[0]);
 
 // Modelled time of configuration i (kChoices) over M x n_count outputs.
@@ -662,6 +669,7 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
   if (best == 1) return launch_cfg<CfgWide>(p, stream);
   if (best == 3) return launch_cfg<CfgTall>(p, stream);
   if (best == 4) return launch_cfg<CfgHalf>(p, stream);
+  if (best == 5) return launch_cfg<CfgNarrow>(p, stream);
   return launch_cfg<CfgSmall>(p, stream);
 }
 
@@ -708,6 +716,7 @@ int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_
   if (best == 1) return launch_cfg<CfgWide, kEpi>(p, stream, q, e, row0);
   if (best == 3) return launch_cfg<CfgTall, kEpi>(p, stream, q, e, row0);
   if (best == 4) return launch_cfg<CfgHalf, kEpi>(p, stream, q, e, row0);
+  if (best == 5) return launch_cfg<CfgNarrow, kEpi>(p, stream, q, e, row0);
   return launch_cfg<CfgSmall, kEpi>(p, stream, q, e, row0);
 }
 }  // namespace
