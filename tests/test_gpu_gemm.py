@@ -263,12 +263,13 @@ def test_pointer_checks_within_one_allocation(oracle, cuda, hiplib):
 
 @pytest.mark.parametrize("M,K,N", [(16385, 1024, 1024), (8194, 1024, 3072), (12294, 256, 1024),
                                    (2818, 256, 3072), (8194, 1024, 1024), (12294, 4096, 1024),
-                                   (16416, 1024, 1024), (16401, 1000, 1024)])
+                                   (16416, 1024, 1024), (16401, 1000, 1024), (16400, 256, 1024)])
 def test_gemm_tail_rows(oracle, cuda, hiplib, M, K, N):
     """M = 256 k + r with r <= 32 (e.g. the compressed negative branch, L + 1
     tokens): 16385 x 1024, 8194 x 3072 and 8194 x 1024 (main rows on 256 x
     128 tiles, the 8448-row call on 256 x 192), 16416 x 1024 (the most tail
-    rows, 32) and 16401 x 1000 x 1024 (17 rows) run the
+    rows, 32), 16401 x 1000 x 1024 (17 rows) and 16400 x 256 x 1024 (16 rows
+    at a short K: the skinny MFMA tile, as a call over exactly them) run the
     tail rows on the few-row kernels (in the main grid they would add a
     round), 12294 x 256 / 4096 x 1024 (the
     reference's sequence length) runs 12288 rows on 192 x 256 tiles -- one

@@ -11,15 +11,18 @@ against the strict fp32 path is reported and held to its expected band
 (bf16 about 2^-9, bf16x3 about 2^-17 of the output RMS).  The epilogues and
 the fused QKV postprocess are fp32 functions of the accumulator, so each
 equals, bit for bit, the oracle's elementwise step / postprocess applied to
-the same mode's plain GEMM output.  Tile shapes sum in one order, so rows
-computed by the 128-row tail launch equal the same rows inside 256-row tiles.
+the same mode's plain GEMM output.  Tile shapes sum in one order, so
+128-row tiles equal the same rows inside 256-row tiles; a row tail split off a
+call (at most 32 rows, when keeping them in the grid would add a round) runs
+on the strict few-row path, like whole calls of at most 32 rows, and equals a
+strict call over exactly those rows.
 """
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from _parity import U, seeded_linear, stats
+from _parity import U, gemm_order_bound, seeded_linear, stats
 
 pytestmark = pytest.mark.gpu
 
@@ -111,12 +114,17 @@ def test_bf16_few_rows_run_strict(oracle, cuda, hiplib):
     (528, 256, 512),     # 16 tail rows in a 256 x 192 grid of one round
     (12294, 64, 3072),   # 6 tail rows kept in a full-chip 256 x 256 grid (588 tiles, 3 rounds);
                          # its 12288 head rows run as 256 x 192 tiles (768 tiles, 3 rounds)
-    (16400, 64, 1024),   # 256 full tiles = one round on 256 CUs; the tail would add one: 128-row launch
+    (16400, 64, 1024),   # 256 full tiles = one round on 256 CUs; the tail would add one: split off
+    (12294, 64, 4096),   # the reference's fc1 shape: 768 tiles = 3 rounds, the tail would add a fourth
+    (16416, 1024, 1024),  # the most split-off rows (32), K long enough for the few-row K split
 ])
 def test_bf16_tail_rows_bitwise(oracle, cuda, hiplib, precision, M, K, N):
-    """Rows past a multiple of 256 give the same bits whether they stay in the
-    256-row grid or run as a separate 128-row launch, and equal the same rows
-    computed inside a larger grid; 128-row tiles equal 256-row tiles."""
+    """Rows past a multiple of 256 either stay in the 256-row grid (then they
+    equal, bit for bit, the same rows computed inside a larger grid) or,
+    when they would add a round, are split off onto the strict few-row path
+    (then they equal a strict call over exactly those rows, and the strict
+    oracle bound); the head rows equal a call over exactly them, and 128-row
+    tiles equal 256-row tiles."""
     import torch
 
     print(f"bf16 tail rows {precision} M={M} K={K} N={N}", flush=True)
@@ -128,9 +136,21 @@ def test_bf16_tail_rows_bitwise(oracle, cuda, hiplib, precision, M, K, N):
     full = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision)
     small = _run(torch, hiplib, cuda, x[:128], c01, q2, s, b[:N], precision)   # 128-row tiles
     assert np.array_equal(got[:M - r].view(np.uint32), head.view(np.uint32))
-    assert np.array_equal(got[M - r:].view(np.uint32), full[M - r:M].view(np.uint32))
     assert np.array_equal(small.view(np.uint32), full[:128].view(np.uint32))
-    rows = np.concatenate([np.arange(0, 256), np.arange(M - r - 64, M)])
+    # the launch plan's rule: a tail that would add a round of 256 x 256 tiles is split off
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    bands = (N + 255) // 256
+    base = (M // 256) * bands
+    split = -(-(base + bands) // cus) > -(-base // cus)
+    if split:
+        strict = _run(torch, hiplib, cuda, x[M - r:M], c01, q2, s, b, "fp32")
+        assert np.array_equal(got[M - r:].view(np.uint32), strict.view(np.uint32))
+        want = oracle.nf24_gemm(x[M - r:M], c01, q2, s, b)     # the reference's fp32 chain
+        bound = gemm_order_bound(x[M - r:M], oracle.decode_nf24(c01, q2, s), b)
+        assert np.all(np.abs(got[M - r:].astype(np.float64) - want) <= bound)
+    else:
+        assert np.array_equal(got[M - r:].view(np.uint32), full[M - r:M].view(np.uint32))
+    rows = np.arange(0, 256) if split else np.concatenate([np.arange(0, 256), np.arange(M - r - 64, M)])
     _check_terms(oracle, x[rows], c01, q2, s, b, got[rows], precision)
 
 

@@ -657,7 +657,8 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
   // The row tail goes first: its workspace is the only thing that can fail
   // (e.g. under graph capture), and then nothing has been enqueued.
   if (const int rem = tail_rows(p.M, p.n_count)) {
-    const int st = launch_nf24_gemv(rows_slice(p, p.M - rem, rem), stream);
+    // the tail rows take the path of a call over exactly those rows
+    const int st = launch_nf24_gemm(rows_slice(p, p.M - rem, rem), stream);
     return st != kOk ? st : launch_nf24_gemm(rows_slice(p, 0, p.M - rem), stream);
   }
   if (const int m1 = round_split_rows(p.M, p.n_count)) {
@@ -720,6 +721,21 @@ int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_
   return launch_cfg<CfgSmall, kEpi>(p, stream, q, e, row0);
 }
 }  // namespace
+
+int nf24::launch_strict_tail(const GemmParams& p, int epi, const QkvArgs& e,
+                             const GemmEpilogueParams& ep, int row0, hipStream_t stream) {
+  GemmParams s = p;
+  s.precision = kPrecisionFp32;
+  if (s.M < 1 || s.M > kTailRows) return kErrDims;
+  switch (epi) {
+    case kEpiStore: return launch_nf24_gemm(s, stream);
+    case kEpiQkv: return launch_tail_rows<kEpiQkv>(s, ep, e, row0, stream);
+    case kEpilogueGelu: return launch_tail_rows<kEpilogueGelu>(s, ep, e, row0, stream);
+    case kEpilogueGated: return launch_tail_rows<kEpilogueGated>(s, ep, e, row0, stream);
+    case kEpilogueAdd: return launch_tail_rows<kEpilogueAdd>(s, ep, e, row0, stream);
+    default: return kErrDims;
+  }
+}
 
 int launch_nf24_gemm_epilogue(const GemmParams& p, const GemmEpilogueParams& e,
                               hipStream_t stream) {

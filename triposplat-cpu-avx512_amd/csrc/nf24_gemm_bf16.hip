@@ -486,8 +486,10 @@ int launch_gemm_bf16(const GemmParams& p, int epi, const QkvArgs& e, const GemmE
   // past the last multiple of 256 that number at most 32 stay in that grid
   // when their partial tiles fit in its last round (M = 12294, N = 3072:
   // 588 tiles, three rounds as without them; 286 against 329 us as a second
-  // launch), else they run as 128-row tiles; both shapes sum every output in
-  // the same order.
+  // launch), else they run on the strict few-row path (launch_strict_tail,
+  // first: its workspace is the only thing that can fail), as whole calls
+  // of that size do in every mode: fp32 rows, 12294 x 1024 x 4096's 6 rows
+  // in ~15 us where 128-row bf16 tiles over 32 column bands took ~50 us.
   if (p.M < 256 || p.n_count < 256) return launch_shape<Bf16Small, true>(a, terms, epi, stream);
   const int rem = p.M % 256;
   const int64_t cus = compute_units();
@@ -503,8 +505,12 @@ int launch_gemm_bf16(const GemmParams& p, int epi, const QkvArgs& e, const GemmE
   if (3 * rounds(row_bands * ((p.n_count + 191) / 192)) < large_cost)
     return launch_shape<Bf16Wide, true>(a, terms, epi, stream);
   if (!split) return launch_shape<Bf16Large, true>(a, terms, epi, stream);
-  const int st = launch_shape<Bf16Large, true>(rows_of(a, 0, p.M - rem), terms, epi, stream);
-  return st != kOk ? st : launch_shape<Bf16Small, true>(rows_of(a, p.M - rem, rem), terms, epi, stream);
+  GemmParams t = p;
+  t.x = p.x + (int64_t)(p.M - rem) * p.stride_x;
+  t.out = p.out != nullptr ? p.out + (int64_t)(p.M - rem) * p.stride_out : nullptr;
+  t.M = rem;
+  const int st = launch_strict_tail(t, epi, e, ep, row0 + p.M - rem, stream);
+  return st != kOk ? st : launch_shape<Bf16Large, true>(rows_of(a, 0, p.M - rem), terms, epi, stream);
 }
 
 }  // namespace nf24

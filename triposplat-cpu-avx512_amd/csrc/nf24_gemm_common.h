@@ -299,5 +299,12 @@ inline bool vec_buffers_fit(const GemmParams& p, int bm, int bk) {
 int launch_gemm_bf16(const GemmParams& p, int epi, const QkvArgs& e, const GemmEpilogueParams& ep,
                      int row0, hipStream_t stream);
 
+// A row tail (at most 32 rows, token index of its row 0 row0) split off a
+// bf16-mode call, on the strict few-row path (nf24_gemm.hip) with epilogue
+// kind epi: as whole calls of at most 32 rows in every mode, the weight
+// stream is the cost there and fp32 is free.
+int launch_strict_tail(const GemmParams& p, int epi, const QkvArgs& e, const GemmEpilogueParams& ep,
+                       int row0, hipStream_t stream);
+
 }  // namespace nf24
 }  // namespace tsplat
