@@ -112,8 +112,7 @@ def test_bf16_few_rows_run_strict(oracle, cuda, hiplib):
 @pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
 @pytest.mark.parametrize("M,K,N", [
     (528, 256, 512),     # 16 tail rows in a 256 x 192 grid of one round
-    (12294, 64, 3072),   # 6 tail rows kept in a full-chip 256 x 256 grid (588 tiles, 3 rounds);
-                         # its 12288 head rows run as 256 x 192 tiles (768 tiles, 3 rounds)
+    (12294, 64, 3072),   # 6 tail rows: the 12288 head rows fill 3 rounds of 256 x 192 tiles
     (16400, 64, 1024),   # 256 full tiles = one round on 256 CUs; the tail would add one: split off
     (12294, 64, 4096),   # the reference's fc1 shape: 768 tiles = 3 rounds, the tail would add a fourth
     (16416, 1024, 1024),  # the most split-off rows (32), K long enough for the few-row K split
@@ -137,21 +136,43 @@ def test_bf16_tail_rows_bitwise(oracle, cuda, hiplib, precision, M, K, N):
     small = _run(torch, hiplib, cuda, x[:128], c01, q2, s, b[:N], precision)   # 128-row tiles
     assert np.array_equal(got[:M - r].view(np.uint32), head.view(np.uint32))
     assert np.array_equal(small.view(np.uint32), full[:128].view(np.uint32))
-    # the launch plan's rule: a tail that would add a round of 256 x 256 tiles is split off
-    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
-    bands = (N + 255) // 256
-    base = (M // 256) * bands
-    split = -(-(base + bands) // cus) > -(-base // cus)
+    # Kept in the grid (the launch model's choice) the tail rows equal the
+    # same rows of the larger grid; split off, a strict call over exactly them.
+    strict = _run(torch, hiplib, cuda, x[M - r:M], c01, q2, s, b, "fp32")
+    split = np.array_equal(got[M - r:].view(np.uint32), strict.view(np.uint32))
+    print(f"tail rows split off: {split}", flush=True)
     if split:
-        strict = _run(torch, hiplib, cuda, x[M - r:M], c01, q2, s, b, "fp32")
-        assert np.array_equal(got[M - r:].view(np.uint32), strict.view(np.uint32))
         want = oracle.nf24_gemm(x[M - r:M], c01, q2, s, b)     # the reference's fp32 chain
         bound = gemm_order_bound(x[M - r:M], oracle.decode_nf24(c01, q2, s), b)
         assert np.all(np.abs(got[M - r:].astype(np.float64) - want) <= bound)
     else:
         assert np.array_equal(got[M - r:].view(np.uint32), full[M - r:M].view(np.uint32))
+    if (M, N) in ((16400, 1024), (12294, 4096)):       # a tail that would add a round
+        assert split
     rows = np.arange(0, 256) if split else np.concatenate([np.arange(0, 256), np.arange(M - r - 64, M)])
     _check_terms(oracle, x[rows], c01, q2, s, b, got[rows], precision)
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+def test_bf16_tile_shapes_bitwise(oracle, cuda, hiplib, precision):
+    """Calls the launch model sends to the other tile shapes -- 12288 rows at
+    N = 1024 (192 x 256), 8192 (256 x 128), 2048 (128 x 64), 4096 at N = 3072
+    (256 x 192) -- equal the same rows of a 16384-row call (256 x 256) bit for
+    bit (every shape sums each output in one order), and the mode's terms on
+    sampled rows."""
+    import torch
+
+    K = 64
+    for N, rows_list in ((1024, (12288, 8192, 2048)), (3072, (4096,))):
+        x, w, b = seeded_linear(40 + N, 16384, K, N, w_scale=0.02)
+        c01, q2, s = oracle.quantize_nf24_i16(w)
+        full = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision)
+        for M in rows_list:
+            print(f"bf16 tile shapes {precision} M={M} N={N}", flush=True)
+            got = _run(torch, hiplib, cuda, x[:M], c01, q2, s, b, precision)
+            assert np.array_equal(got.view(np.uint32), full[:M].view(np.uint32)), (M, N)
+            rows = np.sort(np.random.default_rng(M).choice(M, 24, replace=False))
+            _check_terms(oracle, x[rows], c01, q2, s, b, got[rows], precision)
 
 
 @pytest.mark.parametrize("precision", ["bf16", "bf16x3"])

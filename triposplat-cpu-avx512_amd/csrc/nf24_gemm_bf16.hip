@@ -85,6 +85,14 @@ using Bf16Large = Bf16Cfg<256, 256, 2, 4>;  // 8 waves, 128 x 64 per wave
 // two on each of two SIMDs and one on each of the others)
 using Bf16Wide = Bf16Cfg<256, 192, 4, 3, 2>;
 using Bf16Small = Bf16Cfg<128, 128, 2, 2>;  // 4 waves, 64 x 64 per wave
+// Where the larger tiles leave CUs idle (measured, bf16x3 / bf16, gated
+// epilogue): 12 waves of 64 x 64 over 192 rows -- the reference's 12288
+// rows at N = 1024, 256 tiles: 114 -> 92 / 77 -> 64 us; 8 waves of 64 x 64
+// over 128 columns -- 8192 x 1024: 79 -> 69 / 56 -> 52 us; 4 waves of
+// 32 x 64, two workgroups per CU -- 2048 x 1024: 74 -> 38 / 52 -> 35 us.
+using Bf16Tall = Bf16Cfg<192, 256, 3, 4, 2>;
+using Bf16Half = Bf16Cfg<256, 128, 4, 2, 4>;
+using Bf16Narrow = Bf16Cfg<128, 64, 4, 1, 2>;
 
 // bf16 element offset of (row r, chunk c) in a 32-k tile row.
 template <bool kSwz>
@@ -459,6 +467,35 @@ int launch_shape(const GemmArgs& a, int terms, int epi, hipStream_t stream) {
   return terms == 3 ? launch_terms<C, 3, kVec>(a, epi, stream) : launch_terms<C, 1, kVec>(a, epi, stream);
 }
 
+// The tile shapes the launch model chooses from: a round of the chip
+// (CUs x wgs_per_cu workgroups) costs `round` units, measured at K = 1024
+// for three terms (bf16x3) and one (bf16); the model is rounds x cost.  The
+// VALU- and power-bound kernels gain little from a round left part-empty,
+// so a partial round costs a whole one.
+struct Bf16Choice {
+  int bm, bn, wgs_per_cu, round3, round1;
+};
+constexpr Bf16Choice kBf16Choices[] = {
+    {256, 256, 1, 113, 74}, {256, 192, 1, 85, 58}, {192, 256, 1, 92, 63},
+    {256, 128, 1, 66, 50},  {128, 64, 2, 40, 35}};
+constexpr int kNumBf16Choices = sizeof(kBf16Choices) / sizeof(kBf16Choices[0]);
+
+int64_t bf16_model_time(int i, int M, int n_count, int terms) {
+  const Bf16Choice& c = kBf16Choices[i];
+  const int64_t tiles = (int64_t)((M + c.bm - 1) / c.bm) * ((n_count + c.bn - 1) / c.bn);
+  const int64_t slots = (int64_t)compute_units() * c.wgs_per_cu;
+  return (tiles + slots - 1) / slots * (terms == 3 ? c.round3 : c.round1);
+}
+
+// Index into kBf16Choices with the smallest modelled time (a tie keeps the
+// earlier entry, 256 x 256 first).
+int bf16_pick(int M, int n_count, int terms) {
+  int best = 0;
+  for (int i = 1; i < kNumBf16Choices; ++i)
+    if (bf16_model_time(i, M, n_count, terms) < bf16_model_time(best, M, n_count, terms)) best = i;
+  return best;
+}
+
 // Rows [first, first + count) of the call as their own launch.
 GemmArgs rows_of(GemmArgs a, int first, int count) {
   a.x += (int64_t)first * a.stride_x;
@@ -482,35 +519,37 @@ int launch_gemm_bf16(const GemmParams& p, int epi, const QkvArgs& e, const GemmE
                    (reinterpret_cast<uintptr_t>(p.q2) % 4 == 0) &&
                    vec_buffers_fit(p, Bf16Large::BM, Bf16Large::BK);
   if (!vec) return launch_shape<Bf16Small, false>(a, terms, epi, stream);
-  // 256 x 256 tiles where there are rows and columns to fill them.  Rows
-  // past the last multiple of 256 that number at most 32 stay in that grid
-  // when their partial tiles fit in its last round (M = 12294, N = 3072:
-  // 588 tiles, three rounds as without them; 286 against 329 us as a second
-  // launch), else they run on the strict few-row path (launch_strict_tail,
-  // first: its workspace is the only thing that can fail), as whole calls
-  // of that size do in every mode: fp32 rows, 12294 x 1024 x 4096's 6 rows
-  // in ~15 us where 128-row bf16 tiles over 32 column bands took ~50 us.
   if (p.M < 256 || p.n_count < 256) return launch_shape<Bf16Small, true>(a, terms, epi, stream);
+  // Rows past the last multiple of 256 that number at most 32 stay in the
+  // grid when they add no modelled time (M = 2818, N = 3072: 12 row bands
+  // of 256 x 192 tiles, one round either way), else they run on the strict
+  // few-row path (launch_strict_tail, first: its workspace is the only thing
+  // that can fail), as whole calls of that size do in every mode: fp32 rows,
+  // e.g. 12294 x 1024 x 4096's 6 rows in ~15 us where 128-row bf16 tiles
+  // over 32 column bands took ~50 us.  Every tile shape sums each output in
+  // the same order.
   const int rem = p.M % 256;
-  const int64_t cus = compute_units();
-  auto rounds = [cus](int64_t tiles) { return (tiles + cus - 1) / cus; };
-  const int64_t bands = (p.n_count + 255) / 256, row_bands = (p.M + 255) / 256;
-  const int64_t base = (int64_t)(p.M / 256) * bands;
-  const bool split = rem != 0 && rem <= 32 && rounds(base + bands) > rounds(base);
-  // 256 x 192 tiles when their rounds of the chip, each 3/4 as long, take
-  // less time than the 256 x 256 plan (a split-off tail counted as a
-  // quarter round): M = 4096, N = 3072 gives 256 tiles, every CU once,
-  // where 256 x 256 leaves 64 of 256 idle.  A tie keeps 256 x 256.
-  const int64_t large_cost = split ? 4 * rounds(base) + 1 : 4 * rounds(row_bands * bands);
-  if (3 * rounds(row_bands * ((p.n_count + 191) / 192)) < large_cost)
-    return launch_shape<Bf16Wide, true>(a, terms, epi, stream);
-  if (!split) return launch_shape<Bf16Large, true>(a, terms, epi, stream);
-  GemmParams t = p;
-  t.x = p.x + (int64_t)(p.M - rem) * p.stride_x;
-  t.out = p.out != nullptr ? p.out + (int64_t)(p.M - rem) * p.stride_out : nullptr;
-  t.M = rem;
-  const int st = launch_strict_tail(t, epi, e, ep, row0 + p.M - rem, stream);
-  return st != kOk ? st : launch_shape<Bf16Large, true>(rows_of(a, 0, p.M - rem), terms, epi, stream);
+  const bool split = rem != 0 && rem <= 32 &&
+                     bf16_model_time(bf16_pick(p.M, p.n_count, terms), p.M, p.n_count, terms) >
+                         bf16_model_time(bf16_pick(p.M - rem, p.n_count, terms), p.M - rem, p.n_count,
+                                         terms);
+  const int rows = split ? p.M - rem : p.M;
+  if (split) {
+    GemmParams t = p;
+    t.x = p.x + (int64_t)rows * p.stride_x;
+    t.out = p.out != nullptr ? p.out + (int64_t)rows * p.stride_out : nullptr;
+    t.M = rem;
+    const int st = launch_strict_tail(t, epi, e, ep, row0 + rows, stream);
+    if (st != kOk) return st;
+  }
+  const GemmArgs m = rows_of(a, 0, rows);
+  switch (bf16_pick(rows, p.n_count, terms)) {
+    case 0: return launch_shape<Bf16Large, true>(m, terms, epi, stream);
+    case 1: return launch_shape<Bf16Wide, true>(m, terms, epi, stream);
+    case 2: return launch_shape<Bf16Tall, true>(m, terms, epi, stream);
+    case 3: return launch_shape<Bf16Half, true>(m, terms, epi, stream);
+    default: return launch_shape<Bf16Narrow, true>(m, terms, epi, stream);
+  }
 }
 
 }  // namespace nf24
