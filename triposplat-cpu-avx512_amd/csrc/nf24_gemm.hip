@@ -423,12 +423,15 @@ int launch_cfg(const GemmParams& p, hipStream_t stream, const QkvArgs& e = QkvAr
                    (p.n_count % 2 == 0) && (reinterpret_cast<uintptr_t>(p.code01) % 4 == 0) &&
                    (reinterpret_cast<uintptr_t>(p.q2) % 2 == 0) &&
                    vec_buffers_fit(p, C::BM, C::BK);
-  dim3 grid((unsigned)tiles), block(C::kThreads);
+  // The scalar path's configuration covers the same tiles, possibly with
+  // another K step or wave layout (and so another workgroup size).
+  using S = typename ScalarPathCfg<C>::type;
+  static_assert(S::BM == C::BM && S::BN == C::BN, "the scalar path must cover the same tiles");
+  dim3 grid((unsigned)tiles);
   if (vec)
-    hipLaunchKernelGGL((nf24_gemm_kernel<C, true, kEpi>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((nf24_gemm_kernel<C, true, kEpi>), grid, dim3(C::kThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL((nf24_gemm_kernel<typename ScalarPathCfg<C>::type, false, kEpi>), grid, block, 0,
-                       stream, a);
+    hipLaunchKernelGGL((nf24_gemm_kernel<S, false, kEpi>), grid, dim3(S::kThreads), 0, stream, a);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
