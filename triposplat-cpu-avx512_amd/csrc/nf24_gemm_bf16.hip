@@ -87,12 +87,23 @@ using Bf16Wide = Bf16Cfg<256, 192, 4, 3, 2>;
 using Bf16Small = Bf16Cfg<128, 128, 2, 2>;  // 4 waves, 64 x 64 per wave
 // Where the larger tiles leave CUs idle (measured, bf16x3 / bf16, gated
 // epilogue): 12 waves of 64 x 64 over 192 rows -- the reference's 12288
-// rows at N = 1024, 256 tiles: 114 -> 92 / 77 -> 64 us; 8 waves of 64 x 64
-// over 128 columns -- 8192 x 1024: 79 -> 69 / 56 -> 52 us; 4 waves of
+// rows at N = 1024, 256 tiles: 114 -> 92 / 77 -> 64 us; 256 x 128 (as 8
+// waves of 64 x 64) -- 8192 x 1024: 79 -> 69 / 56 -> 52 us; 4 waves of
 // 32 x 64, two workgroups per CU -- 2048 x 1024: 74 -> 38 / 52 -> 35 us.
 using Bf16Tall = Bf16Cfg<192, 256, 3, 4, 2>;
-using Bf16Half = Bf16Cfg<256, 128, 4, 2, 4>;
+using Bf16Half = Bf16Cfg<256, 128, 8, 2, 2>;
 using Bf16Narrow = Bf16Cfg<128, 64, 4, 1, 2>;
+// 16 waves (four per SIMD) where the accumulators allow them: the 256 x 128
+// tile as 16 waves of 32 x 64 (above; against 8 of 64 x 64, gated: 8192 x
+// 1024 x 1024 69 -> 63 / 57 -> 51 us, 8192 x 4096 x 1024 217 -> 202 / 149 ->
+// 136 us), the 256 x 192 tile as 16 waves of 32 x 96 for every epilogue but
+// QKV (a head per wave): configs[0] in the bench 78.4 -> 75.5 us bf16x3,
+// 48.0 -> 47.6 us bf16.  The kernel is VALU-bound; the fourth wave of a
+// SIMD overlaps more of the decode with the MFMAs.  (192 x 256 as 16 waves
+// of 96 x 32, time -3.5 % at K = 1024 and +0.6 % at 4096: not kept; 256 x
+// 256: 64 accumulators per wave at 16 waves spill.)  Bit-identical: one
+// order per output.
+using Bf16Wide16 = Bf16Cfg<256, 192, 8, 2, 2>;
 
 // bf16 element offset of (row r, chunk c) in a 32-k tile row.
 template <bool kSwz>
@@ -445,7 +456,11 @@ int launch_terms(const GemmArgs& a, int epi, hipStream_t stream) {
       hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpiStore>), grid, block, 0, stream, a);
       break;
     case kEpiQkv:
-      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpiQkv>), grid, block, 0, stream, a);
+      // the QKV epilogue takes one head (64 columns) per wave
+      if constexpr (C::kTN == 64 && C::kNB == 2)
+        hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpiQkv>), grid, block, 0, stream, a);
+      else
+        return kErrDims;
       break;
     case kEpilogueGelu:
       hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpilogueGelu>), grid, block, 0, stream, a);
@@ -476,8 +491,8 @@ struct Bf16Choice {
   int bm, bn, wgs_per_cu, round3, round1;
 };
 constexpr Bf16Choice kBf16Choices[] = {
-    {256, 256, 1, 113, 74}, {256, 192, 1, 85, 58}, {192, 256, 1, 92, 63},
-    {256, 128, 1, 66, 50},  {128, 64, 2, 40, 35}};
+    {256, 256, 1, 113, 74}, {256, 192, 1, 82, 57}, {192, 256, 1, 92, 63},
+    {256, 128, 1, 60, 45},  {128, 64, 2, 40, 35}};
 constexpr int kNumBf16Choices = sizeof(kBf16Choices) / sizeof(kBf16Choices[0]);
 
 int64_t bf16_model_time(int i, int M, int n_count, int terms) {
@@ -545,7 +560,9 @@ int launch_gemm_bf16(const GemmParams& p, int epi, const QkvArgs& e, const GemmE
   const GemmArgs m = rows_of(a, 0, rows);
   switch (bf16_pick(rows, p.n_count, terms)) {
     case 0: return launch_shape<Bf16Large, true>(m, terms, epi, stream);
-    case 1: return launch_shape<Bf16Wide, true>(m, terms, epi, stream);
+    case 1:
+      if (epi == kEpiQkv) return launch_shape<Bf16Wide, true>(m, terms, epi, stream);
+      return launch_shape<Bf16Wide16, true>(m, terms, epi, stream);
     case 2: return launch_shape<Bf16Tall, true>(m, terms, epi, stream);
     case 3: return launch_shape<Bf16Half, true>(m, terms, epi, stream);
     default: return launch_shape<Bf16Narrow, true>(m, terms, epi, stream);
