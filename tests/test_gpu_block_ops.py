@@ -116,12 +116,15 @@ def test_fused_layernorm_modulate_and_head_norm(oracle, cuda):
 @pytest.mark.parametrize("M,K,N", [(600, 256, 1024), (16384, 1024, 4096), (3000, 4096, 1024), (20, 128, 96),
                                    (18432, 1024, 1024),   # whole-round split inside the second gate batch
                                    (16386, 1024, 1024),   # 2-row tail tile inside the second gate batch
-                                   (8194, 1024, 1024)])   # 256 x 128 tiles + the 2-row tail
+                                   (8194, 1024, 1024),    # 256 x 128 tiles + the 2-row tail
+                                   (17, 256, 1024),       # few rows on the 32-row skinny tile
+                                   (6, 4096, 1024),       # few rows on the K-split few-row kernel
+                                   (32, 1024, 3072)])
 def test_gemm_epilogues(oracle, cuda, M, K, N):
     """GELU / gated-residual / add epilogues == NF24 Linear then the separate
-    elementwise kernel (bit for bit when both use the same GEMM tile, M > 32);
-    at M <= 32 the epilogue path uses the MFMA tile instead of the few-row
-    kernel, so it is checked against the oracle within the GEMM bound."""
+    elementwise kernel, bit for bit, at every M (at M <= 32 the epilogue call
+    runs the plain few-row call and then the epilogue, as a row tail does);
+    at M <= 32 also against the oracle within the GEMM bound."""
     import torch
     from tsplat import block_ops as bo
     from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
@@ -141,17 +144,16 @@ def test_gemm_epilogues(oracle, cuda, M, K, N):
     y_gelu = bo.nf24_linear_epilogue(*args, bo.EPILOGUE_GELU)
     y_gated = bo.nf24_linear_epilogue(*args, bo.EPILOGUE_GATED, out=base.clone(), gate=gate)
     y_add = bo.nf24_linear_epilogue(*args, bo.EPILOGUE_ADD, out=base.clone())
-    if M > 32:
-        lin = nf24_linear(*args)
-        exp_gelu = bo.gelu_tanh(lin)
-        exp_gated = base.clone().view(B, M // B, N)
-        bo.residual(exp_gated, lin.clone().view(B, M // B, N), gate.contiguous())
-        exp_add = bo.add_inplace(base.clone(), lin)
-        torch.cuda.synchronize(cuda)
-        assert torch.equal(y_gelu, exp_gelu)
-        assert torch.equal(y_gated, exp_gated.view(M, N))
-        assert torch.equal(y_add, exp_add)
-    else:
+    lin = nf24_linear(*args)
+    exp_gelu = bo.gelu_tanh(lin)
+    exp_gated = base.clone().view(B, M // B, N)
+    bo.residual(exp_gated, lin.clone().view(B, M // B, N), gate.contiguous())
+    exp_add = bo.add_inplace(base.clone(), lin)
+    torch.cuda.synchronize(cuda)
+    assert torch.equal(y_gelu, exp_gelu)
+    assert torch.equal(y_gated, exp_gated.view(M, N))
+    assert torch.equal(y_add, exp_add)
+    if M <= 32:
         xh = x.cpu().numpy()
         c01, q2, s, bh = (t.cpu().numpy() for t in (codes[0], codes[1], scales[0], b))
         lin = oracle.nf24_gemm(xh, c01, q2, s, bh)

@@ -154,6 +154,76 @@ def test_bf16_tail_rows_bitwise(oracle, cuda, hiplib, precision, M, K, N):
 
 
 @pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+@pytest.mark.parametrize("epilogue", [2, 3, 4])
+def test_bf16_epilogue_tail_split_bitwise(oracle, cuda, hiplib, precision, epilogue):
+    """The reference's 12294 rows at N = 1024 in a bf16 mode: the 6 rows past
+    12288 would add a round of tiles, so they run on the strict few-row path
+    with the same epilogue (GELU, gated residual, add) at their own row
+    positions -- equal, bit for bit, to a strict call over exactly those rows
+    (the gated form reading gate batch 1, where rows 12288-12293 of two
+    batches of 6147 lie) -- while rows 0-12287 equal a call of the mode over
+    exactly them."""
+    import torch
+
+    M, K, N, B = 12294, 256, 1024, 2
+    head_rows = M - M % 256
+    print(f"bf16 epilogue tail {precision} epilogue={epilogue}", flush=True)
+    x, w, b = seeded_linear(700 + epilogue, M, K, N, w_scale=0.02)
+    c01, q2, s = oracle.quantize_nf24_i16(w)
+    r = np.random.default_rng(epilogue)
+    base = r.standard_normal((M, N)).astype(np.float32)
+    gate = r.standard_normal((B, N)).astype(np.float32) if epilogue == 3 else None
+    kw = dict(epilogue=epilogue, out=base if epilogue in (3, 4) else None, gate=gate,
+              rows_per_batch=M // B if epilogue == 3 else 1)
+    got = _run(torch, hiplib, cuda, x, c01, q2, s, b, precision, **kw)
+    kw_head = dict(kw, out=base[:head_rows] if epilogue in (3, 4) else None)
+    head = _run(torch, hiplib, cuda, x[:head_rows], c01, q2, s, b, precision, **kw_head)
+    assert np.array_equal(got[:head_rows].view(np.uint32), head.view(np.uint32))
+    kw_tail = dict(kw, out=base[head_rows:] if epilogue in (3, 4) else None,
+                   gate=gate[1:] if epilogue == 3 else None, rows_per_batch=M)
+    tail = _run(torch, hiplib, cuda, x[head_rows:], c01, q2, s, b, "fp32", **kw_tail)
+    assert np.array_equal(got[head_rows:].view(np.uint32), tail.view(np.uint32))
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+def test_bf16_qkv_tail_split_matches_unfused(cuda, precision):
+    """Fused QKV projection at B = 2, L = 6147 (12294 rows, N = 3072): in
+    bf16x3 the 6 rows past 12288 run the strict path's QKV epilogue at their
+    own token positions (bf16 keeps them in its 256 x 256 grid: three rounds
+    either way); in both modes the whole result equals the same mode's GEMM
+    (whose tail takes the same path) followed by the postprocess kernel, bit
+    for bit."""
+    import torch
+    from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
+    from tsplat.qkv import gemm_nf24_qkv_direct, qkv_rope_rmsnorm_pack
+
+    B, L, H, K = 2, 6147, 16, 256
+    C = H * 64
+    print(f"bf16 qkv tail {precision}", flush=True)
+    g = torch.Generator(device=cuda).manual_seed(6147)
+    x = torch.randn((B * L, K), generator=g, device=cuda)
+    w = torch.randn((3 * C, K), generator=g, device=cuda) * 0.02
+    bias = torch.randn((3 * C,), generator=g, device=cuda) * 0.01
+    codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+    r = np.random.default_rng(L)
+    ang = r.standard_normal((1, L, H, 32)).astype(np.float32)
+    fr = torch.from_numpy(np.stack([np.cos(ang), np.sin(ang)], -1).reshape(1, L, H, 64)).to(cuda)
+    qg = torch.from_numpy((1 + 0.05 * r.standard_normal((H, 64))).astype(np.float32)).to(cuda)
+    kg = torch.from_numpy((1 + 0.05 * r.standard_normal((H, 64))).astype(np.float32)).to(cuda)
+    fused = gemm_nf24_qkv_direct(x, codes[0], codes[1], scales[0], bias, fr, qg, kg, B, L, H,
+                                 precision=precision)
+    proj = nf24_linear(x, codes[0], codes[1], scales[0], bias, precision=precision)
+    strict_tail = nf24_linear(x[B * L - 6:], codes[0], codes[1], scales[0], bias)
+    unfused = qkv_rope_rmsnorm_pack(proj, fr, qg, kg, B, L, H)
+    torch.cuda.synchronize(cuda)
+    if precision == "bf16x3":
+        assert torch.equal(proj[B * L - 6:], strict_tail)   # the tail took the strict path
+    for a_, b_ in zip(fused, unfused):
+        assert bool(torch.isfinite(a_).all())
+        assert torch.equal(a_, b_)
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
 def test_bf16_tile_shapes_bitwise(oracle, cuda, hiplib, precision):
     """Calls the launch model sends to the other tile shapes -- 12288 rows at
     N = 1024 (192 x 256), 8192 (256 x 128), 2048 (128 x 64), 4096 at N = 3072

@@ -308,6 +308,37 @@ def test_kv_bf16_round_probe(oracle, cuda, hiplib, mode):
     assert hiplib.triposplat_qkv_postprocess_bf16_probe_mode() == 0
 
 
+@pytest.mark.parametrize("B,L,H,K,precision", [(1, 1, 2, 64, "fp32"), (1, 7, 4, 256, "fp32"),
+                                                (2, 5, 2, 1024, "fp32"), (1, 16, 16, 1024, "fp32"),
+                                                (2, 16, 4, 128, "fp32"), (1, 32, 2, 256, "fp32"),
+                                                (2, 9, 16, 4096, "bf16x3")])
+def test_qkv_fused_few_rows_match_unfused(cuda, B, L, H, K, precision):
+    """At most 32 rows the fused projection runs the plain few-row GEMM and
+    then the QKV epilogue (in every precision), so it equals the NF24 GEMM
+    followed by the postprocess kernel bit for bit, as at M > 32."""
+    import torch
+    from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
+    from tsplat.qkv import gemm_nf24_qkv_direct, qkv_rope_rmsnorm_pack
+
+    print(f"qkv few rows B={B} L={L} H={H} K={K} {precision}", flush=True)
+    C = H * 64
+    g = torch.Generator(device=cuda).manual_seed(B * 100 + L + K)
+    x = torch.randn((B * L, K), generator=g, device=cuda)
+    w = torch.randn((3 * C, K), generator=g, device=cuda) * 0.02
+    bias = torch.randn((3 * C,), generator=g, device=cuda) * 0.01
+    codes, scales, _ = quantize_nf24_i16_per_output_channel(w)
+    fr = torch.from_numpy(_freqs(1, L, H, L + 3)).to(cuda)
+    qg, kg = (torch.from_numpy(a).to(cuda) for a in _gammas(H, H + 5))
+    fused = gemm_nf24_qkv_direct(x, codes[0], codes[1], scales[0], bias, fr, qg, kg, B, L, H,
+                                 precision=precision)
+    proj = nf24_linear(x, codes[0], codes[1], scales[0], bias, precision=precision)
+    unfused = qkv_rope_rmsnorm_pack(proj, fr, qg, kg, B, L, H)
+    torch.cuda.synchronize(cuda)
+    for a_, b_ in zip(fused, unfused):
+        assert bool(torch.isfinite(a_).all())
+        assert torch.equal(a_, b_)
+
+
 def _sweep_cases(seed, n):
     """Seeded random fused projections: batch, odd and tail-row lengths, head
     counts from 1 to 16, K aligned or ragged, one shared or per-batch

@@ -23,7 +23,6 @@
 
 #include <atomic>
 
-#include <type_traits>
 
 namespace tsplat {
 namespace {
@@ -524,15 +523,9 @@ struct ScalarPathCfg<CfgLarge> {
   using type = GemmCfg<256, 256, 16, 4, 4>;
 };
 using CfgSkinny = GemmCfg<32, 128, 32, 1, 4>;
-using CfgTail = GemmCfg<32, 128, 32, 1, 2>;      // <= 32 rows, QKV epilogue: 64-column waves (a head)
-// <= 32 rows otherwise (whole calls of that size with an epilogue): each
-// wave's cost is its chain of K/2 MFMAs per 32 columns (one wave per SIMD,
-// nothing to overlap), so 32-column waves -- twice the waves of 64-column
-// ones -- finish in ~0.55x the time.
-using CfgTailNarrow = GemmCfg<32, 32, 32, 1, 1>;
-
-template <int kEpi>
-using TailCfg = typename std::conditional<kEpi == kEpiQkv, CfgTail, CfgTailNarrow>::type;
+// Accumulator layout of tail_epilogue_kernel: one 32 x 64 block per wave
+// (64 columns: a head, for the QKV epilogue).
+using CfgTail = GemmCfg<32, 128, 32, 1, 2>;
 
 struct Choice {
   int bm, bn, wgs_per_cu, waves;
@@ -678,9 +671,13 @@ int launch_nf24_gemm(const GemmParams& p, hipStream_t stream) {
 }
 
 namespace {
-// The row tail t (at most kTailRows rows, token index of its row 0 row0) of
-// an epilogue GEMM: bias + x W of its rows by the few-row kernels into the
-// per-stream workspace, then tail_epilogue_kernel.
+// At most kTailRows rows t (token index of its row 0 row0) of an epilogue
+// GEMM -- a whole call of that size or the row tail of a larger one: bias +
+// x W of its rows as a plain call over exactly them computes it (the
+// few-row kernels, or the 32-row tile for 9-32 rows over K <= 256) into the
+// per-stream workspace, then tail_epilogue_kernel.  So few rows with an
+// epilogue equal the plain GEMM of those rows followed by the elementwise
+// step, bit for bit, wherever they sit.
 template <int kEpi>
 int launch_tail_rows(const GemmParams& t, const GemmEpilogueParams& e, const QkvArgs& q, int row0,
                      hipStream_t stream) {
@@ -690,7 +687,8 @@ int launch_tail_rows(const GemmParams& t, const GemmEpilogueParams& e, const Qkv
   GemmParams r = t;
   r.out = raw;
   r.stride_out = t.n_count;
-  const int st = launch_nf24_gemv(r, stream);
+  r.precision = kPrecisionFp32;
+  const int st = launch_nf24_gemm(r, stream);
   if (st != kOk) return st;
   GemmArgs a{t.x, t.code01, t.q2, t.scale, t.bias, t.out,
              t.M, t.K, t.N, t.n_start, t.n_count, t.stride_x, t.stride_out, q,
@@ -709,8 +707,9 @@ int launch_epi_kind(const GemmParams& p, const GemmEpilogueParams& e, hipStream_
     const int st = launch_tail_rows<kEpi>(rows_slice(p, p.M - rem, rem), e, q, row0 + p.M - rem, stream);
     return st != kOk ? st : launch_epi_kind<kEpi>(rows_slice(p, 0, p.M - rem), e, stream, q, row0);
   }
-  // Few rows: the 32-row tile (the epilogues live in the MFMA kernels).
-  if (p.M <= 32) return launch_cfg<TailCfg<kEpi>, kEpi>(p, stream, q, e, row0);
+  // Few rows: the plain few-row path, then the epilogue (a single 32-row
+  // tile would run one chain of K/2 MFMAs per wave: 39-41 us at K = 1024).
+  if (p.M <= 32) return launch_tail_rows<kEpi>(p, e, q, row0, stream);
   if (const int m1 = round_split_rows(p.M, p.n_count)) {
     const int st = launch_epi_kind<kEpi>(rows_slice(p, 0, m1), e, stream, q, row0);
     return st != kOk ? st : launch_epi_kind<kEpi>(rows_slice(p, m1, p.M - m1), e, stream, q, row0 + m1);
