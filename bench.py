@@ -376,7 +376,7 @@ def run_gemm(torch, dev, iters, ref_parity=False):
     (`parity_vs_reference`; the GPU tests bound each output by the fp32
     summation-order bound 2*gamma_(K+1)*sum|terms|)."""
     import numpy as np
-    from tsplat.nf24 import nf24_linear, quantize_nf24_i16_per_output_channel
+    from tsplat.nf24 import bf16_planes, nf24_linear, quantize_nf24_i16_per_output_channel
 
     M, K, N = 4096, 1024, 3072
     x = torch.from_numpy(np.random.default_rng(SEEDS["c1_x"]).standard_normal((M, K), dtype=np.float32)).to(dev)
@@ -409,13 +409,27 @@ def run_gemm(torch, dev, iters, ref_parity=False):
         d = (gout.double() - strict.double())
         p_tf = g_flop / (p_ms * 1e-3) / 1e12
         terms = 3 if precision == "bf16x3" else 1  # MFMA work per algorithmic FLOP
+        decoded = gout.clone()
+        # the same products with the weights' bf16 planes built once
+        # (tsplat.nf24.bf16_planes): no decode in the K loop, same result
+        planes = bf16_planes(codes[0], codes[1], scales[0], precision)
+
+        def step_planes(p=precision):
+            nf24_linear(x, codes[0], codes[1], scales[0], bias, out=gout, precision=p, planes=planes)
+
+        warm_up(torch, step_planes, 0.5)
+        pl_ms = sorted(time_events(torch, step_planes, iters) for _ in range(5))[2]
+        pl_tf = g_flop / (pl_ms * 1e-3) / 1e12
         opt_in[precision] = {
             "ms": p_ms, "tflops": p_tf, "frac_bf16_mfma_peak": terms * p_tf / PEAK_BF16_MFMA,
             "speedup_vs_fp32": g_ms / p_ms,
             "rmse_vs_fp32": float(d.pow(2).mean().sqrt()),
             "rel_rmse_vs_fp32": float(d.pow(2).mean().sqrt() / strict.double().pow(2).mean().sqrt()),
             "max_abs_vs_fp32": float(d.abs().max()),
+            "planes_ms": pl_ms, "planes_frac_bf16_mfma_peak": terms * pl_tf / PEAK_BF16_MFMA,
+            "planes_equal_decoded": bool(torch.equal(gout, decoded)),
         }
+        del planes
     parity = cpu_ref = None
     if ref_parity:
         sys.path.insert(0, str(ROOT / "oracle"))

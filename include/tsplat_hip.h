@@ -325,6 +325,33 @@ int tsplat_gemm_nf24_qkv_direct_ex_async(
     float* q_bhld, float* k_out, float* v_out, int B, int L, int K, int N, int H, int D,
     int L_padded, int frequency_batches, int kv_layout, int precision, int kv_round,
     void* stream);
+/* bf16 planes of a packed weight for the opt-in modes (no counterpart in the
+ * reference): w_hi = bf16(w) and, for precision 2 (bf16x3), w_lo = bf16 of the
+ * exact decode minus w_hi -- the values the bf16 kernels otherwise decode and
+ * split from the codes in every call, once.  bf16 bits, k-blocked: element
+ * (k, n) at ((k / 32) * N + n) * 32 + k % 32, zeros past K; ceil(K / 32) * 32
+ * * N * 2 bytes each; w_lo may be null for precision 1.  -2 for a precision
+ * other than 1 or 2. */
+int tsplat_nf24_bf16_planes_async(const int16_t* code01_t, const int8_t* q2_t, const float* scale,
+                                  int K, int N, int precision, uint16_t* w_hi, uint16_t* w_lo,
+                                  void* stream);
+/* tsplat_nf24_gemm_precision_async / tsplat_gemm_nf24_qkv_direct_ex_async
+ * reading the weights of the bf16 kernels from the planes above (16-byte
+ * aligned; otherwise the codes, same result bit for bit).
+ * The codes are still read where the strict kernels run (fp32, M <= 32 and
+ * row tails).  No counterpart in the reference. */
+int tsplat_nf24_gemm_planes_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,
+                                  const float* scale, const float* bias, float* out, int M, int K,
+                                  int N, int output_start, int output_count, int stride_x,
+                                  int stride_out, int epilogue, const float* gate,
+                                  int64_t gate_stride, int rows_per_batch, int precision,
+                                  const uint16_t* w_hi, const uint16_t* w_lo, void* stream);
+int tsplat_gemm_nf24_qkv_direct_planes_async(
+    const float* x, const int16_t* code01_t, const int8_t* q2_t, const float* scale,
+    const float* bias, const float* frequencies, const float* q_gamma, const float* k_gamma,
+    float* q_bhld, float* k_out, float* v_out, int B, int L, int K, int N, int H, int D,
+    int L_padded, int frequency_batches, int kv_layout, int precision, int kv_round,
+    const uint16_t* w_hi, const uint16_t* w_lo, void* stream);
 
 /* ---------------- flow-block elementwise -------------------------------- */
 /* Bit-identical per element to the reference kernels (same operation order,

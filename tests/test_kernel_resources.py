@@ -61,6 +61,8 @@ REQUIRED = [
     ("nf24_gemm", "GemmCfgILi128ELi64ELi32ELi4ELi1ELi2ELi0ELb1EEELb1ELi3E"),   # gated, 2048 x 1024
     ("nf24_gemm_bf16", "Bf16CfgILi256ELi192ELi8ELi2ELi2EEELi3ELb1ELi0E"),  # bf16x3 configs[0], 16 waves
     ("nf24_gemm_bf16", "Bf16CfgILi256ELi128ELi8ELi2ELi2EEELi3ELb1ELi3E"),  # bf16x3 gated, 8192 x 1024
+    ("nf24_gemm_bf16", "Bf16CfgILi256ELi192ELi8ELi2ELi2EEELi3ELb1ELi0ELb1E"),  # bf16x3 from the weight planes
+    ("nf24_gemm_bf16", "nf24_bf16_planes_kernelILi3E"),                       # the planes builder
 ]
 
 

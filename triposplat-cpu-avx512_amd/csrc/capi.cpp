@@ -108,7 +108,7 @@ using namespace tsplat;
 namespace {
 
 constexpr int kHeadDim = 64;
-constexpr int kAbiVersion = 3;
+constexpr int kAbiVersion = 4;
 
 // Profile of the blocking (reference-named) SDPA calls: calls, host time
 // spent growing the key-split workspace (allocate), the rest of the call up
@@ -221,9 +221,12 @@ int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
                        const float* scale, const float* bias, const float* freqs,
                        const float* qg, const float* kg, float* q, float* pk, float* pv, int B,
                        int L, int K, int N, int H, int D, int Lp, int fb, hipStream_t stream,
-                       int precision = kPrecisionFp32, int kv_layout = 0, int kv_round = 0) {
+                       int precision = kPrecisionFp32, int kv_layout = 0, int kv_round = 0,
+                       const uint16_t* w_hi = nullptr, const uint16_t* w_lo = nullptr,
+                       bool with_planes = false) {
   if (!x || !code01 || !q2 || !scale || !bias || !freqs || !qg || !kg || !q || !pk || !pv)
     return kErrNull;
+  if (with_planes && (!w_hi || (precision == kPrecisionBf16x3 && !w_lo))) return kErrNull;
   if (kv_round < 0 || kv_round > 3) return kErrDims;
   if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
     return kErrDims;
@@ -249,9 +252,15 @@ int qkv_direct_checked(const float* x, const int16_t* code01, const int8_t* q2,
   const int64_t kv_keys = kv_layout == 1 ? L : Lp;
   TSPLAT_CHECK(ptrs.check(pk, (int64_t)B * C * kv_keys * 4));
   TSPLAT_CHECK(ptrs.check(pv, (int64_t)B * C * kv_keys * 4));
+  if (with_planes) {
+    TSPLAT_CHECK(ptrs.check(w_hi, planes_bytes(K, N)));
+    if (precision == kPrecisionBf16x3) TSPLAT_CHECK(ptrs.check(w_lo, planes_bytes(K, N)));
+  }
   // RoPE, RMSNorm and the q / packed k,v stores run in the GEMM's epilogue.
   QkvFusedParams p{{x, code01, q2, scale, bias, nullptr, (int)M, K, N, 0, N, K, N, precision},
                    freqs, qg, kg, q, pk, pv, B, L, H, Lp, fb, kv_layout, kv_round};
+  p.gemm.w_hi = with_planes ? w_hi : nullptr;
+  p.gemm.w_lo = with_planes && precision == kPrecisionBf16x3 ? w_lo : nullptr;
   const int st = launch_nf24_gemm_qkv(p, stream);
   if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
   return st;
@@ -543,6 +552,39 @@ int tsplat_gemm_nf24_qkv_direct_ex_async(
   return qkv_direct_checked(x, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, q_bhld,
                             k_out, v_out, B, L, K, N, H, D, L_padded, frequency_batches,
                             static_cast<hipStream_t>(stream), precision, kv_layout, kv_round);
+}
+
+int tsplat_gemm_nf24_qkv_direct_planes_async(
+    const float* x, const int16_t* code01_t, const int8_t* q2_t, const float* scale,
+    const float* bias, const float* frequencies, const float* q_gamma, const float* k_gamma,
+    float* q_bhld, float* k_out, float* v_out, int B, int L, int K, int N, int H, int D,
+    int L_padded, int frequency_batches, int kv_layout, int precision, int kv_round,
+    const uint16_t* w_hi, const uint16_t* w_lo, void* stream) {
+  return qkv_direct_checked(x, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, q_bhld,
+                            k_out, v_out, B, L, K, N, H, D, L_padded, frequency_batches,
+                            static_cast<hipStream_t>(stream), precision, kv_layout, kv_round, w_hi,
+                            w_lo, true);
+}
+
+int tsplat_nf24_bf16_planes_async(const int16_t* code01_t, const int8_t* q2_t, const float* scale,
+                                  int K, int N, int precision, uint16_t* w_hi, uint16_t* w_lo,
+                                  void* stream) {
+  if (!code01_t || !q2_t || !scale || !w_hi) return kErrNull;
+  if (precision != kPrecisionBf16 && precision != kPrecisionBf16x3) return kErrDims;
+  if (precision == kPrecisionBf16x3 && !w_lo) return kErrNull;
+  if (K <= 0 || N <= 0) return kErrDims;
+  const int64_t count = (int64_t)K * N;
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(code01_t, count * 2));
+  TSPLAT_CHECK(ptrs.check(q2_t, count));
+  TSPLAT_CHECK(ptrs.check(scale, (int64_t)N * 4));
+  TSPLAT_CHECK(ptrs.check(w_hi, planes_bytes(K, N)));
+  if (precision == kPrecisionBf16x3) TSPLAT_CHECK(ptrs.check(w_lo, planes_bytes(K, N)));
+  const int st = launch_nf24_bf16_planes(code01_t, q2_t, scale, K, N, precision, w_hi,
+                                         precision == kPrecisionBf16x3 ? w_lo : nullptr,
+                                         static_cast<hipStream_t>(stream));
+  if (st == kErrLaunch) (void)note(hipErrorLaunchFailure);
+  return st;
 }
 
 // ------------------------------------------------------------------ packer

@@ -136,6 +136,48 @@ int sampler_checked(int op, float* x, const float* a, const float* p, const floa
   return launched(launch_ab2_update(x, a, p, s0, s1, batch, per_batch, stream));
 }
 
+// The NF24 GEMM entries' checks and launch; w_hi / w_lo: the bf16 planes
+// of the weights (tsplat_nf24_bf16_planes_async) or null.
+int gemm_precision_checked(const float* x, const int16_t* code01_t, const int8_t* q2_t,
+                           const float* scale, const float* bias, float* out, int M, int K, int N,
+                           int output_start, int output_count, int stride_x, int stride_out,
+                           int epilogue, const float* gate, int64_t gate_stride,
+                           int rows_per_batch, int precision, const uint16_t* w_hi,
+                           const uint16_t* w_lo, hipStream_t stream) {
+  if (!x || !code01_t || !q2_t || !scale || !bias || !out) return kErrNull;
+  if (M <= 0 || K <= 0 || N <= 0 || output_start < 0 || output_count <= 0) return kErrDims;
+  if (output_start + output_count > N || stride_x < K || stride_out < output_count)
+    return kErrRange;
+  if (epilogue != kEpilogueStore && epilogue != kEpilogueGelu && epilogue != kEpilogueGated &&
+      epilogue != kEpilogueAdd)
+    return kErrDims;
+  if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
+    return kErrDims;
+  DeviceRanges ptrs;
+  TSPLAT_CHECK(ptrs.check(x, ((int64_t)(M - 1) * stride_x + K) * 4));
+  TSPLAT_CHECK(ptrs.check(code01_t, (int64_t)K * N * 2));
+  TSPLAT_CHECK(ptrs.check(q2_t, (int64_t)K * N));
+  TSPLAT_CHECK(ptrs.check(scale, (int64_t)N * 4));
+  TSPLAT_CHECK(ptrs.check(bias, (int64_t)N * 4));
+  TSPLAT_CHECK(ptrs.check(out, ((int64_t)(M - 1) * stride_out + output_count) * 4));
+  if (epilogue == kEpilogueGated) {
+    if (!gate) return kErrNull;
+    if (rows_per_batch <= 0 || gate_stride < N) return kErrRange;
+    const int64_t batches = ((int64_t)M + rows_per_batch - 1) / rows_per_batch;
+    TSPLAT_CHECK(ptrs.check(gate, ((batches - 1) * gate_stride + N) * 4));
+  }
+  if (w_hi) {
+    TSPLAT_CHECK(ptrs.check(w_hi, planes_bytes(K, N)));
+    if (precision == kPrecisionBf16x3) TSPLAT_CHECK(ptrs.check(w_lo, planes_bytes(K, N)));
+  }
+  GemmParams p{x, code01_t, q2_t, scale, bias, out, M, K, N, output_start, output_count,
+               stride_x, stride_out, precision};
+  p.w_hi = w_hi;
+  p.w_lo = precision == kPrecisionBf16x3 ? w_lo : nullptr;
+  GemmEpilogueParams e{epilogue, gate, gate_stride, rows_per_batch > 0 ? rows_per_batch : 1};
+  return launched(launch_nf24_gemm_epilogue(p, e, stream));
+}
+
 }  // namespace
 
 extern "C" {
@@ -290,38 +332,27 @@ int tsplat_ab2_update_async(float* sample, const float* prediction,
                          elements_per_batch, as_stream(stream));
 }
 
+int tsplat_nf24_gemm_planes_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,
+                                  const float* scale, const float* bias, float* out, int M, int K,
+                                  int N, int output_start, int output_count, int stride_x,
+                                  int stride_out, int epilogue, const float* gate,
+                                  int64_t gate_stride, int rows_per_batch, int precision,
+                                  const uint16_t* w_hi, const uint16_t* w_lo, void* stream) {
+  if (!w_hi || (precision == kPrecisionBf16x3 && !w_lo)) return kErrNull;
+  return gemm_precision_checked(x, code01_t, q2_t, scale, bias, out, M, K, N, output_start,
+                                output_count, stride_x, stride_out, epilogue, gate, gate_stride,
+                                rows_per_batch, precision, w_hi, w_lo, as_stream(stream));
+}
+
 int tsplat_nf24_gemm_precision_async(const float* x, const int16_t* code01_t,
                                      const int8_t* q2_t, const float* scale, const float* bias,
                                      float* out, int M, int K, int N, int output_start,
                                      int output_count, int stride_x, int stride_out, int epilogue,
                                      const float* gate, int64_t gate_stride, int rows_per_batch,
                                      int precision, void* stream) {
-  if (!x || !code01_t || !q2_t || !scale || !bias || !out) return kErrNull;
-  if (M <= 0 || K <= 0 || N <= 0 || output_start < 0 || output_count <= 0) return kErrDims;
-  if (output_start + output_count > N || stride_x < K || stride_out < output_count)
-    return kErrRange;
-  if (epilogue != kEpilogueStore && epilogue != kEpilogueGelu && epilogue != kEpilogueGated &&
-      epilogue != kEpilogueAdd)
-    return kErrDims;
-  if (precision != kPrecisionFp32 && precision != kPrecisionBf16 && precision != kPrecisionBf16x3)
-    return kErrDims;
-  DeviceRanges ptrs;
-  TSPLAT_CHECK(ptrs.check(x, ((int64_t)(M - 1) * stride_x + K) * 4));
-  TSPLAT_CHECK(ptrs.check(code01_t, (int64_t)K * N * 2));
-  TSPLAT_CHECK(ptrs.check(q2_t, (int64_t)K * N));
-  TSPLAT_CHECK(ptrs.check(scale, (int64_t)N * 4));
-  TSPLAT_CHECK(ptrs.check(bias, (int64_t)N * 4));
-  TSPLAT_CHECK(ptrs.check(out, ((int64_t)(M - 1) * stride_out + output_count) * 4));
-  if (epilogue == kEpilogueGated) {
-    if (!gate) return kErrNull;
-    if (rows_per_batch <= 0 || gate_stride < N) return kErrRange;
-    const int64_t batches = ((int64_t)M + rows_per_batch - 1) / rows_per_batch;
-    TSPLAT_CHECK(ptrs.check(gate, ((batches - 1) * gate_stride + N) * 4));
-  }
-  GemmParams p{x, code01_t, q2_t, scale, bias, out, M, K, N, output_start, output_count,
-               stride_x, stride_out, precision};
-  GemmEpilogueParams e{epilogue, gate, gate_stride, rows_per_batch > 0 ? rows_per_batch : 1};
-  return launched(launch_nf24_gemm_epilogue(p, e, as_stream(stream)));
+  return gemm_precision_checked(x, code01_t, q2_t, scale, bias, out, M, K, N, output_start,
+                                output_count, stride_x, stride_out, epilogue, gate, gate_stride,
+                                rows_per_batch, precision, nullptr, nullptr, as_stream(stream));
 }
 
 int tsplat_nf24_gemm_epilogue_async(const float* x, const int16_t* code01_t, const int8_t* q2_t,

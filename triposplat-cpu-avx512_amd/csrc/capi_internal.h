@@ -28,6 +28,9 @@ class DeviceRanges {
   uintptr_t hi_[kMaxRanges];
 };
 bool aligned16(const void* p);
+// Bytes of one bf16 weight plane of a [K, N] weight: k-blocked
+// [ceil(K / 32), N, 32] (tsplat_nf24_bf16_planes_async).
+inline int64_t planes_bytes(int K, int N) { return (int64_t)((K + 31) / 32) * N * 64; }
 // Waits for the null stream (the blocking reference-named entry points).
 int sync_null_stream();
 // Argument checks of the SDPA entry points, then launch_sdpa on `stream`;

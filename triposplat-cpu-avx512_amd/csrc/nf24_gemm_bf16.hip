@@ -130,6 +130,7 @@ __device__ __forceinline__ bf16x8 lds_frag(const __bf16* base, int r, int c) {
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef unsigned uintx2 __attribute__((ext_vector_type(2)));
+typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
 
 // hi = bf16(v); lo = bf16(v - hi) (only with three terms).  Pairs go
 // through one v_cvt_pk_bf16_f32 each; the hi values come back to fp32 by a
@@ -197,8 +198,17 @@ __device__ __forceinline__ floatx16 mfma_bf16(const bf16x8& a, const bf16x8& b, 
 // kVec: x rows 16-byte aligned with K % 4 == 0; N, n_start, n_count
 // multiples of 4 with code01 8-byte and q2 4-byte aligned (four columns of
 // one k row per 64-bit / 32-bit load).
-template <class C, int kTerms, bool kVec, int kEpi>
+// kPl: W from the bf16 planes a.w_hi / a.w_lo (kVec only) instead of the
+// codes.  The planes are k-blocked, [ceil(K / 32), N, 32]: the 32 k of a
+// step of one column are 64 contiguous bytes and the columns of a step
+// follow each other, so the units -- (tile column, 8-k chunk), four lanes
+// per column -- make one 16-byte load and one 16-byte LDS store per plane,
+// and a wave reads 1 KB in one run; no decode and no split in the K loop.
+// The planes hold the values the decode path computes, stored where it
+// stores them, so both paths give the same result bit for bit.
+template <class C, int kTerms, bool kVec, int kEpi, bool kPl>
 __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a) {
+  static_assert(!kPl || kVec, "the planes path loads through buffer resources");
   constexpr int kPlanes = kTerms == 3 ? 2 : 1;
   constexpr bool kSwz = kTerms == 3;
   __shared__ __attribute__((aligned(16))) __bf16 xs[2][kPlanes][C::BM * C::BK];
@@ -222,7 +232,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
   float w_sc[C::kWIter][4];
   bool w_ok[C::kWIter][4];
 #pragma unroll
-  for (int j = 0; j < C::kWIter; ++j) {
+  for (int j = 0; j < (kPl ? 0 : C::kWIter); ++j) {
     const int u = tid + j * C::kThreads;
     w_col[j] = 4 * (u % (C::BN / 4));
     w_k[j] = C::WK * (u / (C::BN / 4));
@@ -242,6 +252,34 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
   uint32_t cr[kStages][C::kWIter][C::WK][2];  // k row i: int16 codes of columns 0,1 | 2,3
   uint32_t qr[kStages][C::kWIter][C::WK];     // k row i: int8 codes of columns 0..3
 
+  // kPl: this thread's plane units j (tile column p_col, chunk p_ch) and the
+  // byte offset of the unit at k0 = 0, or kBufOob past n_count.
+  static_assert(C::BK == 32, "the planes are blocked by 32 k");
+  constexpr int kPUnits = C::BN * (C::BK / 8);
+  constexpr int kPIter = (kPUnits + C::kThreads - 1) / C::kThreads;
+  static_assert(kPUnits % 64 == 0, "a partial iteration must cover whole waves");
+  auto p_unit = [&](int j) {
+    return kPUnits % C::kThreads == 0 || j + 1 < kPIter || tid + j * C::kThreads < kPUnits;
+  };
+  int p_col[kPIter], p_ch[kPIter];
+  uint32_t p_off[kPIter];
+  uintx4 phr[kStages][kPIter], plr[kStages][kPIter];
+  __amdgpu_buffer_rsrc_t rph, rpl;
+  if constexpr (kPl) {
+    const int64_t bytes = (int64_t)((a.K + 31) / 32) * a.N * 64;
+    rph = buffer_rsrc(a.w_hi, bytes);
+    if constexpr (kTerms == 3) rpl = buffer_rsrc(a.w_lo, bytes);
+#pragma unroll
+    for (int j = 0; j < kPIter; ++j) {
+      const int u = tid + j * C::kThreads;
+      p_col[j] = u / (C::BK / 8);
+      p_ch[j] = u % (C::BK / 8);
+      const int lc = c0 + p_col[j];
+      p_off[j] = (p_unit(j) && lc < a.n_count) ? (uint32_t)(((a.n_start + lc) * 32 + 8 * p_ch[j]) * 2)
+                                                 : kBufOob;
+    }
+  }
+
   // kVec: buffer-resource loads from per-thread byte offsets, as in the
   // strict kernel's TileLoader -- rows past M and columns past n_count carry
   // kBufOob, code rows past K lie past the end of the planes.
@@ -250,8 +288,10 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
   if constexpr (kVec) {
     const int rows = min(C::BM, a.M - m0);
     rx = buffer_rsrc(a.x + (int64_t)m0 * a.stride_x, ((int64_t)(rows - 1) * a.stride_x + a.K) * 4);
-    rc = buffer_rsrc(a.code01, (int64_t)a.K * a.N * 2);
-    rq = buffer_rsrc(a.q2, (int64_t)a.K * a.N);
+    if constexpr (!kPl) {
+      rc = buffer_rsrc(a.code01, (int64_t)a.K * a.N * 2);
+      rq = buffer_rsrc(a.q2, (int64_t)a.K * a.N);
+    }
 #pragma unroll
     for (int j = 0; j < C::kXIter; ++j) {
       const int idx = tid + j * C::kThreads;
@@ -259,7 +299,7 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
       x_off[j] = row < rows ? (uint32_t)(row * a.stride_x + 4 * (idx % (C::BK / 4))) * 4u : kBufOob;
     }
 #pragma unroll
-    for (int j = 0; j < C::kWIter; ++j) {
+    for (int j = 0; j < (kPl ? 0 : C::kWIter); ++j) {
       // all four columns are valid with the first: n_start and n_count are multiples of 4
       const uint32_t e = (uint32_t)(w_k[j] * a.N + a.n_start + c0 + w_col[j]);
       c_off[j] = w_ok[j][0] ? 2u * e : kBufOob;
@@ -279,6 +319,19 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
         xr[S][j] = floatx4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
                            __uint_as_float(v[3])};
+      }
+      if constexpr (kPl) {
+#pragma unroll
+        for (int j = 0; j < kPIter; ++j) {
+          if (!p_unit(j)) continue;
+          // block k0 / 32 starts N * 64 bytes after the previous one; k past K
+          // up to the block's end reads the planes' zero padding
+          const uint32_t off = p_off[j] + 2u * (uint32_t)k0 * (uint32_t)a.N;
+          phr[S][j] = __builtin_bit_cast(uintx4, __builtin_amdgcn_raw_buffer_load_b128(rph, (int)off, 0, 0));
+          if constexpr (kTerms == 3)
+            plr[S][j] = __builtin_bit_cast(uintx4, __builtin_amdgcn_raw_buffer_load_b128(rpl, (int)off, 0, 0));
+        }
+        return;
       }
 #pragma unroll
       for (int j = 0; j < C::kWIter; ++j) {
@@ -353,6 +406,16 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
       const int off = chunk_offset<kSwz>(row, kc >> 1) + 4 * (kc & 1);
       *reinterpret_cast<bf16x4*>(&xs[buf][0][off]) = hi;
       if constexpr (kTerms == 3) *reinterpret_cast<bf16x4*>(&xs[buf][kPlanes - 1][off]) = lo;
+    }
+    if constexpr (kPl) {
+#pragma unroll
+      for (int j = 0; j < kPIter; ++j) {
+        if (!p_unit(j)) continue;
+        const int off = chunk_offset<kSwz>(w_row<kSwz>(p_col[j]), p_ch[j]);
+        *reinterpret_cast<uintx4*>(&ws[buf][0][off]) = phr[S][j];
+        if constexpr (kTerms == 3) *reinterpret_cast<uintx4*>(&ws[buf][kPlanes - 1][off]) = plr[S][j];
+      }
+      return;
     }
 #pragma unroll
     for (int j = 0; j < C::kWIter; ++j) {
@@ -446,30 +509,30 @@ __global__ __launch_bounds__(C::kThreads) void nf24_gemm_bf16_kernel(GemmArgs a)
   }
 }
 
-template <class C, int kTerms, bool kVec>
+template <class C, int kTerms, bool kVec, bool kPl>
 int launch_terms(const GemmArgs& a, int epi, hipStream_t stream) {
   const int64_t tiles = (int64_t)((a.M + C::BM - 1) / C::BM) * ((a.n_count + C::BN - 1) / C::BN);
   if (tiles <= 0 || tiles > 0x7fffffff) return kErrDims;
   const dim3 grid((unsigned)tiles), block(C::kThreads);
   switch (epi) {
     case kEpiStore:
-      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpiStore>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpiStore, kPl>), grid, block, 0, stream, a);
       break;
     case kEpiQkv:
       // the QKV epilogue takes one head (64 columns) per wave
       if constexpr (C::kTN == 64 && C::kNB == 2)
-        hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpiQkv>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpiQkv, kPl>), grid, block, 0, stream, a);
       else
         return kErrDims;
       break;
     case kEpilogueGelu:
-      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpilogueGelu>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpilogueGelu, kPl>), grid, block, 0, stream, a);
       break;
     case kEpilogueGated:
-      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpilogueGated>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpilogueGated, kPl>), grid, block, 0, stream, a);
       break;
     case kEpilogueAdd:
-      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpilogueAdd>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((nf24_gemm_bf16_kernel<C, kTerms, kVec, kEpilogueAdd, kPl>), grid, block, 0, stream, a);
       break;
     default:
       return kErrDims;
@@ -477,9 +540,17 @@ int launch_terms(const GemmArgs& a, int epi, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-template <class C, bool kVec>
+template <class C, bool kVec, bool kPl = false>
 int launch_shape(const GemmArgs& a, int terms, int epi, hipStream_t stream) {
-  return terms == 3 ? launch_terms<C, 3, kVec>(a, epi, stream) : launch_terms<C, 1, kVec>(a, epi, stream);
+  return terms == 3 ? launch_terms<C, 3, kVec, kPl>(a, epi, stream)
+                    : launch_terms<C, 1, kVec, kPl>(a, epi, stream);
+}
+
+// The vector path's tile shapes with or without the planes.
+template <class C>
+int launch_vec(const GemmArgs& a, int terms, int epi, bool planes, hipStream_t stream) {
+  return planes ? launch_shape<C, true, true>(a, terms, epi, stream)
+                : launch_shape<C, true, false>(a, terms, epi, stream);
 }
 
 // The tile shapes the launch model chooses from: a round of the chip
@@ -525,16 +596,23 @@ GemmArgs rows_of(GemmArgs a, int first, int count) {
 int launch_gemm_bf16(const GemmParams& p, int epi, const QkvArgs& e, const GemmEpilogueParams& ep,
                      int row0, hipStream_t stream) {
   const int terms = p.precision == kPrecisionBf16x3 ? 3 : 1;
-  const GemmArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out,
-                   p.M, p.K, p.N, p.n_start, p.n_count, p.stride_x, p.stride_out, e,
-                   ep.gate, ep.gate_stride, ep.rows_per_batch, row0};
+  GemmArgs a{p.x, p.code01, p.q2, p.scale, p.bias, p.out,
+             p.M, p.K, p.N, p.n_start, p.n_count, p.stride_x, p.stride_out, e,
+             ep.gate, ep.gate_stride, ep.rows_per_batch, row0};
+  a.w_hi = p.w_hi;
+  a.w_lo = p.w_lo;
   const bool vec = (reinterpret_cast<uintptr_t>(p.x) % 16 == 0) && (p.stride_x % 4 == 0) &&
                    (p.K % 4 == 0) && (p.N % 4 == 0) && (p.n_start % 4 == 0) &&
                    (p.n_count % 4 == 0) && (reinterpret_cast<uintptr_t>(p.code01) % 8 == 0) &&
                    (reinterpret_cast<uintptr_t>(p.q2) % 4 == 0) &&
                    vec_buffers_fit(p, Bf16Large::BM, Bf16Large::BK);
+  // The planes replace the codes in the K loop on the vector path when they
+  // are 16-byte aligned; otherwise the kernels decode the codes (same result).
+  const bool planes = vec && p.w_hi != nullptr &&
+                      reinterpret_cast<uintptr_t>(p.w_hi) % 16 == 0 &&
+                      (terms == 1 || (p.w_lo != nullptr && reinterpret_cast<uintptr_t>(p.w_lo) % 16 == 0));
   if (!vec) return launch_shape<Bf16Small, false>(a, terms, epi, stream);
-  if (p.M < 256 || p.n_count < 256) return launch_shape<Bf16Small, true>(a, terms, epi, stream);
+  if (p.M < 256 || p.n_count < 256) return launch_vec<Bf16Small>(a, terms, epi, planes, stream);
   // Rows past the last multiple of 256 that number at most 32 stay in the
   // grid when they add no modelled time (M = 2818, N = 3072: 12 row bands
   // of 256 x 192 tiles, one round either way), else they run on the strict
@@ -559,15 +637,78 @@ int launch_gemm_bf16(const GemmParams& p, int epi, const QkvArgs& e, const GemmE
   }
   const GemmArgs m = rows_of(a, 0, rows);
   switch (bf16_pick(rows, p.n_count, terms)) {
-    case 0: return launch_shape<Bf16Large, true>(m, terms, epi, stream);
+    case 0: return launch_vec<Bf16Large>(m, terms, epi, planes, stream);
     case 1:
-      if (epi == kEpiQkv) return launch_shape<Bf16Wide, true>(m, terms, epi, stream);
-      return launch_shape<Bf16Wide16, true>(m, terms, epi, stream);
-    case 2: return launch_shape<Bf16Tall, true>(m, terms, epi, stream);
-    case 3: return launch_shape<Bf16Half, true>(m, terms, epi, stream);
-    default: return launch_shape<Bf16Narrow, true>(m, terms, epi, stream);
+      if (epi == kEpiQkv) return launch_vec<Bf16Wide>(m, terms, epi, planes, stream);
+      return launch_vec<Bf16Wide16>(m, terms, epi, planes, stream);
+    case 2: return launch_vec<Bf16Tall>(m, terms, epi, planes, stream);
+    case 3: return launch_vec<Bf16Half>(m, terms, epi, planes, stream);
+    default: return launch_vec<Bf16Narrow>(m, terms, epi, planes, stream);
   }
 }
 
 }  // namespace nf24
+
+namespace {
+
+// The bf16 planes of a packed weight, as split_w forms them in the K loop:
+// w = fp32((int32)q01 * 256 + q2) * scale (one rounding, no contraction),
+// hi = bf16(w), lo = bf16(fma(p, scale, -hi)); k-blocked [ceil(K / 32), N,
+// 32] with zeros past K.  64 x 64 tiles through LDS: the codes [K, N] are
+// read along n, the planes written along k.
+constexpr int kPlaneTile = 64;
+template <int kTerms>
+__global__ __launch_bounds__(256) void nf24_bf16_planes_kernel(const int16_t* code01, const int8_t* q2,
+                                                               const float* scale, int K, int N,
+                                                               uint16_t* w_hi, uint16_t* w_lo) {
+  __shared__ uint16_t th[kPlaneTile][kPlaneTile + 2];
+  __shared__ uint16_t tl[kTerms == 3 ? kPlaneTile : 1][kPlaneTile + 2];
+  const int n0 = blockIdx.x * kPlaneTile, k0 = blockIdx.y * kPlaneTile;
+  const int tx = threadIdx.x % kPlaneTile, ty = threadIdx.x / kPlaneTile;
+  for (int kk = ty; kk < kPlaneTile; kk += 256 / kPlaneTile) {
+    const int k = k0 + kk, n = n0 + tx;
+    uint16_t h = 0, l = 0;
+    if (k < K && n < N) {
+#pragma clang fp contract(off)
+      const int64_t off = (int64_t)k * N + n;
+      const float p = (float)((int32_t)code01[off] * 256 + (int32_t)q2[off]);
+      const float s = scale[n];
+      const float w = p * s;
+      const __bf16 hb = (__bf16)w;
+      h = __builtin_bit_cast(uint16_t, hb);
+      if constexpr (kTerms == 3) l = __builtin_bit_cast(uint16_t, (__bf16)__builtin_fmaf(p, s, -(float)hb));
+    }
+    th[tx][kk] = h;
+    if constexpr (kTerms == 3) tl[tx][kk] = l;
+  }
+  __syncthreads();
+  const int k32 = (K + 31) / 32 * 32;
+  for (int nn = ty; nn < kPlaneTile; nn += 256 / kPlaneTile) {
+    const int n = n0 + nn, k = k0 + tx;
+    if (n < N && k < k32) {
+      const int64_t off = ((int64_t)(k / 32) * N + n) * 32 + k % 32;
+      w_hi[off] = th[nn][tx];
+      if constexpr (kTerms == 3) w_lo[off] = tl[nn][tx];
+    }
+  }
+}
+
+}  // namespace
+
+int launch_nf24_bf16_planes(const int16_t* code01, const int8_t* q2, const float* scale, int K, int N,
+                            int precision, uint16_t* w_hi, uint16_t* w_lo, hipStream_t stream) {
+  if (K <= 0 || N <= 0 || (K + kPlaneTile - 1) / kPlaneTile > 65535) return kErrDims;
+  // the tiles cover the zero padding of the last 32-k block as well
+  const dim3 grid((unsigned)((N + kPlaneTile - 1) / kPlaneTile), (unsigned)((K + kPlaneTile - 1) / kPlaneTile));
+  if (precision == kPrecisionBf16x3)
+    hipLaunchKernelGGL(nf24_bf16_planes_kernel<3>, grid, dim3(256), 0, stream, code01, q2, scale, K, N, w_hi,
+                       w_lo);
+  else if (precision == kPrecisionBf16)
+    hipLaunchKernelGGL(nf24_bf16_planes_kernel<1>, grid, dim3(256), 0, stream, code01, q2, scale, K, N, w_hi,
+                       w_lo);
+  else
+    return kErrDims;
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
 }  // namespace tsplat

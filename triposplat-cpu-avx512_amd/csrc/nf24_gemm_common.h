@@ -54,6 +54,9 @@ struct GemmArgs {
   int row0;  // global index of row 0 of x / out (the epilogues' token mapping)
   // XCD blocking of the tile grid (xcd_grid): 0, or pm x pn = 8 rectangles
   int xcd_pm, xcd_pn;
+  // bf16 planes of the weights (GemmParams::w_hi / w_lo), or null
+  const uint16_t* w_hi = nullptr;
+  const uint16_t* w_lo = nullptr;
 };
 
 // Tile (row band, column band) of workgroup `id` in a grid of tiles_m x

@@ -32,8 +32,18 @@ struct GemmParams {
   int n_start, n_count;
   int stride_x, stride_out;
   int precision = kPrecisionFp32;
+  // Opt-in bf16 modes: the weights split once into bf16 planes [N, K]
+  // (k-contiguous; launch_nf24_bf16_planes), w_hi = bf16(w) and, for bf16x3,
+  // w_lo = bf16(w - w_hi) -- the values the kernels otherwise decode and
+  // split from the codes in every call.  Null: decode the codes.
+  const uint16_t* w_hi = nullptr;
+  const uint16_t* w_lo = nullptr;
 };
 int launch_nf24_gemm(const GemmParams& p, hipStream_t stream);
+// The bf16 planes of a packed weight [K, N] (codes, scale): w_hi[n * K + k]
+// = bf16(w[k][n]) and, for kPrecisionBf16x3, w_lo likewise (null otherwise).
+int launch_nf24_bf16_planes(const int16_t* code01, const int8_t* q2, const float* scale, int K, int N,
+                            int precision, uint16_t* w_hi, uint16_t* w_lo, hipStream_t stream);
 // Few-row form (1 <= M <= 32), HBM-bound; same result contract.
 int launch_nf24_gemv(const GemmParams& p, hipStream_t stream);
 

@@ -57,6 +57,9 @@ SIGNATURES = {
     "tsplat_nf24_decode_async": ([_vp] * 4 + [_i] * 3 + [_vp], _i),
     "tsplat_nf24_gemm_epilogue_async": ([_vp] * 6 + [_i] * 8 + [_vp, _i64, _i, _vp], _i),
     "tsplat_nf24_gemm_precision_async": ([_vp] * 6 + [_i] * 8 + [_vp, _i64, _i, _i, _vp], _i),
+    "tsplat_nf24_gemm_planes_async": ([_vp] * 6 + [_i] * 8 + [_vp, _i64, _i, _i, _vp, _vp, _vp], _i),
+    "tsplat_nf24_bf16_planes_async": ([_vp] * 3 + [_i] * 3 + [_vp] * 3, _i),
+    "tsplat_gemm_nf24_qkv_direct_planes_async": ([_vp] * 11 + [_i] * 11 + [_vp] * 3, _i),
     "triposplat_layernorm_f32_avx512": ([_vp] * 4 + [_i64, _i, ctypes.c_float, _i, _i], _i),
     "triposplat_multihead_rmsnorm_f32_avx512": ([_vp] * 3 + [_i64, _i, _i, ctypes.c_float, _i], _i),
     "triposplat_rope_complex_f32_avx512": ([_vp] * 3 + [_i64, _i, _i], _i),
@@ -96,11 +99,12 @@ STATUS_TEXT = {
     -8: "needs more scratch than the no-allocation entry point's static buffer",
 }
 
-# tsplat_abi_version() of the library these bindings describe: an entry's
-# argument list changed whenever it moved (ABI 3 put kv_round before the
-# stream argument of the asynchronous QKV entries), so a library reporting
-# another version would read its arguments shifted.
-ABI_VERSION = 3
+# tsplat_abi_version() of the library these bindings describe: it moves
+# whenever an entry's argument list changes (ABI 3 put kv_round before the
+# stream argument of the asynchronous QKV entries: a library reporting another
+# version would read its arguments shifted) or entries are added (ABI 4: the
+# bf16 weight planes).
+ABI_VERSION = 4
 
 _CACHE: dict[str, ctypes.CDLL] = {}
 

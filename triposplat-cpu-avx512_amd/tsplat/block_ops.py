@@ -160,14 +160,14 @@ def silu(x, out=None, library=None):
 
 
 def nf24_linear_epilogue(x2, code01_t, q2_t, scale, bias, epilogue, *, out=None, gate=None,
-                         rows_per_batch=None, precision="fp32", library=None):
+                         rows_per_batch=None, precision="fp32", planes=None, library=None):
     """NF24 Linear with the next elementwise step applied before the store:
     EPILOGUE_GELU -> gelu_tanh(x @ W + b); EPILOGUE_GATED -> out += (x @ W + b) * gate[b];
     EPILOGUE_ADD -> out += x @ W + b.  gate is [B, N] (row stride may exceed N).
-    precision as tsplat.nf24.nf24_linear."""
+    precision and planes as tsplat.nf24.nf24_linear."""
     import torch
 
-    from .nf24 import precision_id
+    from .nf24 import planes_pointers, precision_id
 
     mode = precision_id(precision)
 
@@ -189,6 +189,9 @@ def nf24_linear_epilogue(x2, code01_t, q2_t, scale, bias, epilogue, *, out=None,
             gate.data_ptr() if gate is not None else None, gate_stride, per_batch)
     if mode == 0:
         _call(load_library(library), "tsplat_nf24_gemm_epilogue_async", x2.device, *args)
+    elif planes is not None:
+        _call(load_library(library), "tsplat_nf24_gemm_planes_async", x2.device, *args, mode,
+              *planes_pointers(planes, K, N, mode))
     else:
         _call(load_library(library), "tsplat_nf24_gemm_precision_async", x2.device, *args, mode)
     return out

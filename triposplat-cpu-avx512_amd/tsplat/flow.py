@@ -45,7 +45,7 @@ from dataclasses import dataclass
 from . import block_ops as bo
 from .native_sampler_backend import NativeSamplerBackend
 from .native_sdpa_ctypes import native_sdpa_f32_ex
-from .nf24 import nf24_linear, precision_id, quantize_nf24_i16_per_output_channel
+from .nf24 import bf16_planes, nf24_linear, precision_id, quantize_nf24_i16_per_output_channel
 from .qkv import gemm_nf24_qkv_direct
 
 
@@ -87,6 +87,18 @@ class PackedLinear:
         self.in_features = int(code01_t.shape[0])
         self.out_features = int(code01_t.shape[1])
         self.precision = "fp32"  # GEMM product precision (tsplat.nf24.PRECISIONS)
+        self.planes = None       # bf16 weight planes of self.precision (tsplat.nf24.bf16_planes)
+
+    def set_precision(self, precision, planes=True):
+        """Product precision of this Linear; with planes, a bf16 mode reads
+        the weights from bf16 planes built here once (same results, 2 or 4
+        bytes per weight) instead of decoding the codes in every call."""
+        precision_id(precision)
+        self.precision = precision
+        if precision == "fp32" or not planes:
+            self.planes = None
+        elif self.planes is None or (self.planes[1] is not None) != (precision == "bf16x3"):
+            self.planes = bf16_planes(self.code01_t, self.q2_t, self.scale, precision)
 
     @classmethod
     def random(cls, torch, in_f, out_f, seed, device):
@@ -98,34 +110,36 @@ class PackedLinear:
 
     def __call__(self, x2, out=None, output_start=0, output_count=None):
         return nf24_linear(x2, self.code01_t, self.q2_t, self.scale, self.bias, out=out,
-                           output_start=output_start, output_count=output_count, precision=self.precision)
+                           output_start=output_start, output_count=output_count, precision=self.precision,
+                           planes=self.planes)
 
     def epilogue(self, x2, kind, out=None, gate=None):
         """This Linear with a fused elementwise epilogue (block_ops.EPILOGUE_*)."""
         return bo.nf24_linear_epilogue(x2, self.code01_t, self.q2_t, self.scale, self.bias, kind,
-                                       out=out, gate=gate, precision=self.precision)
+                                       out=out, gate=gate, precision=self.precision, planes=self.planes)
 
     def qkv_direct(self, x2, freqs, q_gamma, k_gamma, B, L, H, kv_layout="packed"):
         """Fused QKV projection + RoPE/RMSNorm (tsplat.qkv.gemm_nf24_qkv_direct)."""
         return gemm_nf24_qkv_direct(x2, self.code01_t, self.q2_t, self.scale, self.bias, freqs,
                                     q_gamma, k_gamma, B, L, H, precision=self.precision,
-                                    kv_layout=kv_layout)
+                                    kv_layout=kv_layout, planes=self.planes)
 
     def host(self):
         return {k: getattr(self, k).cpu().numpy() for k in ("code01_t", "q2_t", "scale", "bias")}
 
 
-def set_model_precision(model, precision, include=("blocks",)):
+def set_model_precision(model, precision, include=("blocks",), planes=True):
     """Product precision of a flow model ("fp32" strict, or the opt-in
     "bf16" / "bf16x3"): "blocks" in include sets the block Linears, "io" the
     timestep / input / output Linears, "attention" the SDPA products (Q K^T
-    and P V); what include does not name stays fp32."""
+    and P V); what include does not name stays fp32.  planes: the bf16-mode
+    Linears build their bf16 weight planes now (PackedLinear.set_precision)."""
     precision_id(precision)
     for blk in model.blocks:
         for lin in blk.lin.values():
-            lin.precision = precision if "blocks" in include else "fp32"
+            lin.set_precision(precision if "blocks" in include else "fp32", planes)
     for lin in (model.t_fc1, model.t_fc2, model.adaln, model.input_layer, model.out_layer):
-        lin.precision = precision if "io" in include else "fp32"
+        lin.set_precision(precision if "io" in include else "fp32", planes)
     model.precision = precision if "blocks" in include else "fp32"
     model.attention_precision = precision if "attention" in include else "fp32"
     return model
@@ -201,8 +215,8 @@ class FlowModel:
         self.precision = "fp32"
         self.attention_precision = "fp32"
 
-    def set_precision(self, precision, include=("blocks",)):
-        return set_model_precision(self, precision, include)
+    def set_precision(self, precision, include=("blocks",), planes=True):
+        return set_model_precision(self, precision, include, planes)
 
     def freqs(self, L):
         if L not in self._freqs:

@@ -103,8 +103,8 @@ class JointFlowModel:
         self.precision = "fp32"
         self.attention_precision = "fp32"
 
-    def set_precision(self, precision, include=("blocks",)):
-        return set_model_precision(self, precision, include)
+    def set_precision(self, precision, include=("blocks",), planes=True):
+        return set_model_precision(self, precision, include, planes)
 
     def freqs(self, L, Lc):
         if (L, Lc) not in self._freqs:

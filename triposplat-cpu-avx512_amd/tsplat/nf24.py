@@ -170,12 +170,59 @@ def precision_id(precision) -> int:
     return PRECISIONS[precision]
 
 
+def bf16_planes(code01_t, q2_t, scale, precision="bf16x3", library=None):
+    """The bf16 planes of a packed weight for the opt-in modes
+    (tsplat_nf24_bf16_planes_async): (w_hi, w_lo), bfloat16, w_hi = bf16(w)
+    and for "bf16x3" w_lo = bf16 of the exact decode minus w_hi (None for
+    "bf16") -- what the bf16 kernels otherwise decode and split from the
+    codes in every call.  k-blocked: [ceil(K / 32), N, 32], weight (k, n) at
+    [k // 32, n, k % 32], zeros past K (planes_to_kn gives [K, N]).  Pass them
+    as planes= to nf24_linear, block_ops.nf24_linear_epilogue and
+    qkv.gemm_nf24_qkv_direct: same results bit for bit, 2 (bf16) or 4
+    (bf16x3) bytes per weight."""
+    import torch
+
+    mode = precision_id(precision)
+    if mode == 0:
+        raise ValueError("the bf16 planes serve precision 'bf16' or 'bf16x3'")
+    K, N = (int(s) for s in code01_t.shape)
+    w_hi = torch.empty(((K + 31) // 32, N, 32), dtype=torch.bfloat16, device=code01_t.device)
+    w_lo = torch.empty_like(w_hi) if mode == 2 else None
+    lib = load_library(library)
+    with torch.cuda.device(code01_t.device):
+        status = lib.tsplat_nf24_bf16_planes_async(
+            code01_t.data_ptr(), q2_t.data_ptr(), scale.data_ptr(), K, N, mode, w_hi.data_ptr(),
+            w_lo.data_ptr() if w_lo is not None else None, current_stream_handle(code01_t.device))
+    check_status(status, "tsplat_nf24_bf16_planes_async")
+    return w_hi, w_lo
+
+
+def planes_to_kn(plane, K):
+    """A k-blocked plane of bf16_planes as a [K, N] tensor (a view's copy)."""
+    kb, N, _ = (int(s) for s in plane.shape)
+    return plane.permute(0, 2, 1).reshape(kb * 32, N)[:K]
+
+
+def planes_pointers(planes, K, N, mode):
+    """(w_hi, w_lo) device pointers of bf16_planes' result for a call of
+    precision id `mode` over a [K, N] weight."""
+    import torch
+
+    w_hi, w_lo = planes
+    shape = ((K + 31) // 32, N, 32)
+    for name, t in (("w_hi", w_hi), ("w_lo", w_lo if mode == 2 else w_hi)):
+        if t is None or t.dtype != torch.bfloat16 or tuple(t.shape) != shape or not t.is_contiguous():
+            raise ValueError(f"planes: {name} must be a contiguous bfloat16 {list(shape)} tensor (bf16_planes)")
+    return w_hi.data_ptr(), (w_lo.data_ptr() if mode == 2 else None)
+
+
 def nf24_linear(x2, code01_t, q2_t, scale, bias, *, output_start=0, output_count=None, out=None,
-                precision="fp32", library=None):
+                precision="fp32", planes=None, library=None):
     """out[M, count] = bias[start:start+count] + x2[M, K] @ W[:, start:start+count]
     on torch's current stream.  x2 must be a contiguous fp32 GPU matrix.
     precision "bf16" / "bf16x3" selects the opt-in bf16-MFMA products
-    (include/tsplat_hip.h); M <= 32 always runs the strict kernels."""
+    (include/tsplat_hip.h); M <= 32 always runs the strict kernels.  planes:
+    bf16_planes(...) of this weight for those modes (same result)."""
     import torch
 
     mode = precision_id(precision)
@@ -191,6 +238,10 @@ def nf24_linear(x2, code01_t, q2_t, scale, bias, *, output_start=0, output_count
                 out.data_ptr(), M, K, N, int(output_start), count, int(x2.stride(0)), int(out.stride(0)))
         if mode == 0:
             name, status = "tsplat_nf24_gemm_async", lib.tsplat_nf24_gemm_async(*args, stream)
+        elif planes is not None:
+            name = "tsplat_nf24_gemm_planes_async"
+            status = lib.tsplat_nf24_gemm_planes_async(*args, 0, None, 0, 1, mode,
+                                                       *planes_pointers(planes, K, N, mode), stream)
         else:
             name = "tsplat_nf24_gemm_precision_async"
             status = lib.tsplat_nf24_gemm_precision_async(*args, 0, None, 0, 1, mode, stream)

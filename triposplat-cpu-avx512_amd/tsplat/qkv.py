@@ -68,15 +68,16 @@ def qkv_rope_rmsnorm_pack(qkv, frequencies, q_gamma, k_gamma, B, L, H, *, L_padd
 
 
 def gemm_nf24_qkv_direct(x2, code01_t, q2_t, scale, bias, frequencies, q_gamma, k_gamma, B, L, H, *,
-                         L_padded=None, precision="fp32", kv_layout="packed", kv_round=None, library=None):
+                         L_padded=None, precision="fp32", kv_layout="packed", kv_round=None, planes=None,
+                         library=None):
     """NF24 QKV projection of x2 [B*L, K] (N = 3*H*64) then the postprocess;
-    precision of the projection as tsplat.nf24.nf24_linear.  kv_layout
-    "packed" returns k/v [B, H, 64, L_padded] (the reference's layout),
-    "bhld" returns k/v [B, H, L, 64] like q (what the unpacked SDPA reads).
-    kv_round: the bf16 probe mode of the stored k/v (None = exact)."""
+    precision (and planes) of the projection as tsplat.nf24.nf24_linear.
+    kv_layout "packed" returns k/v [B, H, 64, L_padded] (the reference's
+    layout), "bhld" returns k/v [B, H, L, 64] like q (what the unpacked SDPA
+    reads).  kv_round: the bf16 probe mode of the stored k/v (None = exact)."""
     import torch
 
-    from .nf24 import precision_id
+    from .nf24 import planes_pointers, precision_id
 
     mode = precision_id(precision)
     rnd = kv_round_id(kv_round)
@@ -98,6 +99,11 @@ def gemm_nf24_qkv_direct(x2, code01_t, q2_t, scale, bias, frequencies, q_gamma, 
         stream = current_stream_handle(x2.device)
         if mode == 0 and kv_layout == "packed" and rnd == 0:
             name, status = "tsplat_gemm_nf24_qkv_direct_async", lib.tsplat_gemm_nf24_qkv_direct_async(*args, stream)
+        elif mode != 0 and planes is not None:
+            name = "tsplat_gemm_nf24_qkv_direct_planes_async"
+            ptrs = planes_pointers(planes, int(x2.shape[1]), int(code01_t.shape[1]), mode)
+            status = lib.tsplat_gemm_nf24_qkv_direct_planes_async(*args, int(kv_layout == "bhld"), mode, rnd,
+                                                                    *ptrs, stream)
         else:
             name = "tsplat_gemm_nf24_qkv_direct_ex_async"
             status = lib.tsplat_gemm_nf24_qkv_direct_ex_async(*args, int(kv_layout == "bhld"), mode, rnd,
