@@ -163,3 +163,32 @@ def test_flow_model_planes_bitwise(cuda):
     assert all(lin.planes is not None for lin in model.blocks[0].lin.values())
     for a_, b_ in zip(outs[0], outs[1]):
         assert torch.equal(a_, b_)
+
+
+def test_linear_patch_planes_bitwise(cuda):
+    """The reference-named Linear patch in bf16x3 with and without the weight
+    planes: same outputs bit for bit (forward and the range hook), the planes
+    recorded in the metadata."""
+    import copy
+
+    import torch
+    from torch import nn
+    from tsplat.native_linear_rnf8_patch import apply_triposplat_native_rnf8_avx512_patch
+
+    torch.manual_seed(5)
+    base = nn.Sequential(nn.Linear(256, 512), nn.GELU(approximate="tanh"), nn.Linear(512, 256)).to(cuda).eval()
+    x = torch.randn(300, 256, device=cuda)
+    outs, metas, models = [], [], []
+    for planes in (False, True):
+        model = copy.deepcopy(base)
+        metas.append(apply_triposplat_native_rnf8_avx512_patch(
+            model, enabled=True, include_regex=r".*", strict=True, stages=3, residual_mode="nf24_i16",
+            precision="bf16x3", bf16_planes=planes))
+        with torch.inference_mode():
+            outs.append((model(x), model[0]._native_avx512_forward_range(x, 128, 256)))
+        models.append(model)
+    torch.cuda.synchronize(cuda)
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    assert metas[1]["gemm_bf16_planes"] and not metas[0]["gemm_bf16_planes"]
+    assert metas[1]["bf16_plane_bytes"] == (256 * 512 + 512 * 256) * 4
+    assert hasattr(models[1][0], "_native_rnf8_bf16_lo") and not hasattr(models[0][0], "_native_rnf8_bf16_hi")

@@ -29,6 +29,7 @@ from ._lib import library_path as _default_library_path
 from ._lib import load_library
 from .nf24 import (RESIDUAL_MODE_ID, make_nf8_codebook, nf24_linear, precision_id,
                    quantize_nf24_i16_per_output_channel)
+from .nf24 import bf16_planes as make_bf16_planes
 
 _MODE_NAMES = {0: "nf8", 1: "symmetric_int8", 4: "nf24_i16"}
 
@@ -47,10 +48,14 @@ def apply_triposplat_native_rnf8_avx512_patch(
     stages: int = 2,
     residual_mode: str = "nf8",
     precision: str = "fp32",
+    bf16_planes: bool = True,
 ) -> dict[str, Any]:
     """``precision`` (no counterpart in the reference): "fp32" (strict, the
     default) or the opt-in bf16-MFMA products "bf16" / "bf16x3" of
-    tsplat.nf24.nf24_linear; it is recorded in the returned metadata."""
+    tsplat.nf24.nf24_linear; it is recorded in the returned metadata.  With
+    a bf16 mode and ``bf16_planes``, each Linear's weight planes
+    (tsplat.nf24.bf16_planes) are built here and read by its calls instead of
+    decoding the codes (same results; 2 or 4 more bytes per weight)."""
     if not enabled:
         return {"enabled": False}
     precision_id(precision)
@@ -106,7 +111,8 @@ def apply_triposplat_native_rnf8_avx512_patch(
     prepacked_manifest = getattr(flow_model, "_native_rnf8_prepacked_manifest", None)
     if prepacked_manifest is not None and (stages != 3 or residual_mode != "nf24_i16"):
         raise ValueError("prepacked NF24 int16 requires stages=3 and residual_mode=nf24_i16")
-    original_bytes = packed_bytes = weight_elements = 0
+    original_bytes = packed_bytes = weight_elements = plane_bytes = 0
+    use_planes = bool(bf16_planes) and precision != "fp32"
     weighted_squared_error = 0.0
     max_abs_error = 0.0
 
@@ -149,10 +155,13 @@ def apply_triposplat_native_rnf8_avx512_patch(
     def call(module, module_name, x2, start, count, is_range):
         started = time.perf_counter()
         try:
+            planes = None
+            if use_planes:
+                planes = (module._native_rnf8_bf16_hi, getattr(module, "_native_rnf8_bf16_lo", None))
             out = nf24_linear(x2, module._native_rnf8_codes0_t, module._native_rnf8_codes1_t,
                               module._native_rnf8_scales0, module._native_rnf8_bias,
                               output_start=start, output_count=count, precision=precision,
-                              library=lib_path)
+                              planes=planes, library=lib_path)
         except RuntimeError as exc:
             runtime["fallbacks"] += 1
             kind = "range kernel" if is_range else "kernel"
@@ -215,6 +224,13 @@ def apply_triposplat_native_rnf8_avx512_patch(
                 raise RuntimeError(f"prepacked NF24 buffers for {name} must be on the GPU")
             error = item["quantization"]
         module.register_buffer("_native_rnf8_codebook", codebook.to(codes[0].device), persistent=False)
+        if use_planes:
+            w_hi, w_lo = make_bf16_planes(codes[0], codes[1], scales[0], precision, library=lib_path)
+            module.register_buffer("_native_rnf8_bf16_hi", w_hi, persistent=False)
+            plane_bytes += w_hi.numel() * 2
+            if w_lo is not None:
+                module.register_buffer("_native_rnf8_bf16_lo", w_lo, persistent=False)
+                plane_bytes += w_lo.numel() * 2
         module.weight = nn.Parameter(torch.empty(0, dtype=torch.float32, device=codes[0].device), requires_grad=False)
         if module.bias is not None:
             module.bias = nn.Parameter(torch.empty(0, dtype=torch.float32, device=codes[0].device), requires_grad=False)
@@ -244,6 +260,8 @@ def apply_triposplat_native_rnf8_avx512_patch(
         "bits_per_weight": 24,
         "activation_dtype": "float32",
         "gemm_precision": precision,
+        "gemm_bf16_planes": use_planes,
+        "bf16_plane_bytes": plane_bytes,
         "float32_weight_retained": False,
         "library_path": lib_path.as_posix(),
         "optimized_library_path": None if optimized_library_path is None else lib_path.as_posix(),
