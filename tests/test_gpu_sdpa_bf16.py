@@ -126,21 +126,24 @@ def test_bf16_sdpa_small_grid_bound(oracle, cuda, precision, B, H, Lq, Lk, bias,
 
 
 @pytest.mark.parametrize("precision", PRECISIONS)
-@pytest.mark.parametrize("L,Lk,bias,packed", [
-    (8192, 8192, None, False),          # 256 query tiles of 512: the wide grid, no key split
-    (8192, 2048, "per_head", False),    # cross-attention shape with a per-head bias
-    (8192 + 512, 8192 + 512, None, True),   # last round split along the keys, packed K/V
-    (8192 + 512, 8193, "shared", False),    # key split with a ragged key tail and a bias
+@pytest.mark.parametrize("B,L,Lk,bias,packed", [
+    (1, 8192, 8192, None, False),          # 256 query tiles of 512: the wide grid, no key split
+    (1, 8192, 2048, "per_head", False),    # cross-attention shape with a per-head bias
+    (1, 8192 + 512, 8192 + 512, None, True),   # last round split along the keys, packed K/V
+    (1, 8192 + 512, 8193, "shared", False),    # key split with a ragged key tail and a bias
+    # too few query tiles per head for the pre-split pass: K/V staged in the kernel
+    (16, 2048, 2048, None, True),
+    (2, 4096 + 100, 4099, "per_head", False),
 ])
-def test_bf16_sdpa_wide_grid_rows(oracle, cuda, precision, L, Lk, bias, packed):
+def test_bf16_sdpa_wide_grid_rows(oracle, cuda, precision, B, L, Lk, bias, packed):
     import torch
 
     H = 16
-    print(f"sdpa wide {precision} L={L} Lk={Lk} bias={bias} packed={packed}", flush=True)
-    q, k, v = _inputs(L + Lk, 1, H, L, Lk)
+    print(f"sdpa wide {precision} B={B} L={L} Lk={Lk} bias={bias} packed={packed}", flush=True)
+    q, k, v = _inputs(L + Lk, B, H, L, Lk)
     b = _bias(bias, H, Lk, 3)
     got = _run(torch, cuda, q, k, v, precision, b, per_head=bias == "per_head", packed=packed)
-    rows = np.unique(np.concatenate([np.random.default_rng(L).choice(L, 40, replace=False),
+    rows = np.unique(np.concatenate([np.random.default_rng(L).choice(L, 40 if B == 1 else 12, replace=False),
                                      [0, L - 1, L - 512, L - 257]]))
     ref, bound = _bound(oracle, q, k, v, b, precision, rows=rows, splits=16)
     sub = got[:, :, rows]
@@ -193,12 +196,9 @@ def test_bf16_sdpa_config1_vs_strict(oracle, cuda):
                                             (2, 3, 40, 300, "per_head")])
 def test_packed_kv_layout_matches(cuda, precision, B, H, Lq, Lk, bias):
     """Key-contiguous k/v [B,H,64,Lkp] stage the same values into the same
-    LDS positions as [B,H,Lk,64] k/v, so each query row sees the same
-    operations: bit-identical output in every precision (small grid, wide
-    grid with a key-split tail).  The packed bf16x3 wide grid runs 256-query
-    workgroups where [B,H,Lk,64] runs 512, so there the rows of the last
-    head's key-split tail (queries 512.., merged by the combine kernel over
-    a different key partition) agree to rounding and all others bitwise."""
+    LDS positions as [B,H,Lk,64] k/v, on the same tile plan, so each query
+    row sees the same operations: bit-identical output in every precision
+    (small grid, wide grid with a key-split tail)."""
     import torch
     from tsplat.native_sdpa_ctypes import native_sdpa_f32_ex
 
@@ -218,13 +218,7 @@ def test_packed_kv_layout_matches(cuda, precision, B, H, Lq, Lk, bias):
     packed = native_sdpa_f32_ex(qd, kp, vp, kv_packed=True, key_count=Lk, precision=precision, **kw)
     torch.cuda.synchronize(cuda)
     assert bool(torch.isfinite(rows).all())
-    if precision == "bf16x3" and B * H * ((Lq + 511) // 512) >= 256:
-        assert torch.equal(packed[:, :-1], rows[:, :-1])
-        assert torch.equal(packed[:, -1, :512], rows[:, -1, :512])
-        tail = (packed[:, -1, 512:] - rows[:, -1, 512:]).abs().max().item()
-        assert tail <= 1e-5 * float(vd.abs().max()), tail
-    else:
-        assert torch.equal(packed, rows)
+    assert torch.equal(packed, rows)
 
 
 def _sweep_cases(seed, n, max_work=2e8):
@@ -254,3 +248,105 @@ def test_sdpa_bf16_random_case_sweep(oracle, cuda, precision, B, H, Lq, Lk, bias
     got = _run(torch, cuda, q, k, v, precision, bias=b, per_head=bias == "per_head", packed=packed, blhd=blhd)
     ref, bound = _bound(oracle, q, k, v, b, precision)
     _check(got, ref, bound)
+
+
+def _raw(lib, fn, torch, cuda, q, k, v, b, out, precision, blhd, Lk, Lkp, stream=None):
+    """One call of a C-ABI SDPA entry (precision 1 = bf16, 2 = bf16x3)."""
+    B, H, Lq, _ = q.shape
+    st = torch.cuda.current_stream(cuda).cuda_stream if stream is None else stream
+    return getattr(lib, fn)(q.data_ptr(), k.data_ptr(), v.data_ptr(), None if b is None else b.data_ptr(),
+                            out.data_ptr(), B, H, Lq, Lk, 64, int(b is not None), 0 if b is None else Lk,
+                            0 if b is None or b.dim() == 1 else Lk, int(Lkp > 0), Lkp, int(blhd), precision, st)
+
+
+def _workspace_bytes(lib):
+    import ctypes
+
+    vals = [ctypes.c_uint64(0) for _ in range(2)]
+    assert lib.triposplat_sdpa_q8t512_workspace_stats(*[ctypes.byref(x) for x in vals]) == 0
+    return vals[0].value, vals[1].value
+
+
+# (B, H, Lq, Lk, bias, packed, blhd): wide grids with enough query tiles of
+# 512 per head for the pre-split pass (12 with [Lk, 64] k/v, 6 with packed
+# k/v): a ragged key tail with a key-split last round, a per-head bias with
+# BLHD output, a shared bias, packed k/v with and without a bias
+PRESPLIT = [(2, 16, 6144 + 100, 6147, None, False, False),
+            (1, 16, 8192, 8192, "per_head", False, True),
+            (1, 16, 8704, 1000, "shared", False, False),
+            (3, 16, 3100, 3001, "per_head", True, False),
+            (4, 8, 4096, 4096, None, True, True)]
+
+
+@pytest.mark.parametrize("precision", [1, 2])
+@pytest.mark.parametrize("B,H,Lq,Lk,bias,packed,blhd", PRESPLIT)
+def test_bf16_sdpa_presplit_matches_direct(cuda, hiplib, precision, B, H, Lq, Lk, bias, packed, blhd):
+    """The precision entry stages K/V once in a pre-split pass where the
+    no-allocation entry stages them in the kernel: the LDS tiles, the tile
+    plan and so the outputs are the same bit for bit.  The workspace grows
+    to hold the pre-split image (the pass ran)."""
+    import torch
+
+    print(f"presplit {precision} B={B} H={H} Lq={Lq} Lk={Lk} bias={bias} packed={packed} blhd={blhd}",
+          flush=True)
+    g = torch.Generator(device=cuda).manual_seed(Lq + Lk + B)
+    q = torch.nn.functional.normalize(torch.randn((B, H, Lq, 64), generator=g, device=cuda), dim=-1) * 8
+    k = torch.nn.functional.normalize(torch.randn((B, H, Lk, 64), generator=g, device=cuda), dim=-1) * 8
+    v = torch.randn((B, H, Lk, 64), generator=g, device=cuda)
+    b = None
+    if bias == "shared":
+        b = torch.rand((Lk,), generator=g, device=cuda) * -2.0
+    elif bias == "per_head":
+        b = torch.rand((H, Lk), generator=g, device=cuda) * -2.0
+    Lkp = 0
+    if packed:
+        Lkp = -(-Lk // 16) * 16
+        kp = torch.zeros((B, H, 64, Lkp), device=cuda)
+        vp = torch.zeros_like(kp)
+        kp[..., :Lk] = k.transpose(2, 3)
+        vp[..., :Lk] = v.transpose(2, 3)
+        k, v = kp, vp
+    shape = (B, Lq, H, 64) if blhd else (B, H, Lq, 64)
+    pre, direct = (torch.full(shape, float("nan"), device=cuda) for _ in range(2))
+    assert _raw(hiplib, "tsplat_sdpa_precision_async", torch, cuda, q, k, v, b, pre, precision, blhd, Lk, Lkp) == 0
+    assert _raw(hiplib, "tsplat_sdpa_noalloc_async", torch, cuda, q, k, v, b, direct, precision, blhd, Lk,
+                Lkp) == 0
+    torch.cuda.synchronize(cuda)
+    image = B * H * -(-Lk // 64) * (4 if precision == 2 else 2) * 64 * 64 * 2
+    assert _workspace_bytes(hiplib)[1] >= image
+    assert bool(torch.isfinite(pre).all())
+    assert torch.equal(pre, direct)
+
+
+def test_bf16_sdpa_presplit_capture_without_workspace(cuda, hiplib):
+    """Captured on a fresh stream, whose pre-split workspace cannot be
+    allocated under capture, the precision entry stages K/V in the kernel;
+    replays (with eager calls between them) equal the eager pre-split
+    result bit for bit and the capture allocates nothing."""
+    import torch
+
+    B, H, L = 1, 16, 8192   # 256 query tiles of 512: no key split, so no partials workspace
+    g = torch.Generator(device=cuda).manual_seed(11)
+    q, k = (torch.nn.functional.normalize(torch.randn((B, H, L, 64), generator=g, device=cuda), dim=-1) * 8
+            for _ in range(2))
+    v = torch.randn((B, H, L, 64), generator=g, device=cuda)
+    want = torch.empty((B, H, L, 64), device=cuda)
+    assert _raw(hiplib, "tsplat_sdpa_precision_async", torch, cuda, q, k, v, None, want, 2, 0, L, 0) == 0
+    torch.cuda.synchronize(cuda)
+    out = torch.empty_like(want)
+    other = torch.empty_like(want)
+    s = torch.cuda.Stream(device=cuda)
+    before = _workspace_bytes(hiplib)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s, capture_error_mode="relaxed"):
+        assert _raw(hiplib, "tsplat_sdpa_precision_async", torch, cuda, q, k, v, None, out, 2, 0, L, 0,
+                    stream=s.cuda_stream) == 0
+    torch.cuda.synchronize(cuda)
+    assert _workspace_bytes(hiplib) == before
+    for _ in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize(cuda)
+        assert torch.equal(out, want)
+        assert _raw(hiplib, "tsplat_sdpa_precision_async", torch, cuda, k, q, v, None, other, 2, 0, L, 0) == 0
+        torch.cuda.synchronize(cuda)

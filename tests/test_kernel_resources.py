@@ -28,12 +28,14 @@ BUDGET = {
     # loads from one shared 32-bit offset keep these 8 bytes and add 8 to the
     # key-bias form.
     ("sdpa", "sdpa_kernelILi1ELb0ELi16ELi64ELb0E"): 8,
-    # opt-in bf16x3 SDPA at 16 waves ([B,H,L,64] k/v): 8 waves spill nothing
-    # but run 6 % slower.  With a key bias the bias row is the accumulators'
-    # starting value (no registers of its own): 88 -> 52 bytes, and the
-    # one-term bf16 form 32 -> 0 (configs[2] bf16x3 3.43 -> 2.88 ms).
-    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb0ELi16ELi64ELi1ELi3E"): 8,
-    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3E"): 52,
+    # opt-in bf16x3 SDPA at 16 waves with a key bias, K/V staged in the
+    # kernel ([B,H,L,64] k/v, and key-contiguous k/v) and from the pre-split
+    # image: 8 waves spill nothing but run 6 % slower.  The bias row is the
+    # accumulators' starting value (no registers of its own).  Key-contiguous
+    # k/v at 8 waves: 3.46 ms at configs[1] against 2.86 at 16.
+    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3ELb0E"): 16,
+    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3ELb1E"): 8,
+    ("sdpa_bf16", "sdpa_bf16_kernelILi1ELb1ELi16ELi64ELi1ELi3ELb0E"): 32,
     # strict NF24 GEMM, 256x256 tile with K steps of 32 and the deferred last
     # slice (vector-load path; epilogues store, GELU, gated, QKV, add): values
     # live across the K loop are stored once before it and reloaded once
@@ -63,6 +65,8 @@ REQUIRED = [
     ("nf24_gemm_bf16", "Bf16CfgILi256ELi128ELi8ELi2ELi2EEELi3ELb1ELi3E"),  # bf16x3 gated, 8192 x 1024
     ("nf24_gemm_bf16", "Bf16CfgILi256ELi192ELi8ELi2ELi2EEELi3ELb1ELi0ELb1E"),  # bf16x3 from the weight planes
     ("nf24_gemm_bf16", "nf24_bf16_planes_kernelILi3E"),                       # the planes builder
+    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb0ELi16ELi64ELi1ELi3ELb1E"),  # bf16x3 configs[1], pre-split tiles
+    ("sdpa_bf16", "sdpa_bf16_presplit_kernelILi0ELi3E"),               # its pre-split pass
 ]
 
 

@@ -1,7 +1,8 @@
 """tsplat_sdpa_noalloc_async: the SDPA entry point that allocates nothing.
 
-It must give the same bytes as tsplat_sdpa_precision_async (same kernels,
-same launch plan; only where the key-split partials live differs), on two
+It must give the same bytes as tsplat_sdpa_precision_async (same launch
+plan and LDS tiles; the key-split partials live in the static array, and
+the precision entry may stage K/V in a pre-split pass), on two
 calls in a row with the second smaller (the static array keeps the first
 call's contents), in each precision and layout it shares with the existing
 entry, and it must work where the workspace path cannot: captured into a

@@ -394,14 +394,18 @@ int triposplat_sdpa_q8t512_profile_get(uint64_t* calls, uint64_t* allocate_ns, u
 
 int triposplat_sdpa_q8t512_workspace_stats(uint64_t* allocations, uint64_t* capacity_bytes) {
   if (!allocations || !capacity_bytes) return kErrNull;
-  uint64_t retired = 0;
+  uint64_t retired = 0, planes_allocations = 0, planes_bytes = 0;
   workspace_stats(kSlotSdpaPartial, allocations, capacity_bytes, &retired);
+  workspace_stats(kSlotSdpaPlanes, &planes_allocations, &planes_bytes, &retired);
+  *allocations += planes_allocations;
+  *capacity_bytes += planes_bytes;
   return kOk;
 }
 
 void triposplat_sdpa_q8t512_workspace_release(void) {
   const auto t0 = std::chrono::steady_clock::now();
   release_workspace(kSlotSdpaPartial);
+  release_workspace(kSlotSdpaPlanes);
   g_sdpa_free_ns.fetch_add((uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
                                std::chrono::steady_clock::now() - t0)
                                .count(),

@@ -30,6 +30,14 @@
 // K and V are converted (and split) once per tile on their way into LDS,
 // as bf16 rows of 72 (K: 64 dims + 8) or kBKV + 8 (V^T) elements: 8
 // consecutive rows read at one column fall in distinct 16-byte bank groups.
+//
+// Wide launches without a caller scratch first run sdpa_bf16_presplit_kernel,
+// which stages every 64-key tile of every (b, h) once, through the same
+// fetch / split / placement code, and writes the LDS rows out as bf16 planes;
+// the main kernel (kPre) then copies a tile's rows into LDS with 16-byte
+// loads and stores, instead of converting, splitting and transposing it in
+// each of the Lq / 512 query tiles that read it.  The LDS contents, and so
+// the results, are the same bit for bit.
 
 #include "sdpa_common.h"
 
@@ -83,28 +91,126 @@ __device__ __forceinline__ void split8(const floatx16& s, int c, bf16x8& hi, bf1
   if constexpr (kLo) lo = __builtin_bit_cast(bf16x8, uintx4{l[0], l[1], l[2], l[3]});
 }
 
+// LDS image of one K/V tile of kBKV == kD keys: bf16 planes of kPlaneElems
+// elements, 0 = K hi, 1 = V^T hi, 2 = K lo, 3 = V^T lo (bf16x3 only); K rows
+// (one key) and V^T rows (one dim) both of kRowElems = 72.
+constexpr int kTileKeys = 64;
+constexpr int kRowElems = kTileKeys + 8;
+constexpr int kPlaneElems = kTileKeys * kRowElems;
+static_assert(kTileKeys == kD, "K rows and V^T rows share one stride");
+
+// Fetches thread tid's kLoads float4 units of K and V for the tile at key0.
+// kLayout: 0 = k and v [B, H, Lk, 64]; 1 = both key-contiguous [B, H, 64, Lkp].
+template <int kLayout, int kThreads, int kLoads>
+__device__ __forceinline__ void fetch_kv(const SdpaArgs& a, const float* kbase, const float* vbase, int tid,
+                                         int key0, floatx4 (&kr)[kLoads], floatx4 (&vr)[kLoads]) {
+#pragma unroll
+  for (int j = 0; j < kLoads; ++j) {
+    const int idx = tid + j * kThreads;
+    if constexpr (kLayout == 0) {
+      fetch_units_kv<kTileKeys>(a, kbase, vbase, idx, key0, kr[j], vr[j]);
+    } else {
+      kr[j] = fetch_unit<true, kTileKeys>(a, kbase, idx, key0);
+      vr[j] = fetch_unit<true, kTileKeys>(a, vbase, idx, key0);
+    }
+  }
+}
+
+// Splits the fetched units and places them in the LDS planes at `planes`:
+// K as key rows, V transposed to dim rows with its keys at vt_pos.
+template <int kLayout, bool kLo, int kThreads, int kLoads>
+__device__ __forceinline__ void place_kv(int tid, const floatx4 (&kr)[kLoads], const floatx4 (&vr)[kLoads],
+                                         __bf16* planes) {
+  __bf16* khi = planes;
+  __bf16* vhi = planes + kPlaneElems;
+  __bf16* klo = planes + 2 * kPlaneElems;
+  __bf16* vlo = planes + 3 * kPlaneElems;
+#pragma unroll
+  for (int j = 0; j < kLoads; ++j) {
+    const int idx = tid + j * kThreads;
+    bf16x4 kh, kl, vh, vl;
+    split4<kLo>(kr[j], kh, kl);
+    split4<kLo>(vr[j], vh, vl);
+    if constexpr (kLayout == 0) {
+      // key row, dims 4c..4c+3: one 8-byte store per K plane, V transposed
+      // element by element
+      const int row = idx / (kD / 4), c = idx % (kD / 4);
+      *reinterpret_cast<bf16x4*>(&khi[row * kRowElems + 4 * c]) = kh;
+      if constexpr (kLo) *reinterpret_cast<bf16x4*>(&klo[row * kRowElems + 4 * c]) = kl;
+      const int p = vt_pos(row);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vhi[(4 * c + e) * kRowElems + p] = vh[e];
+        if constexpr (kLo) vlo[(4 * c + e) * kRowElems + p] = vl[e];
+      }
+    } else {
+      // dim row, keys 4c..4c+3: K transposed element by element, V one
+      // 8-byte store per plane (contiguous in V^T: vt_pos keeps bits 0-1)
+      const int row = idx / (kTileKeys / 4), c = idx % (kTileKeys / 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        khi[(4 * c + e) * kRowElems + row] = kh[e];
+        if constexpr (kLo) klo[(4 * c + e) * kRowElems + row] = kl[e];
+      }
+      *reinterpret_cast<bf16x4*>(&vhi[row * kRowElems + vt_pos(4 * c)]) = vh;
+      if constexpr (kLo) *reinterpret_cast<bf16x4*>(&vlo[row * kRowElems + vt_pos(4 * c)]) = vl;
+    }
+  }
+}
+
+// Global image of the staged tiles: [B * H][ceil(Lk / 64)][planes][64 rows]
+// [64] bf16, the LDS planes without their row padding.
+constexpr int kPreTileElems = kTileKeys * kTileKeys;  // per plane
+constexpr int kPreThreads = 256;
+
+template <int kLayout, int kTerms>
+__global__ __launch_bounds__(kPreThreads) void sdpa_bf16_presplit_kernel(SdpaArgs a, uintx4* out,
+                                                                         int ntiles) {
+  constexpr bool kLo = kTerms == 3;
+  constexpr int kPlanes = kLo ? 4 : 2;
+  constexpr int kLoads = kTileKeys * kD / 4 / kPreThreads;
+  constexpr int kUnits = kPlanes * kTileKeys * kTileKeys / 8;  // 16-byte units
+  __shared__ __attribute__((aligned(16))) __bf16 lds[kPlanes * kPlaneElems];
+  const int tid = threadIdx.x;
+  const int bh = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
+  const int64_t head = kLayout == 1 ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD;
+  floatx4 kr[kLoads], vr[kLoads];
+  fetch_kv<kLayout, kPreThreads, kLoads>(a, a.k + bh * head, a.v + bh * head, tid, tile * kTileKeys, kr, vr);
+  place_kv<kLayout, kLo, kPreThreads, kLoads>(tid, kr, vr, lds);
+  __syncthreads();
+  uintx4* dst = out + (int64_t)blockIdx.x * kUnits;
+#pragma unroll
+  for (int j = 0; j < kUnits / kPreThreads; ++j) {
+    const int u = tid + j * kPreThreads;
+    const int p = u / (kUnits / kPlanes), r = (u / 8) % kTileKeys, ch = u % 8;
+    dst[u] = *reinterpret_cast<const uintx4*>(&lds[p * kPlaneElems + r * kRowElems + 8 * ch]);
+  }
+}
+
 // kLayout: 0 = k and v [B, H, Lk, 64] (v is transposed on its way into
 // LDS); 1 = both key-contiguous [B, H, 64, Lkp] (k is transposed).  kWaves
 // waves of 32 queries share each K/V tile of kBKV keys; kGB 32-key blocks
 // per softmax step (1 keeps 16 score registers live).  kTerms: 1 (bf16) or
-// 3 (bf16x3).
-template <int kLayout, bool kBias, int kWaves, int kBKV, int kGB, int kTerms>
-__global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
+// 3 (bf16x3).  kPre: the tiles come from sdpa_bf16_presplit_kernel's image
+// `pre` (kLayout is then unused).
+template <int kLayout, bool kBias, int kWaves, int kBKV, int kGB, int kTerms, bool kPre>
+__global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a, const uintx4* pre) {
   constexpr int kThreads = kWaves * 64;
   constexpr int kBQ = kWaves * 32;
   constexpr int kNKB = kBKV / 32;
   constexpr bool kLo = kTerms == 3;
-  constexpr int kKS = kD + 8;    // bf16 per K row (one key)
-  constexpr int kVS = kBKV + 8;  // bf16 per V^T row (one dim)
+  constexpr int kPlanes = kLo ? 4 : 2;
+  constexpr int kKS = kRowElems;  // bf16 per K row (one key)
+  constexpr int kVS = kRowElems;  // bf16 per V^T row (one dim)
   constexpr int kUnits = kBKV * kD / 4;  // float4 of K (and of V) per tile
-  constexpr int kLoads = kUnits / kThreads;
-  static_assert(kLoads * kThreads == kUnits, "tile split");
+  constexpr int kLoads = kPre ? 1 : kUnits / kThreads;
+  constexpr int kPUnits = kPlanes * kBKV * kD / 8;  // 16-byte units of a pre-split tile
+  constexpr int kPLoads = kPre ? kPUnits / kThreads : 1;
+  static_assert(kBKV == kTileKeys, "tile image");
+  static_assert(kPre ? kPLoads * kThreads == kPUnits : kLoads * kThreads == kUnits, "tile split");
   static_assert(kThreads >= kBKV, "bias row load");
   static_assert(kNKB % kGB == 0, "softmax groups");
-  __shared__ __attribute__((aligned(16))) __bf16 khi[2][kBKV * kKS];
-  __shared__ __attribute__((aligned(16))) __bf16 klo[2][kLo ? kBKV * kKS : 8];
-  __shared__ __attribute__((aligned(16))) __bf16 vhi[2][kD * kVS];
-  __shared__ __attribute__((aligned(16))) __bf16 vlo[2][kLo ? kD * kVS : 8];
+  __shared__ __attribute__((aligned(16))) __bf16 kvl[2][kPlanes * kPlaneElems];
   __shared__ __attribute__((aligned(16))) float bbuf[2][kBKV];
 
   const int tid = threadIdx.x;
@@ -146,24 +252,22 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
       }
   }
 
-  constexpr bool kKP = kLayout == 1;  // k key-contiguous
-  constexpr bool kVP = kLayout != 0;  // v key-contiguous
-  const float* kbase = a.k + (int64_t)bh * (kKP ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
-  const float* vbase = a.v + (int64_t)bh * (kVP ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD);
+  const int64_t head = kLayout == 1 ? (int64_t)kD * a.Lkp : (int64_t)a.Lk * kD;
+  const float* kbase = a.k + (int64_t)bh * head;
+  const float* vbase = a.v + (int64_t)bh * head;
   const float* brow = kBias ? a.bias + (int64_t)h * a.bias_head_stride : nullptr;
+  const uintx4* pbase = kPre ? pre + (int64_t)bh * ((a.Lk + kBKV - 1) / kBKV) * kPUnits : nullptr;
 
   floatx4 kr[kLoads], vr[kLoads];
+  uintx4 pr[kPLoads];
   float br = 0.0f;
   auto load = [&](int key0) {
+    if constexpr (kPre) {
+      const uintx4* src = pbase + (int64_t)(key0 / kBKV) * kPUnits;
 #pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-      const int idx = tid + j * kThreads;
-      if constexpr (!kKP && !kVP) {
-        fetch_units_kv<kBKV>(a, kbase, vbase, idx, key0, kr[j], vr[j]);
-      } else {
-        kr[j] = fetch_unit<kKP, kBKV>(a, kbase, idx, key0);
-        vr[j] = fetch_unit<kVP, kBKV>(a, vbase, idx, key0);
-      }
+      for (int j = 0; j < kPLoads; ++j) pr[j] = src[tid + j * kThreads];
+    } else {
+      fetch_kv<kLayout, kThreads, kLoads>(a, kbase, vbase, tid, key0, kr, vr);
     }
     if (kBias && tid < kBKV) {
       const int key = key0 + tid;
@@ -171,37 +275,15 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
     }
   };
   auto store = [&](int buf) {
+    if constexpr (kPre) {
 #pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-      const int idx = tid + j * kThreads;
-      bf16x4 kh, kl, vh, vl;
-      split4<kLo>(kr[j], kh, kl);
-      split4<kLo>(vr[j], vh, vl);
-      if constexpr (!kKP) {  // key row, dims 4c..4c+3: one 8-byte store per plane
-        const int row = idx / (kD / 4), c = idx % (kD / 4);
-        *reinterpret_cast<bf16x4*>(&khi[buf][row * kKS + 4 * c]) = kh;
-        if constexpr (kLo) *reinterpret_cast<bf16x4*>(&klo[buf][row * kKS + 4 * c]) = kl;
-      } else {  // dim row, keys 4c..4c+3: transposed element by element
-        const int row = idx / (kBKV / 4), c = idx % (kBKV / 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          khi[buf][(4 * c + e) * kKS + row] = kh[e];
-          if constexpr (kLo) klo[buf][(4 * c + e) * kKS + row] = kl[e];
-        }
+      for (int j = 0; j < kPLoads; ++j) {
+        const int u = tid + j * kThreads;
+        const int p = u / (kPUnits / kPlanes), r = (u / 8) % kBKV, ch = u % 8;
+        *reinterpret_cast<uintx4*>(&kvl[buf][p * kPlaneElems + r * kRowElems + 8 * ch]) = pr[j];
       }
-      if constexpr (!kVP) {  // key row, dims 4c..4c+3: transposed element by element
-        const int row = idx / (kD / 4), c = idx % (kD / 4);
-        const int p = vt_pos(row);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          vhi[buf][(4 * c + e) * kVS + p] = vh[e];
-          if constexpr (kLo) vlo[buf][(4 * c + e) * kVS + p] = vl[e];
-        }
-      } else {  // dim row, keys 4c..4c+3 (contiguous in V^T: vt_pos keeps bits 0-1)
-        const int row = idx / (kBKV / 4), c = idx % (kBKV / 4);
-        *reinterpret_cast<bf16x4*>(&vhi[buf][row * kVS + vt_pos(4 * c)]) = vh;
-        if constexpr (kLo) *reinterpret_cast<bf16x4*>(&vlo[buf][row * kVS + vt_pos(4 * c)]) = vl;
-      }
+    } else {
+      place_kv<kLayout, kLo, kThreads, kLoads>(tid, kr, vr, kvl[buf]);
     }
     if (kBias && tid < kBKV) bbuf[buf][tid] = br;
   };
@@ -223,10 +305,10 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
     const int buf = t & 1;
     const int key0 = w.k_begin + t * kBKV;
     if (t + 1 < ntiles) load(key0 + kBKV);
-    const __bf16* kh_ = khi[buf];
-    const __bf16* kl_ = klo[buf];
-    const __bf16* vh_ = vhi[buf];
-    const __bf16* vl_ = vlo[buf];
+    const __bf16* kh_ = kvl[buf];
+    const __bf16* vh_ = kvl[buf] + kPlaneElems;
+    const __bf16* kl_ = kvl[buf] + 2 * kPlaneElems;
+    const __bf16* vl_ = kvl[buf] + 3 * kPlaneElems;
     const bool tail = key0 + kBKV > a.Lk;
 
     if (wave_live) {
@@ -328,24 +410,62 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a) {
   store_rows<kBQ>(a, o, m_run, l_run);
 }
 
-template <int kLayout, bool kBias, int kTerms, int kWaves>
-int launch_shape(const SdpaParams& p, hipStream_t stream, int cus) {
+template <int kLayout, bool kBias, int kTerms, int kWaves, bool kPre>
+int launch_shape(const SdpaParams& p, hipStream_t stream, int cus, const uintx4* pre) {
   return launch_tiles(make_args(p), p, kWaves * 32, 64, cus, stream, [&](dim3 grid, const SdpaArgs& a) {
-    hipLaunchKernelGGL((sdpa_bf16_kernel<kLayout, kBias, kWaves, 64, 1, kTerms>), grid, dim3(kWaves * 64), 0,
-                       stream, a);
+    hipLaunchKernelGGL((sdpa_bf16_kernel<kLayout, kBias, kWaves, 64, 1, kTerms, kPre>), grid,
+                       dim3(kWaves * 64), 0, stream, a, pre);
   });
 }
 
-// Small grids: 4 waves.  Wide grids: 16 waves, except bf16x3 with packed
-// k/v, which spills 148-160 bytes per lane at 16 waves (6.0 ms at
-// configs[1]) and none at 8 (3.5 ms).
+// Stages every K/V tile once into the stream's pre-split workspace.  Null
+// (and st untouched) when the workspace is not available -- allocation
+// failure, or a graph capture that would need it to grow -- so the caller
+// stages in the main kernel instead; st = kErrLaunch on a failed launch.
+template <int kLayout, int kTerms>
+const uintx4* presplit(const SdpaParams& p, hipStream_t stream, int& st) {
+  constexpr int kPlanes = kTerms == 3 ? 4 : 2;
+  const int64_t ntiles = (p.Lk + kTileKeys - 1) / kTileKeys;
+  const int64_t blocks = (int64_t)p.B * p.H * ntiles;
+  if (blocks <= 0 || blocks > 0x7fffffff) return nullptr;
+  const size_t bytes = (size_t)blocks * kPlanes * kPreTileElems * sizeof(__bf16);
+  auto* img = static_cast<uintx4*>(stream_workspace(stream, bytes, kSlotSdpaPlanes));
+  if (img == nullptr) return nullptr;
+  hipLaunchKernelGGL((sdpa_bf16_presplit_kernel<kLayout, kTerms>), dim3((unsigned)blocks), dim3(kPreThreads), 0,
+                     stream, make_args(p), img, (int)ntiles);
+  if (hipGetLastError() != hipSuccess) {
+    st = kErrLaunch;
+    return nullptr;
+  }
+  return img;
+}
+
+// Query tiles of 512 per head from which the pre-split pass is used: it
+// reads K / V once and writes their bf16 image once (46 us for 16 heads x
+// 16384 keys in bf16x3), and each query tile then saves the conversion and
+// transposition of every K/V tile.  Measured break-even: 8-12 tiles with
+// [Lk, 64] k/v (configs[1]: 2.81 -> 2.69 ms in bf16x3, 1.29 -> 1.24 ms in
+// bf16; 2 tiles: 1.43 -> 1.73 ms), 4-8 with key-contiguous k/v, whose
+// in-kernel staging transposes K element by element.
+template <int kLayout>
+constexpr int kPreMinQueryTiles = kLayout == 1 ? 6 : 12;
+
+// Small grids: 4 waves.  Wide grids: 16 waves, on the pre-split tiles when
+// the call may allocate (no caller scratch) and enough query tiles share
+// each K/V tile, else staging in the kernel.  Both wide forms run the same
+// tile plan, so they give the same bits.
 template <int kLayout, bool kBias, int kTerms>
 int launch_sized(const SdpaParams& p, hipStream_t stream) {
   const int cus = compute_units();
   const int64_t wide_tiles = (int64_t)p.B * p.H * ((p.Lq + 511) / 512);
-  if (wide_tiles < cus) return launch_shape<kLayout, kBias, kTerms, 4>(p, stream, 0);
-  constexpr int kWide = (kLayout == 1 && kTerms == 3) ? 8 : 16;
-  return launch_shape<kLayout, kBias, kTerms, kWide>(p, stream, cus);
+  if (wide_tiles < cus) return launch_shape<kLayout, kBias, kTerms, 4, false>(p, stream, 0, nullptr);
+  if (p.scratch == nullptr && (p.Lq + 511) / 512 >= kPreMinQueryTiles<kLayout>) {
+    int st = kOk;
+    const uintx4* img = presplit<kLayout, kTerms>(p, stream, st);
+    if (st != kOk) return st;
+    if (img != nullptr) return launch_shape<0, kBias, kTerms, 16, true>(p, stream, cus, img);
+  }
+  return launch_shape<kLayout, kBias, kTerms, 16, false>(p, stream, cus, nullptr);
 }
 
 template <int kLayout, bool kBias>

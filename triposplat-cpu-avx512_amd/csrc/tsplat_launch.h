@@ -213,7 +213,12 @@ int launch_nf24_decode(const int16_t* code01_t, const int8_t* q2_t, const float*
 // stream, slot); null on allocation failure, or when the stream is under
 // graph capture and its buffer is too small.  The policy (reuse, free after
 // the stream, retire a buffer a capture recorded) is in workspace_pool.h.
-enum WorkspaceSlot : int { kSlotGemvPartial = 0, kSlotSdpaPartial = 1, kSlotGemmTail = 2 };
+enum WorkspaceSlot : int {
+  kSlotGemvPartial = 0,
+  kSlotSdpaPartial = 1,
+  kSlotGemmTail = 2,
+  kSlotSdpaPlanes = 3,  // pre-split bf16 K/V tiles of the bf16 SDPA modes
+};
 void* stream_workspace(hipStream_t stream, size_t bytes, int slot);
 // Frees the slot's buffers of the current device that no capture recorded
 // (after their streams) and retires the others.

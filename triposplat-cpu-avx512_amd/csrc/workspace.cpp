@@ -1,7 +1,7 @@
 // Per-stream device workspaces for kernels that need scratch memory: the
-// split-K partial sums of the few-row GEMM and the key-split partials of the
-// SDPA tail.  Every user overwrites the part it reads, so buffers are not
-// cleared.  The grow / free / retire policy is WorkspacePool's
+// split-K partial sums of the few-row GEMM, the key-split partials of the
+// SDPA tail and the pre-split K/V tiles of the bf16 SDPA modes.  Every user
+// overwrites the part it reads, so buffers are not cleared.  The grow / free / retire policy is WorkspacePool's
 // (workspace_pool.h); this file supplies the HIP operations and a lock.
 
 #include <hip/hip_runtime.h>
@@ -41,7 +41,8 @@ struct HipOps {
 };
 
 using Pool = WorkspacePool<hipStream_t, HipOps>;
-static_assert(kSlotSdpaPartial < Pool::kSlots && kSlotGemmTail < Pool::kSlots,
+static_assert(kSlotSdpaPartial < Pool::kSlots && kSlotGemmTail < Pool::kSlots &&
+                  kSlotSdpaPlanes < Pool::kSlots,
               "workspace slot out of range");
 
 std::mutex g_mu;
