@@ -108,8 +108,9 @@ int triposplat_sdpa_f32_avx512_exact_q8t512_packed_blhd(
  * and query block report this library's tiles (64 keys, 128 queries).
  * Profile: calls and wall time of the blocking calls (allocate/pack/free
  * report 0: there is no per-call workspace or pack step).
- * Workspace: the SDPA's key-split partials live in grow-only device buffers,
- * one per (device, stream); stats report their allocations and bytes.
+ * Workspace: the SDPA's key-split partials, and the bf16 modes' pre-split
+ * K/V image, live in grow-only device buffers, one per (device, stream, use);
+ * stats report their allocations and bytes together.
  * Release frees, after its stream, the buffer of every stream on the current
  * device that is idle, and keeps (until the process ends) the buffers a HIP
  * graph captured, those of a stream under capture at that moment (waiting on
@@ -139,7 +140,11 @@ int tsplat_sdpa_async(const float* q, const float* k, const float* v,
  * 2 bf16x3 (three bf16 terms per product: hi*hi + hi*lo + lo*hi, 16
  * significant bits per operand); q' = q * 0.125 * log2(e) in fp32, p the
  * unnormalised exponentials; max, exp2, sums and normalisation in fp32.
- * Other values -> -2. */
+ * Other values -> -2.  Modes 1 and 2 on wide grids with at least 12 query
+ * tiles of 512 per head (6 with kv_packed) first stage K and V once into a
+ * bf16 image in the per-stream workspace (512 bytes per key and head in
+ * bf16x3, 256 in bf16); without the workspace (under graph capture with a
+ * too small buffer) they stage in the kernel, with the same result. */
 int tsplat_sdpa_precision_async(const float* q, const float* k, const float* v,
                                 const float* key_bias_or_null, float* out, int B, int H, int Lq,
                                 int Lk, int D, int has_key_bias, int key_bias_len,
@@ -149,7 +154,8 @@ int tsplat_sdpa_precision_async(const float* q, const float* k, const float* v,
 /* No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  tsplat_sdpa_precision_async, same arguments and
- * result, calling no hipMalloc / hipFree: the key-split partials of a
+ * result, calling no hipMalloc / hipFree (the bf16 modes stage K and V in
+ * the kernel, never in a pre-split image): the key-split partials of a
  * partial last round of query tiles go to a static 66 MiB device array
  * instead of the library's per-stream workspace.  That holds every launch
  * plan of a 256-CU device; a call that would need more returns -8 before any
