@@ -29,12 +29,12 @@ BUDGET = {
     # key-bias form.
     ("sdpa", "sdpa_kernelILi1ELb0ELi16ELi64ELb0E"): 8,
     # opt-in bf16x3 SDPA at 16 waves with a key bias, K/V staged in the
-    # kernel ([B,H,L,64] k/v, and key-contiguous k/v) and from the pre-split
-    # image: 8 waves spill nothing but run 6 % slower.  The bias row is the
-    # accumulators' starting value (no registers of its own).  Key-contiguous
-    # k/v at 8 waves: 3.46 ms at configs[1] against 2.86 at 16.
+    # kernel ([B,H,L,64] k/v, and key-contiguous k/v): 8 waves spill nothing
+    # but run 6 % slower.  The bias row is the accumulators' starting value
+    # (no registers of its own).  Key-contiguous k/v at 8 waves: 3.46 ms at
+    # configs[1] against 2.86 at 16.  Wide calls that may allocate read the
+    # pre-split image instead (no staging registers, no spill).
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3ELb0E"): 16,
-    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3ELb1E"): 8,
     ("sdpa_bf16", "sdpa_bf16_kernelILi1ELb1ELi16ELi64ELi1ELi3ELb0E"): 32,
     # strict NF24 GEMM, 256x256 tile with K steps of 32 and the deferred last
     # slice (vector-load path; epilogues store, GELU, gated, QKV, add): values
@@ -66,7 +66,8 @@ REQUIRED = [
     ("nf24_gemm_bf16", "Bf16CfgILi256ELi192ELi8ELi2ELi2EEELi3ELb1ELi0ELb1E"),  # bf16x3 from the weight planes
     ("nf24_gemm_bf16", "nf24_bf16_planes_kernelILi3E"),                       # the planes builder
     ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb0ELi16ELi64ELi1ELi3ELb1E"),  # bf16x3 configs[1], pre-split tiles
-    ("sdpa_bf16", "sdpa_bf16_presplit_kernelILi0ELi3E"),               # its pre-split pass
+    ("sdpa_bf16", "sdpa_bf16_kernelILi0ELb1ELi16ELi64ELi1ELi3ELb1E"),  # the same with a key bias
+    ("sdpa_bf16", "sdpa_bf16_presplit_kernelILi0ELi3ELb0E"),           # its pre-split pass
 ]
 
 

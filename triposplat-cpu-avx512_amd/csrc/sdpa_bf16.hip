@@ -33,11 +33,13 @@
 //
 // Wide launches without a caller scratch first run sdpa_bf16_presplit_kernel,
 // which stages every 64-key tile of every (b, h) once, through the same
-// fetch / split / placement code, and writes the LDS rows out as bf16 planes;
-// the main kernel (kPre) then copies a tile's rows into LDS with 16-byte
-// loads and stores, instead of converting, splitting and transposing it in
-// each of the Lq / 512 query tiles that read it.  The LDS contents, and so
-// the results, are the same bit for bit.
+// fetch / split / placement code, and writes the tile's LDS contents to
+// memory (its bf16 planes without the row padding, then the key-bias row in
+// log2 units); the main kernel (kPre) then copies the planes into LDS with
+// 16-byte loads and stores, and the bias row with one direct-to-LDS load,
+// instead of converting, splitting and transposing the tile in each of the
+// Lq / 512 query tiles that read it.  The LDS contents, and so the results,
+// are the same bit for bit.
 
 #include "sdpa_common.h"
 
@@ -51,6 +53,10 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ floatx16 mfma_bf16(const bf16x8& a, const bf16x8& b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
+
+// s_waitcnt operand: vector-memory count 0, export and LDS/scalar counts
+// left at their maxima (not waited on).
+constexpr int kWaitVmcnt0 = 0x0f70;
 
 // Position of tile key k in a V^T row: bits 2 and 3 swapped.
 __device__ __forceinline__ int vt_pos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
@@ -158,18 +164,20 @@ __device__ __forceinline__ void place_kv(int tid, const floatx4 (&kr)[kLoads], c
   }
 }
 
-// Global image of the staged tiles: [B * H][ceil(Lk / 64)][planes][64 rows]
-// [64] bf16, the LDS planes without their row padding.
-constexpr int kPreTileElems = kTileKeys * kTileKeys;  // per plane
+// Global image of the staged tiles: per (b*H + h, tile of 64 keys), the LDS
+// planes (kPlanes x 64 rows x 64 bf16, the rows without their padding), then
+// with a key bias the tile's 64 bias values in log2 units (zero past Lk).
+template <int kTerms, bool kBias>
+constexpr int kImageTileBytes = (kTerms == 3 ? 4 : 2) * kTileKeys * kTileKeys * 2 + (kBias ? kTileKeys * 4 : 0);
 constexpr int kPreThreads = 256;
 
-template <int kLayout, int kTerms>
+template <int kLayout, int kTerms, bool kBias>
 __global__ __launch_bounds__(kPreThreads) void sdpa_bf16_presplit_kernel(SdpaArgs a, uintx4* out,
                                                                          int ntiles) {
   constexpr bool kLo = kTerms == 3;
   constexpr int kPlanes = kLo ? 4 : 2;
   constexpr int kLoads = kTileKeys * kD / 4 / kPreThreads;
-  constexpr int kUnits = kPlanes * kTileKeys * kTileKeys / 8;  // 16-byte units
+  constexpr int kUnits = kPlanes * kTileKeys * kTileKeys / 8;  // 16-byte units of the planes
   __shared__ __attribute__((aligned(16))) __bf16 lds[kPlanes * kPlaneElems];
   const int tid = threadIdx.x;
   const int bh = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
@@ -178,12 +186,17 @@ __global__ __launch_bounds__(kPreThreads) void sdpa_bf16_presplit_kernel(SdpaArg
   fetch_kv<kLayout, kPreThreads, kLoads>(a, a.k + bh * head, a.v + bh * head, tid, tile * kTileKeys, kr, vr);
   place_kv<kLayout, kLo, kPreThreads, kLoads>(tid, kr, vr, lds);
   __syncthreads();
-  uintx4* dst = out + (int64_t)blockIdx.x * kUnits;
+  uintx4* dst = out + (int64_t)blockIdx.x * (kImageTileBytes<kTerms, kBias> / 16);
 #pragma unroll
   for (int j = 0; j < kUnits / kPreThreads; ++j) {
     const int u = tid + j * kPreThreads;
     const int p = u / (kUnits / kPlanes), r = (u / 8) % kTileKeys, ch = u % 8;
     dst[u] = *reinterpret_cast<const uintx4*>(&lds[p * kPlaneElems + r * kRowElems + 8 * ch]);
+  }
+  if (kBias && tid < kTileKeys) {
+    const int key = tile * kTileKeys + tid;
+    const float* brow = a.bias + (int64_t)(bh % a.H) * a.bias_head_stride;
+    reinterpret_cast<float*>(dst + kUnits)[tid] = key < a.Lk ? brow[key] * kLog2e : 0.0f;
   }
 }
 
@@ -204,7 +217,7 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a, cons
   constexpr int kVS = kRowElems;  // bf16 per V^T row (one dim)
   constexpr int kUnits = kBKV * kD / 4;  // float4 of K (and of V) per tile
   constexpr int kLoads = kPre ? 1 : kUnits / kThreads;
-  constexpr int kPUnits = kPlanes * kBKV * kD / 8;  // 16-byte units of a pre-split tile
+  constexpr int kPUnits = kPlanes * kBKV * kD / 8;  // 16-byte units of a tile's image planes
   constexpr int kPLoads = kPre ? kPUnits / kThreads : 1;
   static_assert(kBKV == kTileKeys, "tile image");
   static_assert(kPre ? kPLoads * kThreads == kPUnits : kLoads * kThreads == kUnits, "tile split");
@@ -256,22 +269,33 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a, cons
   const float* kbase = a.k + (int64_t)bh * head;
   const float* vbase = a.v + (int64_t)bh * head;
   const float* brow = kBias ? a.bias + (int64_t)h * a.bias_head_stride : nullptr;
-  const uintx4* pbase = kPre ? pre + (int64_t)bh * ((a.Lk + kBKV - 1) / kBKV) * kPUnits : nullptr;
+  constexpr int kTileBytes = kImageTileBytes<kTerms, kBias>;
+  const char* pbase =
+      kPre ? reinterpret_cast<const char*>(pre) + (int64_t)bh * ((a.Lk + kBKV - 1) / kBKV) * kTileBytes : nullptr;
 
   floatx4 kr[kLoads], vr[kLoads];
   uintx4 pr[kPLoads];
   float br = 0.0f;
-  auto load = [&](int key0) {
+  // load(key0, buf): kPre fetches thread tid's 16-byte units of the tile's
+  // image planes into registers, and the last wave copies the bias row
+  // straight into LDS buffer buf (direct-to-LDS, no register); otherwise
+  // the fp32 units and the bias value are fetched into registers.
+  // store(buf) places the units in LDS buffer buf (kPre: and waits for the
+  // bias copy), before the barrier that publishes it.
+  auto load = [&](int key0, int buf) {
     if constexpr (kPre) {
-      const uintx4* src = pbase + (int64_t)(key0 / kBKV) * kPUnits;
+      const char* src = pbase + (int64_t)(key0 / kBKV) * kTileBytes;
 #pragma unroll
-      for (int j = 0; j < kPLoads; ++j) pr[j] = src[tid + j * kThreads];
+      for (int j = 0; j < kPLoads; ++j) pr[j] = reinterpret_cast<const uintx4*>(src)[tid + j * kThreads];
+      if (kBias && __builtin_amdgcn_readfirstlane(wave) == kWaves - 1)
+        __builtin_amdgcn_global_load_lds(src + kPUnits * 16 + lane * 4,
+                                         (__attribute__((address_space(3))) void*)(&bbuf[buf][0]), 4, 0, 0);
     } else {
       fetch_kv<kLayout, kThreads, kLoads>(a, kbase, vbase, tid, key0, kr, vr);
-    }
-    if (kBias && tid < kBKV) {
-      const int key = key0 + tid;
-      br = key < a.Lk ? brow[key] * kLog2e : 0.0f;
+      if (kBias && tid < kBKV) {
+        const int key = key0 + tid;
+        br = key < a.Lk ? brow[key] * kLog2e : 0.0f;
+      }
     }
   };
   auto store = [&](int buf) {
@@ -282,10 +306,11 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a, cons
         const int p = u / (kPUnits / kPlanes), r = (u / 8) % kBKV, ch = u % 8;
         *reinterpret_cast<uintx4*>(&kvl[buf][p * kPlaneElems + r * kRowElems + 8 * ch]) = pr[j];
       }
+      if constexpr (kBias) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     } else {
       place_kv<kLayout, kLo, kThreads, kLoads>(tid, kr, vr, kvl[buf]);
+      if (kBias && tid < kBKV) bbuf[buf][tid] = br;
     }
-    if (kBias && tid < kBKV) bbuf[buf][tid] = br;
   };
 
   floatx16 o[2];
@@ -297,14 +322,14 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a, cons
   float l_run = 0.0f;
 
   const int ntiles = (w.k_end - w.k_begin + kBKV - 1) / kBKV;
-  load(w.k_begin);
+  load(w.k_begin, 0);
   store(0);
   __syncthreads();
 
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     const int key0 = w.k_begin + t * kBKV;
-    if (t + 1 < ntiles) load(key0 + kBKV);
+    if (t + 1 < ntiles) load(key0 + kBKV, buf ^ 1);
     const __bf16* kh_ = kvl[buf];
     const __bf16* vh_ = kvl[buf] + kPlaneElems;
     const __bf16* kl_ = kvl[buf] + 2 * kPlaneElems;
@@ -422,17 +447,16 @@ int launch_shape(const SdpaParams& p, hipStream_t stream, int cus, const uintx4*
 // (and st untouched) when the workspace is not available -- allocation
 // failure, or a graph capture that would need it to grow -- so the caller
 // stages in the main kernel instead; st = kErrLaunch on a failed launch.
-template <int kLayout, int kTerms>
+template <int kLayout, int kTerms, bool kBias>
 const uintx4* presplit(const SdpaParams& p, hipStream_t stream, int& st) {
-  constexpr int kPlanes = kTerms == 3 ? 4 : 2;
   const int64_t ntiles = (p.Lk + kTileKeys - 1) / kTileKeys;
   const int64_t blocks = (int64_t)p.B * p.H * ntiles;
   if (blocks <= 0 || blocks > 0x7fffffff) return nullptr;
-  const size_t bytes = (size_t)blocks * kPlanes * kPreTileElems * sizeof(__bf16);
+  const size_t bytes = (size_t)blocks * kImageTileBytes<kTerms, kBias>;
   auto* img = static_cast<uintx4*>(stream_workspace(stream, bytes, kSlotSdpaPlanes));
   if (img == nullptr) return nullptr;
-  hipLaunchKernelGGL((sdpa_bf16_presplit_kernel<kLayout, kTerms>), dim3((unsigned)blocks), dim3(kPreThreads), 0,
-                     stream, make_args(p), img, (int)ntiles);
+  hipLaunchKernelGGL((sdpa_bf16_presplit_kernel<kLayout, kTerms, kBias>), dim3((unsigned)blocks),
+                     dim3(kPreThreads), 0, stream, make_args(p), img, (int)ntiles);
   if (hipGetLastError() != hipSuccess) {
     st = kErrLaunch;
     return nullptr;
@@ -461,7 +485,7 @@ int launch_sized(const SdpaParams& p, hipStream_t stream) {
   if (wide_tiles < cus) return launch_shape<kLayout, kBias, kTerms, 4, false>(p, stream, 0, nullptr);
   if (p.scratch == nullptr && (p.Lq + 511) / 512 >= kPreMinQueryTiles<kLayout>) {
     int st = kOk;
-    const uintx4* img = presplit<kLayout, kTerms>(p, stream, st);
+    const uintx4* img = presplit<kLayout, kTerms, kBias>(p, stream, st);
     if (st != kOk) return st;
     if (img != nullptr) return launch_shape<0, kBias, kTerms, 16, true>(p, stream, cus, img);
   }
