@@ -143,8 +143,9 @@ int tsplat_sdpa_async(const float* q, const float* k, const float* v,
  * Other values -> -2.  Modes 1 and 2 on wide grids with at least 12 query
  * tiles of 512 per head (6 with kv_packed) first stage K and V once into a
  * bf16 image in the per-stream workspace (512 bytes per key and head in
- * bf16x3, 256 in bf16, +4 with a key bias); without the workspace (under graph capture with a
- * too small buffer) they stage in the kernel, with the same result. */
+ * bf16x3, 256 in bf16, +4 with a key bias; at most 2 GiB); without the
+ * workspace (under graph capture with a too small buffer) or above that
+ * size they stage in the kernel, with the same result. */
 int tsplat_sdpa_precision_async(const float* q, const float* k, const float* v,
                                 const float* key_bias_or_null, float* out, int B, int H, int Lq,
                                 int Lk, int D, int has_key_bias, int key_bias_len,

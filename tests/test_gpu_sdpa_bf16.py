@@ -350,3 +350,25 @@ def test_bf16_sdpa_presplit_capture_without_workspace(cuda, hiplib):
         assert torch.equal(out, want)
         assert _raw(hiplib, "tsplat_sdpa_precision_async", torch, cuda, k, q, v, None, other, 2, 0, L, 0) == 0
         torch.cuda.synchronize(cuda)
+
+
+def test_bf16_sdpa_presplit_image_cap(cuda, hiplib):
+    """A call whose pre-split image would exceed 2 GiB (1024 heads x 65 key
+    tiles x 32 KiB in bf16x3) stages in the kernel: the workspace does not
+    grow by the image, and the result equals the no-allocation entry's."""
+    import torch
+
+    B, H, Lq, Lk = 64, 16, 6144, 4160
+    g = torch.Generator(device=cuda).manual_seed(21)
+    q = torch.randn((B, H, Lq, 64), generator=g, device=cuda)
+    k = torch.randn((B, H, Lk, 64), generator=g, device=cuda)
+    v = torch.randn((B, H, Lk, 64), generator=g, device=cuda)
+    assert B * H * -(-Lk // 64) * 4 * 64 * 64 * 2 > 2 << 30
+    before = _workspace_bytes(hiplib)[1]
+    got, want = (torch.full((B, H, Lq, 64), float("nan"), device=cuda) for _ in range(2))
+    assert _raw(hiplib, "tsplat_sdpa_precision_async", torch, cuda, q, k, v, None, got, 2, 0, Lk, 0) == 0
+    assert _raw(hiplib, "tsplat_sdpa_noalloc_async", torch, cuda, q, k, v, None, want, 2, 0, Lk, 0) == 0
+    torch.cuda.synchronize(cuda)
+    assert _workspace_bytes(hiplib)[1] - before < 1 << 30
+    assert bool(torch.isfinite(got).all())
+    assert torch.equal(got, want)

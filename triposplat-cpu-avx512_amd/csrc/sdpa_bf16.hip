@@ -443,16 +443,23 @@ int launch_shape(const SdpaParams& p, hipStream_t stream, int cus, const uintx4*
   });
 }
 
+// Largest pre-split image (as large as the fp32 K and V it replaces, in
+// bf16x3) the library allocates for one call; larger calls stage in the
+// kernel rather than grow a stream's workspace further.
+constexpr size_t kPreMaxImageBytes = size_t(2) << 30;
+
 // Stages every K/V tile once into the stream's pre-split workspace.  Null
-// (and st untouched) when the workspace is not available -- allocation
-// failure, or a graph capture that would need it to grow -- so the caller
-// stages in the main kernel instead; st = kErrLaunch on a failed launch.
+// (and st untouched) when the image would exceed kPreMaxImageBytes or the
+// workspace is not available -- allocation failure, or a graph capture that
+// would need it to grow -- so the caller stages in the main kernel instead;
+// st = kErrLaunch on a failed launch.
 template <int kLayout, int kTerms, bool kBias>
 const uintx4* presplit(const SdpaParams& p, hipStream_t stream, int& st) {
   const int64_t ntiles = (p.Lk + kTileKeys - 1) / kTileKeys;
   const int64_t blocks = (int64_t)p.B * p.H * ntiles;
   if (blocks <= 0 || blocks > 0x7fffffff) return nullptr;
   const size_t bytes = (size_t)blocks * kImageTileBytes<kTerms, kBias>;
+  if (bytes > kPreMaxImageBytes) return nullptr;
   auto* img = static_cast<uintx4*>(stream_workspace(stream, bytes, kSlotSdpaPlanes));
   if (img == nullptr) return nullptr;
   hipLaunchKernelGGL((sdpa_bf16_presplit_kernel<kLayout, kTerms, kBias>), dim3((unsigned)blocks),
