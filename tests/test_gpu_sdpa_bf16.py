@@ -372,3 +372,52 @@ def test_bf16_sdpa_presplit_image_cap(cuda, hiplib):
     assert _workspace_bytes(hiplib)[1] - before < 1 << 30
     assert bool(torch.isfinite(got).all())
     assert torch.equal(got, want)
+
+
+def test_bf16_sdpa_presplit_captured_then_grown(cuda, hiplib):
+    """Captured on a stream whose pre-split workspace already holds the image
+    (an eager call first), the graph records the pre-split pass; a larger
+    eager call then grows the stream's buffer, and later replays (which keep
+    the buffer the capture recorded) still equal the eager result bit for
+    bit, with eager calls between them."""
+    import torch
+
+    H, L = 16, 8192   # 256 query tiles of 512: no key split
+    g = torch.Generator(device=cuda).manual_seed(12)
+
+    def inputs(Lk):
+        q = torch.nn.functional.normalize(torch.randn((1, H, L, 64), generator=g, device=cuda), dim=-1) * 8
+        k = torch.nn.functional.normalize(torch.randn((1, H, Lk, 64), generator=g, device=cuda), dim=-1) * 8
+        return q, k, torch.randn((1, H, Lk, 64), generator=g, device=cuda)
+
+    small, large = inputs(L), inputs(2 * L)
+    s = torch.cuda.Stream(device=cuda)
+    want = torch.empty((1, H, L, 64), device=cuda)
+    out = torch.empty_like(want)
+    other = torch.empty_like(want)
+    torch.cuda.synchronize(cuda)
+    with torch.cuda.stream(s):
+        assert _raw(hiplib, "tsplat_sdpa_precision_async", torch, cuda, *small, None, want, 2, 0, L, 0,
+                    stream=s.cuda_stream) == 0
+    torch.cuda.synchronize(cuda)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s, capture_error_mode="relaxed"):
+        assert _raw(hiplib, "tsplat_sdpa_precision_async", torch, cuda, *small, None, out, 2, 0, L, 0,
+                    stream=s.cuda_stream) == 0
+    torch.cuda.synchronize(cuda)
+    allocations = _workspace_bytes(hiplib)[0]
+    with torch.cuda.stream(s):
+        assert _raw(hiplib, "tsplat_sdpa_precision_async", torch, cuda, *large, None, other, 2, 0, 2 * L, 0,
+                    stream=s.cuda_stream) == 0
+    torch.cuda.synchronize(cuda)
+    assert _workspace_bytes(hiplib)[0] == allocations + 1   # the larger image grew s's buffer
+    for _ in range(3):
+        out.fill_(float("nan"))
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize(cuda)
+        assert torch.equal(out, want)
+        with torch.cuda.stream(s):
+            assert _raw(hiplib, "tsplat_sdpa_precision_async", torch, cuda, *large, None, other, 2, 0, 2 * L,
+                        0, stream=s.cuda_stream) == 0
+        torch.cuda.synchronize(cuda)
