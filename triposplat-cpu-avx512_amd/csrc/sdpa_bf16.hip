@@ -127,10 +127,11 @@ __device__ __forceinline__ void fetch_kv(const SdpaArgs& a, const float* kbase, 
 template <int kLayout, bool kLo, int kThreads, int kLoads>
 __device__ __forceinline__ void place_kv(int tid, const floatx4 (&kr)[kLoads], const floatx4 (&vr)[kLoads],
                                          __bf16* planes) {
+  // (without kLo the lo planes do not exist and are never stored to)
   __bf16* khi = planes;
   __bf16* vhi = planes + kPlaneElems;
-  __bf16* klo = planes + 2 * kPlaneElems;
-  __bf16* vlo = planes + 3 * kPlaneElems;
+  __bf16* klo = kLo ? planes + 2 * kPlaneElems : planes;
+  __bf16* vlo = kLo ? planes + 3 * kPlaneElems : planes;
 #pragma unroll
   for (int j = 0; j < kLoads; ++j) {
     const int idx = tid + j * kThreads;
@@ -332,8 +333,8 @@ __global__ __launch_bounds__(kWaves * 64) void sdpa_bf16_kernel(SdpaArgs a, cons
     if (t + 1 < ntiles) load(key0 + kBKV, buf ^ 1);
     const __bf16* kh_ = kvl[buf];
     const __bf16* vh_ = kvl[buf] + kPlaneElems;
-    const __bf16* kl_ = kvl[buf] + 2 * kPlaneElems;
-    const __bf16* vl_ = kvl[buf] + 3 * kPlaneElems;
+    const __bf16* kl_ = kLo ? kvl[buf] + 2 * kPlaneElems : kh_;
+    const __bf16* vl_ = kLo ? kvl[buf] + 3 * kPlaneElems : vh_;
     const bool tail = key0 + kBKV > a.Lk;
 
     if (wave_live) {
