@@ -421,3 +421,28 @@ def test_bf16_sdpa_presplit_captured_then_grown(cuda, hiplib):
             assert _raw(hiplib, "tsplat_sdpa_precision_async", torch, cuda, *large, None, other, 2, 0, 2 * L,
                         0, stream=s.cuda_stream) == 0
         torch.cuda.synchronize(cuda)
+
+
+def _presplit_sweep(seed, n):
+    """Seeded wide-grid calls that take the pre-split pass: 12+ query tiles
+    of 512 per head ([Lk, 64] k/v) or 6+ (packed), B*H*tiles >= 256, ragged
+    Lq and Lk, no / shared / per-head bias, BHLD or BLHD output."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        packed = bool(r.random() < 0.4)
+        tiles = int(r.integers(6 if packed else 12, 18))
+        Lq = (tiles - 1) * 512 + int(r.integers(1, 513))
+        H = int(r.integers(1, 17))
+        B = max(1, -(-256 // (H * tiles)) + int(r.integers(0, 2)))
+        if B * H * tiles > 600:
+            continue
+        out.append((B, H, Lq, int(r.integers(1, 3000)), [None, "shared", "per_head"][r.integers(0, 3)], packed,
+                    bool(r.random() < 0.5)))
+    return out
+
+
+@pytest.mark.parametrize("precision", [1, 2])
+@pytest.mark.parametrize("B,H,Lq,Lk,bias,packed,blhd", _presplit_sweep(4242, 8))
+def test_bf16_sdpa_presplit_random_sweep(cuda, hiplib, precision, B, H, Lq, Lk, bias, packed, blhd):
+    test_bf16_sdpa_presplit_matches_direct(cuda, hiplib, precision, B, H, Lq, Lk, bias, packed, blhd)
