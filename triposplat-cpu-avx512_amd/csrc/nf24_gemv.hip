@@ -567,8 +567,19 @@ int launch_mfma_form(const GemmParams& p, int splits, hipStream_t stream) {
         stream_workspace(stream, (size_t)splits * p.M * p.n_count * 4, kSlotGemvPartial));
     if (a.partial == nullptr) return kErrWorkspace;
   }
-  hipLaunchKernelGGL((nf24_gemv_mfma_kernel<kCols, kMfmaWaves, 4>),
-                     dim3((unsigned)(p.n_count / kCols * splits)), dim3(kMfmaWaves * 64), 0, stream, a);
+  // Chunks in flight per wave: 4, or as many as a wave owns when that is
+  // fewer (a K split can leave a wave one 32-row chunk: the out-projection's
+  // 6-row tail at K = 1024, whose chunks 2-4 were loaded, decoded and
+  // multiplied by x = 0; 12294 x 1024 x 1024 212.0 -> 208.7 us, the same
+  // bits).
+  const int chunks = per_wave / kMfmaRows;
+  const dim3 grid((unsigned)(p.n_count / kCols * splits)), block(kMfmaWaves * 64);
+  if (chunks >= 4)
+    hipLaunchKernelGGL((nf24_gemv_mfma_kernel<kCols, kMfmaWaves, 4>), grid, block, 0, stream, a);
+  else if (chunks >= 2)
+    hipLaunchKernelGGL((nf24_gemv_mfma_kernel<kCols, kMfmaWaves, 2>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((nf24_gemv_mfma_kernel<kCols, kMfmaWaves, 1>), grid, block, 0, stream, a);
   if (hipGetLastError() != hipSuccess) return kErrLaunch;
   if (splits == 1) return kOk;
   return launch_merge(a.partial, p.bias, p.out, p.M, p.n_count, p.n_start, p.stride_out, splits, stream);
