@@ -534,7 +534,7 @@ int launch_mt(GemvArgs a, int cgroups, int splits, hipStream_t stream) {
 // the partial sums (splits * M * count * 8 bytes) stay under half the weight
 // bytes; a split costs a second, small kernel.
 namespace {
-// The MFMA form, 8 waves, all loads of 4 chunks in flight, slabs of 32
+// The MFMA form, 8 waves, all loads of up to 4 chunks in flight, slabs of 32
 // columns when that gives at least 192 workgroups, else of 16 (N = 3072:
 // 192 slabs of 16).  Measured against the K-split wide kernel (cold weights,
 // HIP-graph replay, per call; M = 16 / 8 / 4): N = 3072, K = 1024: 8.4 /
